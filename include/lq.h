@@ -1,0 +1,109 @@
+/* liblq -- C ABI of the MI355X (gfx950) INT8 recurrent-state decode path for Gated DeltaNet (GDN) and
+ * Kimi Delta Attention (KDA).
+ *
+ * Every entry point takes plain device pointers, sizes and a hipStream_t (passed as void*), launches its HIP kernels on
+ * that stream, allocates nothing, never synchronises, and returns 0 on success or a negative lq_status.  All tensors
+ * are owned by the caller (torch in leapquant_amd.state).
+ *
+ * State-cache layout (the drop-in contract, /root/reference/leapquant/state.py:1-6,29-40):
+ *   ssm  fp32 [NS][HV][V][K], slot stride SS floats, inner dims packed.  Inside each (slot, head) block of V*K*4 bytes:
+ *        Sq int8 [V][K] at byte 0 | Sk f32 [K] at V*K | Sv f32 [V] at V*K+4K | UQ fp16 [R][K+V] at V*K+4K+4V
+ *        (UQ[r][0:K] = U^T[r], UQ[r][K:K+V] = Q^T[r]).  The remaining bytes of the block are not touched.
+ *   Window buffer (separate tensors, state.py:61-69; one deliberate change: keys are stored once per KEY head):
+ *        Kbuf bf16 [NS][H][L][K]   buffered normalised keys (identical for the HV/H value heads sharing a key head)
+ *        Ubuf bf16 [NS][HV][L][V]  buffered delta-rule values u_j
+ *        Wbuf f32  [NS][HV][L]     entry weights w_j (GDN: gate products since the entry; KDA: 1)
+ *        Pbuf f32  [NS][HV][KA]    GDN (KA = 1): decay of the checkpoint, init 1;  KDA (KA = K): cumulative log-gate, init 0
+ *        Gbuf fp16 [NS][HV][L][K]  KDA only: per-entry step decay exp(g_j), init 1
+ *        hcnt i32  [NS][HV]        valid entries in the window
+ *   A row n of a call with idx[n] <= 0 is a padding row: its outputs are zero and no state is written.
+ */
+#ifndef LQ_H
+#define LQ_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_ABI_VERSION 1
+
+enum lq_status {
+  LQ_OK = 0,
+  LQ_ERR_ARG = -1,     /* a size, shape or pointer the kernels do not support */
+  LQ_ERR_HIP = -2,     /* a HIP launch error (hipGetLastError after the launch) */
+};
+
+/* Pointers and sizes of one layer's state: the fp32 cache the checkpoint aliases and the window buffer. */
+typedef struct lq_state {
+  void* ssm;              /* fp32 [NS][HV][V][K] at slot 0 (the tensor's data pointer, storage offset included) */
+  long long slot_stride;  /* SS: floats between consecutive slots (>= HV*V*K) */
+  void* Kbuf;             /* bf16 [NS][H][L][K] */
+  void* Ubuf;             /* bf16 [NS][HV][L][V] */
+  float* Wbuf;            /* [NS][HV][L] */
+  float* Pbuf;            /* [NS][HV][KA] */
+  void* Gbuf;             /* fp16 [NS][HV][L][K] (KDA) or NULL (GDN) */
+  int* hcnt;              /* [NS][HV] */
+  int NS, HV, H, K, V, L, R;
+} lq_state;
+
+/* Decode inputs of one call: N rows, one token each. */
+typedef struct lq_step_io {
+  const void* mixed;      /* bf16 [N][2*H*K + HV*V]: q (key heads) | k (key heads) | v (value heads), after the conv */
+  const void* a;          /* bf16 raw gate: GDN [N][HV]; KDA [N][HV][K] */
+  const void* b;          /* bf16 [N][HV]: beta = sigmoid(b) */
+  const float* A_log;     /* [HV] */
+  const float* dt_bias;   /* GDN [HV]; KDA [HV][K] */
+  const int* idx;         /* [N] state slot of each row; <= 0: padding row */
+  void* out;              /* bf16 [N][HV][V] */
+  int N;
+  float scale;            /* query scale (K^-1/2 by default) */
+} lq_step_io;
+
+int lq_abi_version(void);
+
+/* GDN decode step: one token per row; appends (k, u, w = 1) to the window and updates the gate products.
+ * Replaces make_gdn_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o)
+ * (/root/reference/leapquant/kernels.py:27-692, launched at state.py:112-113).  Requires K = V = 128, 1 <= L <= 64,
+ * 1 <= R <= 4, HV % H == 0 and HV / H in {1, 2, 4}.  A head whose window is already full (hcnt >= L) is left
+ * untouched and its output row is zero (the flush after every step keeps hcnt < L on entry). */
+int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream);
+
+/* KDA decode step (per-key-channel gate).  glb != 0: GLM's bounded gate glb * sigmoid(exp(A_log) (a + dt_bias));
+ * glb == 0: Kimi's -exp(A_log) softplus(a + dt_bias).
+ * Replaces make_kda_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ,
+ * idx, o) (kernels.py:694-1075, launched at state.py:108-109).  Same shape limits as lq_gdn_step. */
+int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream);
+
+/* End-of-window flush of every (idx[n] > 0, hv) head whose window is full (hcnt == L): rebuild, one subspace
+ * iteration from Q0 [V][R] with CholeskyQR2, fp16 factors, smoothed residual requantised to codes in [-qmax, qmax]
+ * (127: INT8; 31: 6-bit in the same int8 container), window reset.  Due heads are found on the device.
+ * Replaces make_flush(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx)
+ * (kernels.py:1077-2033, launched at state.py:115-116).  Requires K = V = 128, 1 <= L <= 64, R == 4. */
+int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream);
+
+/* Standalone quantize of the fp32 states of the slots idx[n] > 0 (read from the same ssm blocks the checkpoint then
+ * overwrites), window reset (Wbuf = 0, Pbuf = 1, hcnt = 0).  qmax 127 (INT8) or 31 (6-bit).
+ * Replaces make_quantize(...)(S0, Sq, Sk, Sv, UQ, Wbuf, Pbuf, hcnt, Q0, idx) (kernels.py:2126-2242, state.py:163-165).
+ * Requires K = V = 128, 1 <= R <= 4. */
+int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream);
+
+/* Prefill dequant (GDN): fp32 S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T written over the ssm blocks of the
+ * slots idx[n] > 0, then window reset.  Replaces make_dequant(...)(S0, Sq, Sk, Sv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt,
+ * UQ, idx) (kernels.py:2041-2123, state.py:152-154).  Requires K = V = 128, 1 <= L <= 64, 1 <= R <= 4. */
+int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream);
+
+/* Rank-R subspace iteration on n fp32 matrices x [n][K][V]: `iters` rounds of P = MGS(x Q), Q = MGS(x^T P) from
+ * Q0 [V][R]; U = x Q.  Outputs U [n][K][R], Q [n][V][R] (fp32).
+ * Replaces make_lowrank / lowrank_factor (kernels.py:2246-2331).  Requires K = V = 128, 1 <= R <= 4. */
+int lq_lowrank(const float* x, const float* Q0, float* U, float* Q, int n, int K, int V, int R, int iters,
+               void* stream);
+
+/* Baseline for the measurements (no reference counterpart): the same GDN decode step on a dense state S
+ * [NS][HV][V][K] stored as bf16 (state_dtype 0) or fp32 (state_dtype 1), updated in place:
+ * S' = alpha S + u k^T, u = beta (v - alpha S k), o = S' q. */
+int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, int K, int V, const lq_step_io* io, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LQ_H */

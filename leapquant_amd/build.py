@@ -1,0 +1,55 @@
+"""Builds liblq.so (the HIP kernels + C ABI of include/lq.h) in-tree for gfx950.
+
+    python -m leapquant_amd.build          # -> leapquant_amd/_build/liblq.so
+
+hipcc cross-compiles without a GPU.  Every HIP file gets `-Xclang -target-feature -Xclang -packed-fp32-ops` (no
+packed FP32 instructions in the device code).
+"""
+import os
+import subprocess
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+CSRC = os.path.join(HERE, "csrc")
+OUT = os.path.join(HERE, "_build")
+LIB = os.path.join(OUT, "liblq.so")
+SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dense.hip")
+ARCH = os.environ.get("LQ_OFFLOAD_ARCH", "gfx950")
+
+
+def hipcc():
+    for p in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", "hipcc"):
+        if p and (os.path.sep not in p or os.path.exists(p)):
+            return p
+    raise RuntimeError("hipcc not found")
+
+
+def build(verbose=False):
+    os.makedirs(OUT, exist_ok=True)
+    cc = hipcc()
+    flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    objs = []
+    for s in SOURCES:
+        src = os.path.join(CSRC, s)
+        obj = os.path.join(OUT, s.replace(".hip", ".o"))
+        cmd = [cc] + flags + ["-c", src, "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError("hipcc failed on %s:\n%s" % (s, r.stderr))
+        if verbose:
+            err = "\n".join(x for x in r.stderr.splitlines() if "packed-fp32-ops" not in x)
+            if err.strip():
+                print(err)
+        objs.append(obj)
+    tmp = LIB + ".tmp"
+    cmd = [cc, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", tmp] + objs
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n%s" % r.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

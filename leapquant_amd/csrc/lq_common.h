@@ -1,0 +1,105 @@
+// Shared device helpers of liblq (gfx950, wave64).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/lq.h"
+
+#define LQ_QMAX 127.0f
+#define LQ_EPS 1e-12f              // kernels.py:23
+#define LQ_SOFTPLUS_THRESHOLD 20.0 // kernels.py:21
+#define LQ_PNMIN 1e-20f            // kernels.py:1078
+#define LQ_NORM_EPS 1e-6           // kernels.py:246-247
+
+typedef uint16_t bf16_t;   // bfloat16 bits
+typedef uint16_t f16_t;    // IEEE half bits
+
+// ---- scalar conversions ----------------------------------------------------------------------------------------
+__device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+// fp32 -> bf16, round to nearest even (NaN kept quiet)
+__device__ __forceinline__ bf16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (bf16_t)(u >> 16);
+}
+__device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
+
+__device__ __forceinline__ float h2f(f16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+__device__ __forceinline__ f16_t f2h(float f) { return __builtin_bit_cast(f16_t, (_Float16)f); }
+__device__ __forceinline__ float hround(float f) { return (float)(_Float16)f; }
+
+// ---- wave64 lane exchange (DPP: fused into the consuming VALU op, no LDS traffic) -------------------------------
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+#define DPP_XOR1 0xb1          // quad_perm [1,0,3,2]
+#define DPP_XOR2 0x4e          // quad_perm [2,3,0,1]
+#define DPP_HALF_MIRROR 0x141  // lane i <- lane 7-i within each 8-lane half row
+#define DPP_MIRROR 0x140       // lane i <- lane 15-i within each 16-lane row
+
+// all-reduce over the 8 lanes 8m..8m+7
+__device__ __forceinline__ float sum8(float x) {
+  x += dpp<DPP_XOR1>(x);
+  x += dpp<DPP_XOR2>(x);
+  x += dpp<DPP_HALF_MIRROR>(x);
+  return x;
+}
+__device__ __forceinline__ float max8(float x) {
+  x = fmaxf(x, dpp<DPP_XOR1>(x));
+  x = fmaxf(x, dpp<DPP_XOR2>(x));
+  x = fmaxf(x, dpp<DPP_HALF_MIRROR>(x));
+  return x;
+}
+// all-reduce over the 16 lanes of a DPP row
+__device__ __forceinline__ float sum16(float x) {
+  x = sum8(x);
+  x += dpp<DPP_MIRROR>(x);
+  return x;
+}
+__device__ __forceinline__ float max16(float x) {
+  x = max8(x);
+  x = fmaxf(x, dpp<DPP_MIRROR>(x));
+  return x;
+}
+// all-reduce over the wave
+__device__ __forceinline__ float sum64(float x) {
+  x = sum16(x);
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+__device__ __forceinline__ float max64(float x) {
+  x = max16(x);
+  x = fmaxf(x, __shfl_xor(x, 16));
+  x = fmaxf(x, __shfl_xor(x, 32));
+  return x;
+}
+
+// ---- gates (scalar, per (row, head) or per channel); evaluated in fp64 and rounded once ----------------------------
+__device__ __forceinline__ double softplus20(double x) {
+  return x <= LQ_SOFTPLUS_THRESHOLD ? log1p(exp(x)) : x;
+}
+// GDN decay alpha = exp(-exp(A_log) softplus(a + dt_bias))  (kernels.py:141-143)
+__device__ __forceinline__ float gdn_alpha(float a, float dtb, float alog) {
+  double xg = (double)(a + dtb);
+  return (float)exp(-exp((double)alog) * softplus20(xg));
+}
+// beta = f32(bf16(sigmoid(f32(b))))  (kernels.py:144)
+__device__ __forceinline__ float beta_of(float b) {
+  return bfround((float)(1.0 / (1.0 + exp(-(double)b))));
+}
+__device__ __forceinline__ float rsqrt_rn(double x) { return (float)(1.0 / sqrt(x)); }
+
+// ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------
+struct Block {
+  const int8_t* Sq;   // [V][K]
+  float* Sk;          // [K]
+  float* Sv;          // [V]
+  f16_t* UQ;          // [R][K+V]
+};
+__device__ __forceinline__ char* block_base(const lq_state& st, int slot, int hv) {
+  return (char*)st.ssm + 4ll * ((long long)slot * st.slot_stride + (long long)hv * st.V * st.K);
+}

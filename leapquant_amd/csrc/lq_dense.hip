@@ -1,0 +1,128 @@
+// Dense-state GDN decode step (bf16 or fp32 state): the baseline the INT8 step is measured against.
+// S' = alpha S + u k^T, u = beta (v - alpha S k), o = S' q with the same gate, beta and norms as the INT8 step.
+// One workgroup per (row, key head), 128 threads per value head; each 8-lane group owns 8 rows, each lane 16 columns.
+#include "lq_common.h"
+
+namespace {
+
+constexpr int KD = 128, VD = 128;
+
+template <int G, bool F32>
+__global__ __launch_bounds__(128 * G) void dense_step_kernel(void* S, int NS, int HV, int H, lq_step_io io) {
+  const int n = blockIdx.x / H, hk = blockIdx.x - n * H;
+  const int tid = threadIdx.x, g = tid >> 7, lt = tid & 127, rg = lt >> 3, cc = lt & 7;
+  const int hv = hk * G + g;
+  const long long MIX = 2ll * H * KD + (long long)HV * VD;
+  bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
+  const int slot = io.idx[n];
+  if (slot <= 0) { out[lt] = 0; return; }
+  const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
+  float qv[16], kv[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    qv[i] = bf2f(mrow[hk * KD + 16 * cc + i]);
+    kv[i] = bf2f(mrow[H * KD + hk * KD + 16 * cc + i]);
+  }
+  const float alpha = gdn_alpha(bf2f(((const bf16_t*)io.a)[(long long)n * HV + hv]), io.dt_bias[hv], io.A_log[hv]);
+  const float beta = beta_of(bf2f(((const bf16_t*)io.b)[(long long)n * HV + hv]));
+  float nq = 0.f, nk = 0.f, nkq = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    nq = fmaf(qv[i], qv[i], nq);
+    nk = fmaf(kv[i], kv[i], nk);
+    nkq = fmaf(kv[i], qv[i], nkq);
+  }
+  nq = sum8(nq); nk = sum8(nk); nkq = sum8(nkq);
+  const float inq = rsqrt_rn((double)nq + LQ_NORM_EPS) * io.scale;
+  const float ink = rsqrt_rn((double)nk + LQ_NORM_EPS);
+  const float kappa = nkq * inq * ink;
+  float kn[16], qn[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) { kn[i] = kv[i] * ink; qn[i] = qv[i] * inq; }
+  const long long head = ((long long)slot * HV + hv) * VD * KD;
+  constexpr int RB = F32 ? 4 : 8;          // rows per batch held in registers
+  float yk = 0.f;
+  for (int b0 = 0; b0 < 8; b0 += RB) {
+    float s[RB][16];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const long long off = head + (long long)(8 * rg + b0 + r) * KD + 16 * cc;
+      if (F32) {
+        const float4* p = (const float4*)((const float*)S + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float4 x = p[e];
+          s[r][4 * e] = x.x; s[r][4 * e + 1] = x.y; s[r][4 * e + 2] = x.z; s[r][4 * e + 3] = x.w;
+        }
+      } else {
+        const uint4* p = (const uint4*)((const bf16_t*)S + off);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const uint4 x = p[e];
+          const uint32_t u[4] = {x.x, x.y, x.z, x.w};
+#pragma unroll
+          for (int z = 0; z < 4; ++z) {
+            s[r][8 * e + 2 * z] = __uint_as_float(u[z] << 16);
+            s[r][8 * e + 2 * z + 1] = __uint_as_float(u[z] & 0xffff0000u);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+      const int v = 8 * rg + b0 + r;
+      float m = 0.f, y = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) { m = fmaf(s[r][i], kn[i], m); y = fmaf(s[r][i], qn[i], y); }
+      m = sum8(m); y = sum8(y);
+      const float vin = bf2f(mrow[2ll * H * KD + hv * VD + v]);
+      const float u = beta * (vin - alpha * m);
+      const float o = alpha * y + kappa * u;
+      if (cc == b0 + r) yk = o;           // lane cc keeps row 8 rg + cc
+      const long long off = head + (long long)v * KD + 16 * cc;
+      if (F32) {
+        float4* p = (float4*)((float*)S + off);
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          p[e] = make_float4(fmaf(u, kn[4 * e], alpha * s[r][4 * e]), fmaf(u, kn[4 * e + 1], alpha * s[r][4 * e + 1]),
+                             fmaf(u, kn[4 * e + 2], alpha * s[r][4 * e + 2]), fmaf(u, kn[4 * e + 3], alpha * s[r][4 * e + 3]));
+      } else {
+        uint4* p = (uint4*)((bf16_t*)S + off);
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          uint32_t w[4];
+#pragma unroll
+          for (int z = 0; z < 4; ++z) {
+            const int c = 8 * e + 2 * z;
+            w[z] = (uint32_t)f2bf(fmaf(u, kn[c], alpha * s[r][c])) |
+                   ((uint32_t)f2bf(fmaf(u, kn[c + 1], alpha * s[r][c + 1])) << 16);
+          }
+          p[e] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+      }
+    }
+  }
+  out[8 * rg + cc] = f2bf(yk);
+}
+
+}  // namespace
+
+extern "C" int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, int K, int V, const lq_step_io* io,
+                             void* stream) {
+  if (!S || !io || K != KD || V != VD || H <= 0 || HV <= 0 || HV % H != 0 || NS <= 0 || io->N < 0) return LQ_ERR_ARG;
+  if (state_dtype != 0 && state_dtype != 1) return LQ_ERR_ARG;
+  if (io->N == 0) return LQ_OK;
+  const int G = HV / H;
+  dim3 grid((unsigned)(io->N * H));
+  hipStream_t s = (hipStream_t)stream;
+#define LQ_DENSE(GG, FF) dense_step_kernel<GG, FF><<<grid, 128 * GG, 0, s>>>(S, NS, HV, H, *io)
+  if (state_dtype == 0) {
+    if (G == 1) LQ_DENSE(1, false); else if (G == 2) LQ_DENSE(2, false); else if (G == 4) LQ_DENSE(4, false);
+    else return LQ_ERR_ARG;
+  } else {
+    if (G == 1) LQ_DENSE(1, true); else if (G == 2) LQ_DENSE(2, true); else if (G == 4) LQ_DENSE(4, true);
+    else return LQ_ERR_ARG;
+  }
+#undef LQ_DENSE
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}

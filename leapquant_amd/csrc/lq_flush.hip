@@ -1,0 +1,815 @@
+// End-of-window flush, standalone quantize, prefill dequant and low-rank factoriser (gfx950).
+//
+// Semantics: /root/reference/leapquant/kernels.py:1077-2033 (flush), 2126-2242 (quantize), 2041-2123 (dequant),
+// 2246-2331 (lowrank).  Layout of the checkpoint and window buffer: include/lq.h.
+//
+// One workgroup of 256 threads (4 waves) per (slot, value head).  The head's 128 x 128 matrix lives in registers in the
+// accumulator layout of v_mfma_f32_16x16x32_bf16: wave w owns key channels c in [32w, 32w + 32), lane l holds
+//     acc[mt][nt][i] = M[c][v],   c = 32 w + 16 mt + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
+// The window rebuild (a rank-L GEMM, ~29 flop/byte at L = 64) runs on MFMA with bf16 hi/lo operands exactly where the
+// reference splits; the rank-R subspace products, CholeskyQR2, residual, smoothing and requantisation are VALU work on
+// that layout with DPP / LDS reductions.  Due heads are found on the device (hcnt == L), so the fixed grid is
+// graph-capture safe.
+#include "lq_common.h"
+
+namespace {
+
+constexpr int KD = 128, VD = 128;
+constexpr int LPMAX = 64;            // largest window
+constexpr int OPS = LPMAX + 8;       // operand row stride (bf16): 144 B rows
+constexpr int FT = 256;              // threads per workgroup
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+struct Tile {
+  f32x4 a[2][8];
+};
+
+struct FlushShared {
+  bf16_t op[3][KD][OPS];       // rebuild operands [c or v][j]
+  float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
+  float svr[VD];               // row factor of the dequant (Sv pn / qmax, KDA: Sv / qmax)
+  float pc[KD];                // KDA: exp(Pbuf)
+  float w[LPMAX];
+  float uo[4][KD];             // old U^T (KDA: fp16(U^T pc)), rows >= R zero
+  float qo[4][VD];             // old Q^T, rows >= R zero
+  f32x4 qv[VD];                // current Q operand [v][r] (fp16-rounded Q0, then Q16); fp32 Q before CholeskyQR
+  f32x4 pp[KD];                // P16, then U16 [c][r]
+  f32x4 qpart[4][VD];          // per-wave partials of the row reductions
+  float rowmax[4][VD];
+};
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+// out[k][r] = sum_v M[c_k][v] X[v][r] for the lane's 8 key channels c_k (k = 4 mt + i), complete in every lane
+__device__ __forceinline__ void colred(const Tile& t, const f32x4* X, f32x4 out[8]) {
+  const int l = lane_id();
+  f32x4 xv[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) xv[nt] = X[16 * nt + (l & 15)];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const float m = t.a[mt][nt][i];
+        s[0] = fmaf(m, xv[nt][0], s[0]);
+        s[1] = fmaf(m, xv[nt][1], s[1]);
+        s[2] = fmaf(m, xv[nt][2], s[2]);
+        s[3] = fmaf(m, xv[nt][3], s[3]);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = sum16(s[r]);
+      out[4 * mt + i] = s;
+    }
+  }
+}
+
+// part[w][v][r] = sum over this wave's 32 channels c of M[c][v] Y[c][r]  (caller sums the 4 waves)
+__device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*part)[VD]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  f32x4 yc[2][4];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yc[mt][i] = Y[32 * w + 16 * mt + 4 * q + i];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float m = t.a[mt][nt][i];
+        s[0] = fmaf(m, yc[mt][i][0], s[0]);
+        s[1] = fmaf(m, yc[mt][i][1], s[1]);
+        s[2] = fmaf(m, yc[mt][i][2], s[2]);
+        s[3] = fmaf(m, yc[mt][i][3], s[3]);
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[r] += __shfl_xor(s[r], 16);
+      s[r] += __shfl_xor(s[r], 32);
+    }
+    if (q == 0) part[w][16 * nt + (l & 15)] = s;
+  }
+}
+
+// R x R product sum_x A[a][x] B[x][r] over 128 x (A row-major [4][128], B [128] of f32x4), computed by one wave
+__device__ __forceinline__ void small_gram(const float (*A)[128], const f32x4* B, float M[4][4]) {
+  const int l = lane_id();
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float s = A[a][l] * B[l][r];
+      s = fmaf(A[a][l + 64], B[l + 64][r], s);
+      M[a][r] = sum64(s);
+    }
+  }
+}
+
+// CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835) on the 2 rows a lane of wave 0 holds
+__device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
+  float gg[10];
+  int k = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c <= r; ++c) gg[k++] = sum64(fmaf(p0[r], p0[c], p1[r] * p1[c]));
+  float ll[10];
+  ll[0] = rsqrt_rn(fmaxf(gg[0], 1e-30f));
+  ll[1] = gg[1] * ll[0];
+  ll[2] = rsqrt_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
+  ll[3] = gg[3] * ll[0];
+  ll[4] = (gg[4] - ll[3] * ll[1]) * ll[2];
+  ll[5] = rsqrt_rn(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
+  ll[6] = gg[6] * ll[0];
+  ll[7] = (gg[7] - ll[6] * ll[1]) * ll[2];
+  ll[8] = (gg[8] - ll[6] * ll[3] - ll[7] * ll[4]) * ll[5];
+  ll[9] = rsqrt_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    f32x4& p = s ? p1 : p0;
+    p[0] = p[0] * ll[0];
+    p[1] = (p[1] - p[0] * ll[1]) * ll[2];
+    p[2] = (p[2] - p[0] * ll[3] - p[1] * ll[4]) * ll[5];
+    p[3] = (p[3] - p[0] * ll[6] - p[1] * ll[7] - p[2] * ll[8]) * ll[9];
+  }
+}
+
+// modified Gram-Schmidt on the R columns of the 128 x 4 matrix whose rows l, l + 64 a lane of wave 0 holds
+// (kernels.py:2170-2183, 2190-2203)
+__device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
+  for (int j = 0; j < R; ++j) {
+    for (int c = 0; c < j; ++c) {
+      const float sc = sum64(fmaf(p0[c], p0[j], p1[c] * p1[j]));
+      p0[j] = p0[j] - sc * p0[c];
+      p1[j] = p1[j] - sc * p1[c];
+    }
+    const float nrm = sum64(fmaf(p0[j], p0[j], p1[j] * p1[j]));
+    const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
+    p0[j] *= rs;
+    p1[j] *= rs;
+  }
+}
+
+// Tile init with the dequantised checkpoint codes  x svr[v] x skl[c]  (codes read in place from the state block)
+__device__ __forceinline__ void tile_from_codes(Tile& t, const int8_t* Sq, const float* svr, const float* skl) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt) {
+    const int c0 = 32 * w + 16 * mt + 4 * q;
+    float kc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const uint32_t word = *(const uint32_t*)(Sq + v * KD + c0);
+      const float rv = svr[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = ((float)(int)(int8_t)(word >> (8 * i)) * rv) * kc[i];
+    }
+  }
+}
+
+// acc[c][v] += sum_j A[c][j] B[v][j] over nks 32-entry steps (bf16 operands from LDS, fp32 accumulate)
+__device__ __forceinline__ void rebuild_mfma(Tile& t, const bf16_t (*A)[OPS], const bf16_t (*B)[OPS], int nks) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  for (int ks = 0; ks < nks; ++ks) {
+    bf16x8 af[2];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) af[mt] = *(const bf16x8*)&A[32 * w + 16 * mt + (l & 15)][32 * ks + 8 * q];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x8 bfr = *(const bf16x8*)&B[16 * nt + (l & 15)][32 * ks + 8 * q];
+#pragma unroll
+      for (int mt = 0; mt < 2; ++mt) t.a[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr, t.a[mt][nt], 0, 0, 0);
+    }
+  }
+}
+
+// Stage the window into the MFMA operands.  GDN (kda = false): op0[c][j] = K_j[c], op1 / op2 [v][j] = hi / lo of
+// w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c] with D_j the product of the
+// later entries' decays (kernels.py:1453-1463), op2[v][j] = u_j[v].  Entries j >= h and the padding to 32 are zero.
+__device__ void stage_window(FlushShared& sh, const lq_state& st, int slot, int hv, int h, int LP, bool kda) {
+  const int tid = threadIdx.x;
+  const int G = st.HV / st.H, hk = hv / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD;
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * VD;
+  if (!kda) {
+    for (int it = tid; it < LP * 16; it += FT) {       // (j, 8-column chunk)
+      const int j = it >> 4, c8 = (it & 15) * 8;
+      uint4 kw = make_uint4(0, 0, 0, 0), uw = make_uint4(0, 0, 0, 0);
+      if (j < h) {
+        kw = *(const uint4*)(Kb + (long long)j * KD + c8);
+        uw = *(const uint4*)(Ub + (long long)j * VD + c8);
+      }
+      const float wj = j < h ? sh.w[j] : 0.f;
+      const uint32_t ku[4] = {kw.x, kw.y, kw.z, kw.w}, uu[4] = {uw.x, uw.y, uw.z, uw.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bf16_t kb = (bf16_t)(ku[e >> 1] >> (16 * (e & 1)));
+        const bf16_t ub = (bf16_t)(uu[e >> 1] >> (16 * (e & 1)));
+        sh.op[0][c8 + e][j] = kb;
+        const float wu = wj * bf2f(ub);
+        const bf16_t hi = f2bf(wu);
+        sh.op[1][c8 + e][j] = hi;
+        sh.op[2][c8 + e][j] = f2bf(wu - bf2f(hi));
+      }
+    }
+  } else {
+    if (tid < KD) {                                     // thread per key channel: backward decay product
+      const int c = tid;
+      const f16_t* Gb = (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD + c;
+      float dcur = 1.0f;
+      for (int j = LP - 1; j >= 0; --j) {
+        bf16_t hi = 0, lo = 0;
+        if (j < h) {
+          const float kd = bf2f(Kb[(long long)j * KD + c]) * (sh.w[j] * dcur);
+          hi = f2bf(kd);
+          lo = f2bf(kd - bf2f(hi));
+          dcur = dcur * h2f(Gb[(long long)j * KD]);
+        }
+        sh.op[0][c][j] = hi;
+        sh.op[1][c][j] = lo;
+      }
+    } else {
+      const int v = tid - KD;
+      for (int j = 0; j < LP; ++j) sh.op[2][v][j] = j < h ? Ub[(long long)j * VD + v] : (bf16_t)0;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// flush (kernels.py:1077-2033)
+// ------------------------------------------------------------------------------------------------------------------
+template <bool KDA>
+__global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx,
+                                                   float qmax) {
+  __shared__ FlushShared sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  const int slot = idx[n];
+  if (slot <= 0) return;
+  const long long sh_ = (long long)slot * HV + hv;
+  if (st.hcnt[sh_] != L) return;                      // due = slot > 0 and a full window (kernels.py:1200)
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  char* base = block_base(st, slot, hv);
+  int8_t* Sq = (int8_t*)base;
+  float* Sk = (float*)(base + VD * KD);
+  float* Sv = Sk + KD;
+  f16_t* UQ = (f16_t*)(Sv + VD);
+  const int LP = (L + 31) & ~31;
+
+  // ---- stage 1: scalars, old factors and scales to LDS ----
+  float pn = 1.f, rpn = 1.f;
+  if (!KDA) {
+    pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);               // kernels.py:1471
+    rpn = 1.0f / pn;                                  // kernels.py:1477
+  }
+  if (tid < KD) {
+    const int c = tid;
+    float pcv = 1.f;
+    if (KDA) { pcv = (float)exp((double)st.Pbuf[sh_ * KD + c]); sh.pc[c] = pcv; }   // kernels.py:1451
+    sh.skl[c] = KDA ? Sk[c] * pcv : Sk[c];                                          // kernels.py:1519
+    for (int a = 0; a < 4; ++a) {
+      float u = a < R ? h2f(UQ[a * (KD + VD) + c]) : 0.f;
+      if (KDA) u = hround(u * pcv);                                                   // kernels.py:1464-1465
+      sh.uo[a][c] = u;
+    }
+  } else {
+    const int v = tid - KD;
+    sh.svr[v] = KDA ? Sv[v] * (1.0f / qmax) : Sv[v] * (pn / qmax);                  // kernels.py:1468, 1483
+    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? h2f(UQ[a * (KD + VD) + KD + v]) : 0.f;
+    f32x4 q0v;
+    for (int r = 0; r < 4; ++r) q0v[r] = r < R ? hround(Q0[v * R + r]) : 0.f;   // kernels.py:1573-1577
+    sh.qv[v] = q0v;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < L ? st.Wbuf[sh_ * L + tid] : 0.f;
+  __syncthreads();
+  stage_window(sh, st, slot, hv, L, LP, KDA);
+  __syncthreads();
+
+  // ---- stage 2: B = deq(S0) (+ decay) + window, fp16 (kernels.py:1483-1571) ----
+  Tile t;
+  tile_from_codes(t, Sq, sh.svr, sh.skl);
+  if (!KDA) {
+    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+  } else {
+    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+    rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
+  }
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = hround(t.a[mt][nt][i]);
+
+  // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
+  // P = B^T Q + pn U_old (Q_old^T Q), fp16
+  auto p_step = [&]() {
+    float M[4][4];
+    small_gram(sh.qo, sh.qv, M);                      // Q_old^T Q (every wave)
+    f32x4 pc8[8];
+    colred(t, sh.qv, pc8);
+    if ((l & 15) == 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const int c = 32 * w + 16 * (k >> 2) + 4 * q + (k & 3);
+        f32x4 p;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float corr = sh.uo[0][c] * M[0][r] + sh.uo[1][c] * M[1][r] + sh.uo[2][c] * M[2][r] + sh.uo[3][c] * M[3][r];
+          p[r] = r < R ? hround(pc8[k][r] + pn * corr) : 0.f;
+        }
+        sh.pp[c] = p;
+      }
+    }
+  };
+  p_step();
+  __syncthreads();
+  // Q = B P16 + pn Q_old (U_old^T P16)
+  rowred(t, sh.pp, sh.qpart);
+  __syncthreads();
+  if (tid < VD) {
+    const int v = tid;
+    f32x4 s = sh.qpart[0][v] + sh.qpart[1][v] + sh.qpart[2][v] + sh.qpart[3][v];
+    sh.qpart[0][v] = s;
+  }
+  float M2[4][4];
+  small_gram(sh.uo, sh.pp, M2);
+  __syncthreads();
+  if (tid < VD) {
+    const int v = tid;
+    f32x4 s = sh.qpart[0][v];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      s[r] += pn * (sh.qo[0][v] * M2[0][r] + sh.qo[1][v] * M2[1][r] + sh.qo[2][v] * M2[2][r] + sh.qo[3][v] * M2[3][r]);
+    sh.qv[v] = s;
+  }
+  __syncthreads();
+  // CholeskyQR2 (wave 0), fp16 Q
+  if (w == 0) {
+    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+    cholqr_pass(p0, p1);
+    cholqr_pass(p0, p1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { p0[r] = r < R ? hround(p0[r]) : 0.f; p1[r] = r < R ? hround(p1[r]) : 0.f; }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+  }
+  __syncthreads();
+  p_step();                                           // U16 = P step with Q16
+  __syncthreads();
+
+  // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
+  {
+    f32x4 qov[8], qnv[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      qov[nt] = f32x4{sh.qo[0][v], sh.qo[1][v], sh.qo[2][v], sh.qo[3][v]};
+      qnv[nt] = sh.qv[v];
+    }
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = 32 * w + 16 * mt + 4 * q + i;
+        const f32x4 uoc = f32x4{sh.uo[0][c], sh.uo[1][c], sh.uo[2][c], sh.uo[3][c]};
+        const f32x4 unc = sh.pp[c];
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          float e = KDA ? t.a[mt][nt][i] : t.a[mt][nt][i] * rpn;
+          e = fmaf(qov[nt][0], uoc[0], e);
+          e = fmaf(qov[nt][1], uoc[1], e);
+          e = fmaf(qov[nt][2], uoc[2], e);
+          e = fmaf(qov[nt][3], uoc[3], e);
+          if (!KDA) e = e * pn;
+          e = fmaf(-qnv[nt][0], unc[0], e);
+          e = fmaf(-qnv[nt][1], unc[1], e);
+          e = fmaf(-qnv[nt][2], unc[2], e);
+          e = fmaf(-qnv[nt][3], unc[3], e);
+          t.a[mt][nt][i] = hround(e);
+        }
+      }
+  }
+
+  // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
+  float rsk[8];
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) s += fabsf(t.a[mt][nt][i]);
+      s = sum16(s);
+      const float msum = s * (1.0f / VD);
+      rsk[4 * mt + i] = fminf(rsqrt_rn(msum), 1.0f / LQ_EPS);
+      if ((l & 15) == 0) Sk[32 * w + 16 * mt + 4 * q + i] = fmaxf(sqrtf(msum), LQ_EPS);
+    }
+  // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    float m = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        t.a[mt][nt][i] *= rsk[4 * mt + i];
+        m = fmaxf(m, fabsf(t.a[mt][nt][i]));
+      }
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    const float rmax = fmaxf(fmaxf(fmaxf(sh.rowmax[0][v], sh.rowmax[1][v]), fmaxf(sh.rowmax[2][v], sh.rowmax[3][v])), LQ_EPS);
+    const float rq = qmax * (1.0f / rmax);
+    if (w == 0 && q == 0) Sv[v] = rmax;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t bits = __float_as_uint(__builtin_fmaf(t.a[mt][nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+        word |= (bits & 0xffu) << (8 * i);
+      }
+      *(uint32_t*)(Sq + v * KD + 32 * w + 16 * mt + 4 * q) = word;
+    }
+  }
+  // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
+  if (tid < KD) {
+    const int c = tid;
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + c] = f2h(sh.pp[c][r]);
+    if (KDA) {
+      st.Pbuf[sh_ * KD + c] = 0.f;
+      f16_t* Gb = (f16_t*)st.Gbuf + sh_ * L * KD + c;
+      for (int j = 0; j < L; ++j) Gb[(long long)j * KD] = 0x3c00;   // fp16 1.0
+    }
+  } else {
+    const int v = tid - KD;
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
+  }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    if (!KDA) st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// standalone quantize of an fp32 state (kernels.py:2126-2242)
+// ------------------------------------------------------------------------------------------------------------------
+struct QuantShared {
+  f32x4 qv[VD];
+  f32x4 pp[KD];
+  f32x4 qpart[4][VD];
+  float rowmax[4][VD];
+  float sk[KD];
+};
+
+__global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* __restrict__ Q0,
+                                                      const int* __restrict__ idx, float qmax) {
+  __shared__ QuantShared sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  const int slot = idx[n];
+  if (slot <= 0) return;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  char* base = block_base(st, slot, hv);
+  const float* S = (const float*)base;
+  Tile t;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const float4 x = *(const float4*)(S + v * KD + 32 * w + 16 * mt + 4 * q);
+      t.a[mt][nt] = f32x4{x.x, x.y, x.z, x.w};
+    }
+  if (tid < VD) {
+    f32x4 q0v;
+    for (int r = 0; r < 4; ++r) q0v[r] = r < R ? Q0[tid * R + r] : 0.f;
+    sh.qv[tid] = q0v;
+  }
+  __syncthreads();
+  // P = S^T Q, MGS; Q = S P, MGS (ITERS = 1)
+  f32x4 pc8[8];
+  colred(t, sh.qv, pc8);
+  if ((l & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = pc8[k];
+  }
+  __syncthreads();
+  if (w == 0) {
+    f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
+    mgs(p0, p1, R);
+    sh.pp[l] = p0;
+    sh.pp[l + 64] = p1;
+  }
+  __syncthreads();
+  rowred(t, sh.pp, sh.qpart);
+  __syncthreads();
+  if (w == 0) {
+    f32x4 p0 = sh.qpart[0][l] + sh.qpart[1][l] + sh.qpart[2][l] + sh.qpart[3][l];
+    f32x4 p1 = sh.qpart[0][l + 64] + sh.qpart[1][l + 64] + sh.qpart[2][l + 64] + sh.qpart[3][l + 64];
+    mgs(p0, p1, R);
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+  }
+  __syncthreads();
+  // U = fp16(S^T Q), Q16 = fp16(Q)
+  colred(t, sh.qv, pc8);
+  __syncthreads();
+  if ((l & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      f32x4 u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(pc8[k][r]) : 0.f;
+      sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = u;
+    }
+  }
+  if (tid < VD) {
+    f32x4 x = sh.qv[tid];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = r < R ? hround(x[r]) : 0.f;
+    sh.qv[tid] = x;
+  }
+  __syncthreads();
+  // E = S - Q U^T (fp32), column scales
+  {
+    f32x4 qnv[8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) qnv[nt] = sh.qv[16 * nt + (l & 15)];
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const f32x4 unc = sh.pp[32 * w + 16 * mt + 4 * q + i];
+        float s = 0.f;
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) {
+          float e = t.a[mt][nt][i];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) e = fmaf(-qnv[nt][r], unc[r], e);
+          t.a[mt][nt][i] = e;
+          s += fabsf(e);
+        }
+        s = sum16(s);
+        const float skc = fmaxf(sqrtf(s / (float)VD), LQ_EPS);      // kernels.py:2222
+        if ((l & 15) == 0) sh.sk[32 * w + 16 * mt + 4 * q + i] = skc;
+      }
+  }
+  __syncthreads();
+  float skr[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) skr[k] = sh.sk[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    float m = 0.f;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[mt][nt][i] / skr[4 * mt + i]));   // kernels.py:2224-2227
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
+  }
+  __syncthreads();
+  // every read of the fp32 state is done: the checkpoint may now overwrite the block
+  int8_t* Sq = (int8_t*)base;
+  float* Sk = (float*)(base + VD * KD);
+  float* Sv = Sk + KD;
+  f16_t* UQ = (f16_t*)(Sv + VD);
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    const float svv = fmaxf(fmaxf(fmaxf(sh.rowmax[0][v], sh.rowmax[1][v]), fmaxf(sh.rowmax[2][v], sh.rowmax[3][v])), LQ_EPS);
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = (t.a[mt][nt][i] / (skr[4 * mt + i] * svv)) * qmax;   // kernels.py:2229
+        const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
+        word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
+      }
+      *(uint32_t*)(Sq + v * KD + 32 * w + 16 * mt + 4 * q) = word;
+    }
+    if (w == 0 && q == 0) Sv[v] = svv;
+  }
+  if (tid < KD) {
+    Sk[tid] = sh.sk[tid];
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + tid] = f2h(sh.pp[tid][r]);
+  } else {
+    const int v = tid - KD;
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
+  }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(FT) void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
+  __shared__ FlushShared sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  const int slot = idx[n];
+  if (slot <= 0) return;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  char* base = block_base(st, slot, hv);
+  const int8_t* Sq = (const int8_t*)base;
+  const float* Sk = (const float*)(base + VD * KD);
+  const float* Sv = Sk + KD;
+  const f16_t* UQ = (const f16_t*)(Sv + VD);
+  const int h = min(st.hcnt[sh_], L);
+  const float P = st.Pbuf[sh_];
+  const int LP = h > 0 ? ((h + 31) & ~31) : 0;
+  if (tid < KD) {
+    sh.skl[tid] = Sk[tid];
+    for (int a = 0; a < 4; ++a) sh.uo[a][tid] = a < R ? h2f(UQ[a * (KD + VD) + tid]) : 0.f;
+  } else {
+    const int v = tid - KD;
+    sh.svr[v] = Sv[v];
+    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? h2f(UQ[a * (KD + VD) + KD + v]) : 0.f;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < h ? st.Wbuf[sh_ * L + tid] : 0.f;
+  __syncthreads();
+  if (LP > 0) stage_window(sh, st, slot, hv, h, LP, false);
+  Tile t;
+  {
+    const float inv = 1.0f / qmax;
+#pragma unroll
+    for (int mt = 0; mt < 2; ++mt) {
+      const int c0 = 32 * w + 16 * mt + 4 * q;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const int v = 16 * nt + (l & 15);
+        const uint32_t word = *(const uint32_t*)(Sq + v * KD + c0);
+        const float rv = sh.svr[v];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = c0 + i;
+          float x = (((float)(int)(int8_t)(word >> (8 * i)) * inv) * sh.skl[c]) * rv;    // kernels.py:2107
+#pragma unroll
+          for (int a = 0; a < 4; ++a) x = fmaf(sh.qo[a][v], sh.uo[a][c], x);           // kernels.py:2109-2111
+          t.a[mt][nt][i] = x * P;                                                       // kernels.py:2113
+        }
+      }
+    }
+  }
+  __syncthreads();
+  if (LP > 0) {
+    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+  }
+  __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
+  float* S = (float*)base;
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      *(float4*)(S + v * KD + 32 * w + 16 * mt + 4 * q) = make_float4(t.a[mt][nt][0], t.a[mt][nt][1], t.a[mt][nt][2], t.a[mt][nt][3]);
+    }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// low-rank factoriser (kernels.py:2246-2314): x [n][K][V]; P = MGS(x Q), Q = MGS(x^T P) x iters; U = x Q
+// ------------------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(FT) void lowrank_kernel(const float* __restrict__ x, const float* __restrict__ Q0,
+                                                     float* __restrict__ U, float* __restrict__ Qo, int R, int iters) {
+  __shared__ QuantShared sh;
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  const float* X = x + (long long)b * KD * VD;
+  Tile t;                                             // t[c][v] = x[c][v]
+#pragma unroll
+  for (int mt = 0; mt < 2; ++mt)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = X[(32 * w + 16 * mt + 4 * q + i) * VD + v];
+    }
+  if (tid < VD) {
+    f32x4 q0v;
+    for (int r = 0; r < 4; ++r) q0v[r] = r < R ? Q0[tid * R + r] : 0.f;
+    sh.qv[tid] = q0v;
+  }
+  __syncthreads();
+  f32x4 pc8[8];
+  for (int it = 0; it < iters; ++it) {
+    colred(t, sh.qv, pc8);                            // P = x Q
+    if ((l & 15) == 0) {
+#pragma unroll
+      for (int k = 0; k < 8; ++k) sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = pc8[k];
+    }
+    __syncthreads();
+    if (w == 0) {
+      f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
+      mgs(p0, p1, R);
+      sh.pp[l] = p0;
+      sh.pp[l + 64] = p1;
+    }
+    __syncthreads();
+    rowred(t, sh.pp, sh.qpart);                       // Q = x^T P
+    __syncthreads();
+    if (w == 0) {
+      f32x4 p0 = sh.qpart[0][l] + sh.qpart[1][l] + sh.qpart[2][l] + sh.qpart[3][l];
+      f32x4 p1 = sh.qpart[0][l + 64] + sh.qpart[1][l + 64] + sh.qpart[2][l + 64] + sh.qpart[3][l + 64];
+      mgs(p0, p1, R);
+      sh.qv[l] = p0;
+      sh.qv[l + 64] = p1;
+    }
+    __syncthreads();
+  }
+  colred(t, sh.qv, pc8);                              // U = x Q
+  if ((l & 15) == 0) {
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const int c = 32 * w + 16 * (k >> 2) + 4 * q + (k & 3);
+      for (int r = 0; r < R; ++r) U[((long long)b * KD + c) * R + r] = pc8[k][r];
+    }
+  }
+  if (tid < VD)
+    for (int r = 0; r < R; ++r) Qo[((long long)b * VD + tid) * R + r] = sh.qv[tid][r];
+}
+
+int check_block_state(const lq_state* st, bool need_buf) {
+  if (!st || !st->ssm || !st->hcnt || !st->Wbuf || !st->Pbuf) return LQ_ERR_ARG;
+  if (st->K != KD || st->V != VD || st->L < 1 || st->L > LPMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0) return LQ_ERR_ARG;
+  if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3)) return LQ_ERR_ARG;
+  if (((uintptr_t)st->ssm & 15) != 0) return LQ_ERR_ARG;
+  if (need_buf && (!st->Kbuf || !st->Ubuf)) return LQ_ERR_ARG;
+  return LQ_OK;
+}
+
+}  // namespace
+
+extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream) {
+  int rc = check_block_state(st, true);
+  if (rc) return rc;
+  if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || (kda && !st->Gbuf)) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  dim3 grid((unsigned)(N * st->HV));
+  if (kda) flush_kernel<true><<<grid, FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
+  else flush_kernel<false><<<grid, FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
+  int rc = check_block_state(st, false);
+  if (rc) return rc;
+  if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  quantize_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
+  int rc = check_block_state(st, true);
+  if (rc) return rc;
+  if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  dequant_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, idx, qmax);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_lowrank(const float* x, const float* Q0, float* U, float* Q, int n, int K, int V, int R, int iters,
+                          void* stream) {
+  if (K != KD || V != VD || R < 1 || R > 4 || n < 0 || iters < 1) return LQ_ERR_ARG;
+  if (n == 0) return LQ_OK;
+  if (!x || !Q0 || !U || !Q) return LQ_ERR_ARG;
+  lowrank_kernel<<<dim3((unsigned)n), FT, 0, (hipStream_t)stream>>>(x, Q0, U, Q, R, iters);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}

@@ -1,0 +1,244 @@
+"""Per-layer LeapQuant state on MI355X: the 8-bit checkpoint lives inside vLLM's fp32 state slot, the window buffer next
+to it.  Drop-in for /root/reference/leapquant/state.py (same names, arguments, errors and call order).
+
+Layout of one (slot, head) inside the fp32 [V, K] state slot (state.py:1-6, 29-40 of the reference):
+    int8 residual [V][K] | smoothing scales Sk f32[K], Sv f32[V] | Compensator Tokens U^T | Q^T fp16 [R][K+V]
+The window buffer (keys, values, weights of the tokens since the last flush) and the per-slot counters are separate
+tensors; the keys are kept once per key head (Kbuf [NS, H, L, K]).
+"""
+import ctypes
+import functools
+
+import torch
+
+from . import _lib
+from . import kernels as KN
+
+WINDOW = 16          # tokens per window (L), state.py:16
+RANK = 4             # Compensator Tokens per head (R), state.py:17
+
+_make_dequant = functools.lru_cache(maxsize=None)(KN.make_dequant)
+_make_quantize = functools.lru_cache(maxsize=None)(KN.make_quantize)
+
+
+def _ident(t):
+    """Same storage + same view -> same layer state."""
+    return (t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), tuple(t.stride()))
+
+
+def _alias(ssm, dtype, shape, stride, offset):
+    out = torch.empty(0, dtype=dtype, device=ssm.device)
+    out.set_(ssm.untyped_storage(), offset, shape, stride)
+    return out
+
+
+def state_views(ssm, R):
+    """Views of the 8-bit checkpoint aliasing vLLM's fp32 state tensor [NS, HV, V, K] (no allocation): Sq (int8),
+    q32 (int32 words of Sq), sq16 (int16 pairs of Sq), Sk, Sv, skv (Sk || Sv) and uq (fp16 U^T | Q^T)."""
+    NS, HV, V, K = ssm.shape
+    SS = ssm.stride(0)
+    off = ssm.storage_offset()
+    sc = off + V * K // 4                       # fp32 offset of Sk
+    return dict(
+        Sq=_alias(ssm, torch.int8, (NS, HV, V, K), (4 * SS, 4 * V * K, K, 1), 4 * off),
+        q32=_alias(ssm, torch.int32, (NS, HV, V, K // 4), (SS, V * K, K // 4, 1), off),
+        sq16=_alias(ssm, torch.int16, (NS, HV, V, K // 2), (2 * SS, 2 * V * K, K // 2, 1), 2 * off),
+        Sk=_alias(ssm, torch.float32, (NS, HV, K), (SS, V * K, 1), sc),
+        Sv=_alias(ssm, torch.float32, (NS, HV, V), (SS, V * K, 1), sc + K),
+        skv=_alias(ssm, torch.float32, (NS, HV, K + V), (SS, V * K, 1), sc),
+        uq=_alias(ssm, torch.float16, (NS, HV, R, K + V), (2 * SS, 2 * V * K, K + V, 1), 2 * (sc + K + V)))
+
+
+class LeapQuantState:
+    """Window buffers + kernels of one linear-attention layer.
+
+    kda=False: Gated DeltaNet (Qwen).  kda=True: Kimi Delta Attention (GLM), gate_lower_bound = GLM's bounded gate.
+    nmax: the most rows one decode call can carry (accepted for parity; the HIP flush needs no work-list sizing).
+    qmax: code range of the checkpoint (127: INT8; 31: 6-bit codes in the int8 container).
+    """
+
+    def __init__(self, ssm, H, kda=False, gate_lower_bound=0.0, nmax=0, L=WINDOW, R=RANK, qmax=KN.QMAX):
+        assert ssm.dtype == torch.float32, f"LeapQuant needs the fp32 recurrent state cache, got {ssm.dtype}"
+        NS, HV, V, K = ssm.shape
+        SS = ssm.stride(0)
+        assert ssm.stride()[1:] == (V * K, K, 1), f"state inner dims must be packed, got strides {ssm.stride()}"
+        assert V * K // 4 + K + V + R * (K + V) // 2 <= V * K, "checkpoint must fit inside the fp32 slot"
+        dev = ssm.device
+        self.key = _ident(ssm)
+        self.kda, self.NS, self.HV, self.H, self.K, self.V, self.L, self.R = kda, NS, HV, H, K, V, L, R
+        self.SS, self.qmax, self.glb = SS, float(qmax), float(gate_lower_bound)
+        KA = K if kda else 1
+
+        self.Kbuf = torch.zeros(NS, H, L, K, device=dev, dtype=torch.bfloat16)
+        self.Ubuf = torch.zeros(NS, HV, L, V, device=dev, dtype=torch.bfloat16)
+        self.Wbuf = torch.zeros(NS, HV, L, device=dev)
+        self.Pbuf = torch.zeros(NS, HV, KA, device=dev) if kda else torch.ones(NS, HV, 1, device=dev)
+        # KDA: each entry's per-step decay factor exp(g_j) (fp16); GDN: unused
+        self.Gbuf = (torch.ones(NS, HV, L, KA, device=dev, dtype=torch.float16) if kda
+                     else torch.zeros(NS, HV, L, 1, device=dev))
+        self.Gd = torch.zeros(1, 1, 1, 1, dtype=torch.bfloat16, device=dev)
+        self.hcnt = torch.zeros(NS, HV, dtype=torch.int32, device=dev)
+        self.Q0 = torch.randn(V, R, generator=torch.Generator().manual_seed(0)).to(dev)
+
+        if kda:
+            self.kstep = KN.make_kda_step(NS, HV, H, K, V, L, SS, R=R, GLB=float(gate_lower_bound))
+        else:
+            self.kstep = KN.make_gdn_step(NS, HV, H, K, V, L, SS, R=R)
+        self.kflush = KN.make_flush(NS, HV, K, V, L, SS, R=R, ITERS=1, KDA=kda, NMAX=nmax, qmax=qmax)
+        if not kda:                          # KDA prefill round trip runs in torch + the HIP low-rank factoriser
+            self.kdeq = _make_dequant(NS, HV, K, V, L, SS, buf_dtype=KN.BF16, R=R, qmax=qmax)
+            self.kquant = _make_quantize(NS, HV, K, V, L, SS, R=R, ITERS=1, qmax=qmax)
+        self._lib = _lib.lib()
+        self._vkey = None
+        self._skey = None
+        self._f32 = {}
+
+    def _p32(self, t):
+        """fp32 copy of a layer parameter, cached per tensor (several layers can share one state tensor)."""
+        c = self._f32.get(t.data_ptr())
+        if c is None:
+            c = self._f32[t.data_ptr()] = t.detach().to(torch.float32).contiguous()
+        return c
+
+    def views(self, ssm):
+        k = _ident(ssm)
+        if self._vkey != k:
+            self._vkey, self._v = k, state_views(ssm, self.R)
+        return self._v
+
+    def _struct(self, ssm):
+        """lq_state of this layer for the cache tensor ssm (cached per tensor identity)."""
+        k = _ident(ssm)
+        if self._skey != k:
+            if ssm.data_ptr() % 16 or self.SS % 4:
+                raise ValueError("the fp32 state cache must be 16-byte aligned with a slot stride divisible by 4")
+            self._st = KN.state_struct(ssm, self.SS, self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf,
+                                       self.Gbuf if self.kda else None, self.hcnt, self.NS, self.HV, self.H, self.K,
+                                       self.V, self.L, self.R)
+            self._skey = k
+        return self._st
+
+    def decode(self, ssm, mixed, a, b, A_log, dt_bias, idx, out):
+        """One decode token per row, then the end-of-window flush of the heads whose window became full.
+        a: GDN (N, HV) | KDA (N, HV, K) raw gate;  dt_bias: GDN (HV,) | KDA (HV*K,)."""
+        A_log = A_log if A_log.dtype == torch.float32 else self._p32(A_log)
+        dt_bias = dt_bias if dt_bias.dtype == torch.float32 else self._p32(dt_bias)
+        KA = self.K if self.kda else 1
+        N = idx.shape[0]
+        a = a.reshape(N, self.HV, KA).contiguous()
+        dt_bias = dt_bias.reshape(self.HV, KA).contiguous()
+        A_log = A_log.reshape(self.HV).contiguous()
+        idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        idx = idx.contiguous()
+        if (mixed.dtype != torch.bfloat16 or not mixed.is_contiguous()
+                or mixed.shape != (N, 2 * self.H * self.K + self.HV * self.V)):
+            raise ValueError("mixed: contiguous bf16 [N, 2HK + HV V] expected")
+        if out.dtype != torch.bfloat16 or out.numel() != N * self.HV * self.V or not out.is_contiguous():
+            raise ValueError("out: contiguous bf16 [N, HV, V] expected")
+        if b.dtype != torch.bfloat16 or b.numel() != N * self.HV:
+            raise ValueError("b: bf16 [N, HV] expected")
+        b = b.contiguous()
+        st = self._struct(ssm)
+        io = KN._step_io(mixed, a, b, A_log, dt_bias, idx, out, self.kstep_scale)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(mixed.device).cuda_stream)
+        L = self._lib
+        if self.kda:
+            _lib.check(L.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(self.glb), stream),
+                       "lq_kda_step")
+        else:
+            _lib.check(L.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), stream), "lq_gdn_step")
+        _lib.check(L.lq_flush(ctypes.byref(st), ctypes.c_void_p(self.Q0.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+                              N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
+
+    @property
+    def kstep_scale(self):
+        return 128 ** -0.5 if self.kda else self.K ** -0.5
+
+    def _kda_rebuild(self, ssm, sl):
+        """KDA: S = exp(P) (Q U^T + deq(res)) + sum_{j<h} w_j u_j (x) (k_j * D_j), D_j the product of the decays of the
+        entries after j (entries j >= h count as 1).  Torch on the GPU, as in state.py:118-128 of the reference."""
+        v = self.views(ssm)
+        K = self.K
+        uq = v["uq"][sl].float()
+        S0 = torch.matmul(uq[..., K:].transpose(-1, -2), uq[..., :K]) \
+            + v["Sq"][sl].float() * (v["Sk"][sl][..., None, :] / self.qmax) * v["Sv"][sl][..., :, None]
+        h = self.hcnt[sl]
+        live = torch.arange(self.L, device=ssm.device)[None, None, :, None] < h[..., None, None]
+        E = torch.where(live, self.Gbuf[sl].float(), torch.ones((), device=ssm.device))
+        # D_j = prod_{i > j} E_i: exclusive reverse cumulative product
+        D = torch.cat([torch.flip(torch.cumprod(torch.flip(E[:, :, 1:], [2]), 2), [2]), torch.ones_like(E[:, :, :1])], 2)
+        G = self.HV // self.H
+        kdec = self.Kbuf[sl].float().repeat_interleave(G, dim=1) * D
+        wu = self.Wbuf[sl][..., None] * self.Ubuf[sl].float()                     # [n, HV, L, V]
+        return torch.exp(self.Pbuf[sl])[..., None, :] * S0 + torch.matmul(wu.transpose(-1, -2), kdec)
+
+    def _kda_checkpoint(self, ssm, sl):
+        """KDA: 8-bit checkpoint of the fp32 states in the slots sl (state.py:130-142): rank-R factors from the HIP
+        low-rank factoriser (3 subspace iterations), fp16; smoothed residual quantised with clamp(round(.))."""
+        v = self.views(ssm)
+        S = ssm[sl].float()                                        # [n, HV, V, K]
+        U, Q = KN.lowrank_factor(S.transpose(-1, -2), self.R)     # rank-R fit in the [K, V] orientation
+        Uh, Qh = U.half(), Q.half()
+        res = S - torch.matmul(Qh.float(), Uh.float().transpose(-1, -2))
+        sk = res.abs().mean(-2).sqrt().clamp_min(KN.EPS)
+        sv = (res.abs() / sk[..., None, :]).amax(-1).clamp_min(KN.EPS)
+        codes = torch.round(res / (sk[..., None, :] * sv[..., :, None]) * self.qmax).clamp(-self.qmax, self.qmax)
+        v["Sq"][sl] = codes.to(torch.int8)
+        v["Sk"][sl] = sk
+        v["Sv"][sl] = sv
+        v["uq"][sl] = torch.cat([Uh.transpose(-1, -2), Qh.transpose(-1, -2)], -1)
+        self.Wbuf[sl] = 0.0
+        self.Pbuf[sl] = 0.0
+        self.Gbuf[sl] = 1.0
+        self.hcnt[sl] = 0
+
+    def dequantize(self, ssm, idx):
+        """Materialise the fp32 state of the slots idx in place (before the engine's own prefill kernel runs)."""
+        if idx.numel() == 0:
+            return
+        if self.kda:
+            sl = idx.to(torch.int64)
+            ssm[sl] = self._kda_rebuild(ssm, sl)
+            return
+        v = self.views(ssm)
+        self.kdeq(ssm, v["Sq"], v["Sk"], v["Sv"], self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf, self.Gbuf, self.hcnt,
+                  v["uq"], idx.to(torch.int32).contiguous())
+
+    def quantize(self, ssm, idx):
+        """Write the 8-bit checkpoint of the fp32 states in the slots idx and reset their windows (after a prefill)."""
+        if idx.numel() == 0:
+            return
+        if self.kda:
+            self._kda_checkpoint(ssm, idx.to(torch.int64))
+            return
+        v = self.views(ssm)
+        self.kquant(ssm, v["Sq"], v["Sk"], v["Sv"], v["uq"], self.Wbuf, self.Pbuf, self.hcnt, self.Q0,
+                    idx.to(torch.int32).contiguous())
+
+
+_STATES = {}
+_GEN = [0]
+
+
+def get_state(layer, ssm, **kw):
+    """The LeapQuantState of `layer` for its current state tensor (rebuilt when the engine swaps the cache after
+    profiling)."""
+    st = layer.__dict__.get("_leapquant")
+    k = _ident(ssm)
+    if st is not None and st.key == k:
+        return st
+    if st is not None and st.gen == _GEN[0]:            # cache re-allocated: drop all buffers of the old one
+        _GEN[0] += 1
+        _STATES.clear()
+        if torch.cuda.is_available():
+            torch.cuda.empty_cache()
+    st = _STATES.get(k)
+    if st is None:
+        cc = getattr(layer, "cache_config", None)
+        if cc is not None and getattr(cc, "mamba_cache_mode", "none") != "none":
+            raise RuntimeError("LeapQuant keeps each sequence's window buffer next to its state slot and does not support "
+                               "prefix caching of the recurrent state: run vLLM with --no-enable-prefix-caching")
+        st = _STATES[k] = LeapQuantState(ssm, **kw)
+        st.gen = _GEN[0]
+    layer._leapquant = st
+    return st

@@ -14,12 +14,23 @@ def pytest_configure(config):
 
 
 def pytest_collection_modifyitems(config, items):
-    # GPU tests run in one process on the GPU box; print the case name before each so a fault names its test.
-    pass
+    """GPU tests are skipped only where there is no GPU at all; on a GPU box a missing liblq.so fails them."""
+    try:
+        import torch
+        has_gpu = torch.cuda.device_count() > 0
+    except Exception:
+        has_gpu = False
+    if has_gpu:
+        return
+    skip = pytest.mark.skip(reason="no GPU in this container")
+    for it in items:
+        if it.get_closest_marker("gpu") is not None:
+            it.add_marker(skip)
 
 
 @pytest.fixture(autouse=True)
 def _announce(request):
+    # GPU tests run in one process on the GPU box; print the case name before each so a fault names its test.
     if request.node.get_closest_marker("gpu") is not None:
         print("\n[gpu-case] %s" % request.node.nodeid, flush=True)
     yield

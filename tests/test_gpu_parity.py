@@ -1,0 +1,292 @@
+"""GPU parity of the HIP kernels (liblq.so, through the C ABI via leapquant_amd) against the CPU oracle.
+
+Bars: per-step outputs within rtol 2e-2 / atol 1e-3 in bf16; INT8 (and 6-bit) codes equal
+except <= 1 LSB on <= 0.1 % of the elements.  Each kernel is compared on identical input state: the state is built by
+the oracle, copied to the GPU, and one kernel call is compared with one oracle call.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import lq_oracle as O
+from tests import lqgpu as G
+from tests.fixtures import gate_params, make_inputs, make_state
+
+pytestmark = pytest.mark.gpu
+
+RT, AT = 2e-2, 1e-3
+
+
+def _prestep(rng, st, Q0, kda, steps, NS, HV, H, glb=0.0):
+    """Oracle decode steps (each + flush) on random subsets of the slots: every slot ends at its own window fill."""
+    A_log, dt_bias = gate_params(HV, 128, kda)
+    for _ in range(steps):
+        sl = rng.permutation(np.arange(1, NS))[: rng.integers(1, NS)]
+        mixed, a, b = make_inputs(rng, len(sl), HV, H, kda=kda)
+        if kda:
+            O.kda_step(st, mixed, a, b, A_log, dt_bias, sl, glb=glb)
+        else:
+            O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
+        O.flush(st, Q0, sl)
+
+
+def _run_step(lq, ssm, mixed, a, b, A_log, dt_bias, idx):
+    v = lq.views(ssm)
+    out = torch.empty(idx.shape[0], lq.HV, lq.V, dtype=torch.bfloat16, device=G.DEV)
+    if lq.kda:
+        lq.kstep(v["q32"], v["Sk"], v["Sv"], v["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gbuf, lq.hcnt,
+                 mixed, a, b, A_log, dt_bias, v["uq"], idx, out)
+    else:
+        lq.kstep(v["q32"], v["Sk"], v["Sv"], v["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.hcnt,
+                 mixed, a, b, A_log, dt_bias, v["uq"], idx, out)
+    torch.cuda.synchronize()
+    return out.float().cpu().numpy()
+
+
+def _run_flush(lq, ssm, idx):
+    v = lq.views(ssm)
+    Gb = lq.Gbuf.view(torch.bfloat16) if lq.kda else lq.Gd
+    lq.kflush(v["q32"], v["Sk"], v["Sv"], v["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, Gb, lq.hcnt, v["sq16"],
+              v["uq"], lq.Q0, idx)
+    torch.cuda.synchronize()
+
+
+def _assert_step_state(g, r, slots_touched):
+    """Window appends and scalars after one step: bf16 appends within 1 ulp, fp32 scalars to 1e-6."""
+    assert np.array_equal(g["hcnt"], r["hcnt"])
+    assert G.bf16_ulps(g["Ubuf"], r["Ubuf"]).max() <= 1
+    assert G.bf16_ulps(g["Kbuf"], r["Kbuf"]).max() <= 1
+    np.testing.assert_allclose(g["Wbuf"], r["Wbuf"], rtol=1e-6, atol=0)
+    np.testing.assert_allclose(g["Pbuf"], r["Pbuf"], rtol=1e-6, atol=0)
+    if r["kda"]:
+        np.testing.assert_allclose(g["Gbuf"].astype(np.float32), r["Gbuf"].astype(np.float32), rtol=1e-3, atol=0)
+    for k in ("Sq", "Sk", "Sv", "UQ"):                   # the step never touches the checkpoint
+        assert np.array_equal(g[k], r[k]), k
+
+
+@pytest.mark.parametrize("kda", [False, True])
+@pytest.mark.parametrize("L,GQA", [(16, 2), (64, 2), (64, 1), (16, 4)])
+def test_step_matches_oracle(kda, L, GQA):
+    rng = np.random.default_rng(100 + L + GQA + 7 * kda)
+    NS, HV = 6, 4
+    H = HV // GQA
+    st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda)
+    _prestep(rng, st, Q0, kda, steps=L + 9, NS=NS, HV=HV, H=H)
+    idx = np.array([3, 0, 1, 5, -1, 2], np.int64)
+    N = len(idx)
+    mixed, a, b = make_inputs(rng, N, HV, H, kda=kda)
+    A_log, dt_bias = gate_params(HV, 128, kda)
+    ssm, lq = G.to_gpu(st)
+    before = O.copy_state(st)
+    o_ref = (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, idx)
+    o_gpu = _run_step(lq, ssm, *G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx))
+    np.testing.assert_allclose(o_gpu, o_ref, rtol=RT, atol=AT)
+    assert np.all(o_gpu[[1, 4]] == 0)                       # padding rows
+    assert (G.bf16_ulps(o_gpu, o_ref) <= 2).mean() > 0.99
+    g = G.from_gpu(ssm, lq)
+    _assert_step_state(g, st, idx)
+    assert np.array_equal(g["hcnt"][4], before["hcnt"][4])  # slot 4 is not in idx
+
+
+def _flush_case(rng, kda, L, qmax=127.0, NS=6, HV=4, H=2):
+    st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda, qmax=qmax)
+    _prestep(rng, st, Q0, kda, steps=L + 5, NS=NS, HV=HV, H=H)
+    # bring slots 1 and 3 to a full window (due), leave the others partial
+    A_log, dt_bias = gate_params(HV, 128, kda)
+    for s in (1, 3):
+        while st["hcnt"][s, 0] < L:
+            mixed, a, b = make_inputs(rng, 1, HV, H, kda=kda)
+            (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, np.array([s]))
+    return st, Q0
+
+
+@pytest.mark.parametrize("kda", [False, True])
+@pytest.mark.parametrize("L", [16, 64])
+def test_flush_matches_oracle(kda, L):
+    rng = np.random.default_rng(200 + L + 7 * kda)
+    st, Q0 = _flush_case(rng, kda, L)
+    idx = np.array([1, 0, 2, 3, -1], np.int64)
+    ssm, lq = G.to_gpu(st)
+    before = O.copy_state(st)
+    dbg = O.flush(st, Q0, idx, return_debug=True)
+    assert len(dbg["pairs"]) == 2 * 4
+    _run_flush(lq, ssm, torch.from_numpy(idx.astype(np.int32)).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    frac, mx = G.code_mismatch(g["Sq"], st["Sq"])
+    assert mx <= 1 and frac <= 1e-3, (frac, mx)
+    np.testing.assert_allclose(g["Sk"], st["Sk"], rtol=2e-3)
+    np.testing.assert_allclose(g["Sv"], st["Sv"], rtol=2e-3)
+    uq_g, uq_r = g["UQ"].astype(np.float64), st["UQ"].astype(np.float64)
+    assert np.linalg.norm(uq_g - uq_r) <= 1e-2 * np.linalg.norm(uq_r)
+    for k in ("hcnt", "Wbuf", "Pbuf"):
+        assert np.array_equal(g[k], st[k]), k
+    if kda:
+        assert np.array_equal(g["Gbuf"], st["Gbuf"])
+    # heads that were not due are untouched
+    for s in (2,):
+        assert np.array_equal(g["Sq"][s], before["Sq"][s]) and np.array_equal(g["UQ"][s], before["UQ"][s])
+
+
+@pytest.mark.parametrize("kda", [False, True])
+def test_flush_6bit_matches_oracle(kda):
+    rng = np.random.default_rng(300 + kda)
+    st, Q0 = _flush_case(rng, kda, 16, qmax=31.0)
+    idx = np.array([1, 3], np.int64)
+    ssm, lq = G.to_gpu(st, qmax=31.0)
+    O.flush(st, Q0, idx, qmax=31.0)
+    _run_flush(lq, ssm, torch.from_numpy(idx.astype(np.int32)).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    assert np.abs(g["Sq"][[1, 3]].astype(np.int32)).max() <= 31
+    frac, mx = G.code_mismatch(g["Sq"], st["Sq"])
+    assert mx <= 1 and frac <= 1e-3, (frac, mx)
+
+
+def test_flush_fully_decayed_head():
+    """Pbuf below the PNMIN floor (kernels.py:1471): the flush must stay finite and match the oracle."""
+    rng = np.random.default_rng(400)
+    st, Q0 = _flush_case(rng, False, 16)
+    st["Pbuf"][1, 0, 0] = 1e-38
+    st["Pbuf"][3, 1, 0] = 0.0
+    idx = np.array([1, 3], np.int64)
+    ssm, lq = G.to_gpu(st)
+    O.flush(st, Q0, idx)
+    _run_flush(lq, ssm, torch.from_numpy(idx.astype(np.int32)).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    assert np.all(np.isfinite(g["Sk"])) and np.all(np.isfinite(g["Sv"]))
+    frac, mx = G.code_mismatch(g["Sq"], st["Sq"])
+    assert mx <= 1 and frac <= 1e-3, (frac, mx)
+
+
+@pytest.mark.parametrize("qmax,heavy", [(127.0, False), (127.0, True), (31.0, False)])
+def test_quantize_matches_oracle(qmax, heavy):
+    rng = np.random.default_rng(500 + int(qmax) + heavy)
+    NS, HV, H = 5, 4, 2
+    S = (0.02 * (rng.standard_t(3, (NS, HV, 128, 128)) if heavy else rng.standard_normal((NS, HV, 128, 128))))
+    S = S.astype(np.float32)
+    S[2, 1] = 0.0                                        # all-zero state: EPS floors
+    st = O.new_state(NS, HV, H, L=16)
+    Q0 = O.make_q0(128, 4)
+    ssm, lq = G.to_gpu(st, qmax=qmax)
+    ssm.copy_(torch.from_numpy(S))
+    idx = np.array([2, 0, 4, 1], np.int64)
+    O.quantize(st, S, Q0, idx, qmax=qmax)
+    lq.quantize(ssm, torch.from_numpy(idx).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    for s in (1, 2, 4):
+        frac, mx = G.code_mismatch(g["Sq"][s], st["Sq"][s])
+        assert mx <= 1 and frac <= 1e-3, (s, frac, mx)
+        # an fp16 rounding flip of one factor entry moves a whole row / column of E by ~2^-11 |Q U|
+        np.testing.assert_allclose(g["Sk"][s], st["Sk"][s], rtol=1e-3)
+        np.testing.assert_allclose(g["Sv"][s], st["Sv"][s], rtol=1e-3)
+        np.testing.assert_allclose(g["UQ"][s].astype(np.float32), st["UQ"][s].astype(np.float32), rtol=2e-3, atol=2e-4)
+    assert np.all(g["Sq"][2, 1] == 0) and np.all(g["Sk"][2, 1] == np.float32(1e-12))
+    np.testing.assert_array_equal(ssm[3].cpu().numpy(), S[3])   # slot 3 not in idx: untouched
+
+
+def test_dequant_matches_oracle():
+    rng = np.random.default_rng(600)
+    NS, HV, H = 6, 4, 2
+    st, S, Q0 = make_state(rng, NS, HV, H, L=64)
+    _prestep(rng, st, Q0, False, steps=40, NS=NS, HV=HV, H=H)
+    idx = np.array([1, 0, 3, 5], np.int64)
+    ssm, lq = G.to_gpu(st)
+    ref = O.dequant(st, idx)
+    lq.dequantize(ssm, torch.from_numpy(idx).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    for s in (1, 3, 5):
+        got = ssm[s].cpu().numpy()
+        err = np.abs(got - ref[s]).max() / np.abs(ref[s]).max()
+        assert err < 1e-5, (s, err)
+    assert np.array_equal(g["hcnt"], st["hcnt"]) and np.array_equal(g["Wbuf"], st["Wbuf"])
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+def test_dense_step_matches_oracle(dtype):
+    from leapquant_amd import kernels as KN
+    rng = np.random.default_rng(700)
+    NS, HV, H, N = 5, 4, 2, 4
+    S = (0.02 * rng.standard_normal((NS, HV, 128, 128))).astype(np.float32)
+    if dtype == "bf16":
+        S = O.bf16(S)
+    idx = np.array([2, 0, 4, 1], np.int64)
+    mixed, a, b = make_inputs(rng, N, HV, H)
+    A_log, dt_bias = gate_params(HV)
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float32
+    Sg = torch.from_numpy(S).to(tdt).to(G.DEV)
+    Sref = S.copy()
+    o_ref = O.dense_state_step(Sref, mixed, a, b, A_log, dt_bias, idx, H, state_dtype=dtype)
+    mg, ag, bg, Ag, dg, ig = G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx)
+    out = torch.empty(N, HV, 128, dtype=torch.bfloat16, device=G.DEV)
+    KN.dense_step(Sg, mg, ag, bg, Ag, dg, ig, out, H)
+    torch.cuda.synchronize()
+    np.testing.assert_allclose(out.float().cpu().numpy(), o_ref, rtol=RT, atol=AT)
+    Sg = Sg.float().cpu().numpy()
+    if dtype == "bf16":                                  # 1 bf16 ulp of the element, or of 2^-8 of the state scale
+        assert np.all(np.abs(Sg - Sref) <= 2.0 ** -8 * np.maximum(np.abs(Sref), 0.02) + 1e-9)
+    else:
+        np.testing.assert_allclose(Sg, Sref, rtol=1e-5, atol=1e-7)
+
+
+def test_lowrank_matches_oracle():
+    from leapquant_amd import kernels as KN
+    rng = np.random.default_rng(800)
+    x = (0.02 * rng.standard_normal((6, 128, 128))).astype(np.float32)
+    x[2] += np.outer(rng.standard_normal(128), rng.standard_normal(128)).astype(np.float32) * 0.05
+    Q0 = O.make_q0(128, 4)
+    U_ref, Q_ref = O.lowrank(x, Q0, iters=3)
+    U, Q = KN.lowrank_factor(torch.from_numpy(x).to(G.DEV), 4, iters=3)
+    torch.cuda.synchronize()
+    U, Q = U.cpu().numpy(), Q.cpu().numpy()
+    assert np.linalg.norm(U - U_ref) <= 1e-3 * np.linalg.norm(U_ref)
+    assert np.linalg.norm(Q - Q_ref) <= 1e-3 * np.linalg.norm(Q_ref)
+
+
+def test_kda_round_trip_matches_oracle():
+    rng = np.random.default_rng(900)
+    NS, HV, H = 5, 4, 4
+    st, S, Q0 = make_state(rng, NS, HV, H, L=16, kda=True)
+    _prestep(rng, st, Q0, True, steps=12, NS=NS, HV=HV, H=H)
+    slots = np.array([1, 4], np.int64)
+    ssm, lq = G.to_gpu(st)
+    reb = O.kda_rebuild(st, slots)
+    lq.dequantize(ssm, torch.from_numpy(slots).to(G.DEV))
+    torch.cuda.synchronize()
+    for s in slots:
+        got = ssm[s].cpu().numpy()
+        assert np.abs(got - reb[s]).max() <= 1e-5 * np.abs(reb[s]).max()
+    # checkpoint of the rebuilt states
+    S_all = np.zeros((NS, HV, 128, 128), np.float32)
+    for s in slots:
+        S_all[s] = ssm[s].cpu().numpy()
+    O.kda_checkpoint(st, S_all, slots, Q0)
+    lq.quantize(ssm, torch.from_numpy(slots).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    for s in slots:
+        frac, mx = G.code_mismatch(g["Sq"][s], st["Sq"][s])
+        assert mx <= 1 and frac <= 1e-3, (s, frac, mx)
+        np.testing.assert_allclose(g["Sk"][s], st["Sk"][s], rtol=1e-4)
+    assert np.all(g["hcnt"][slots] == 0) and np.all(g["Pbuf"][slots] == 0)
+
+
+@pytest.mark.parametrize("name", ["oracle_gdn_L16", "oracle_gdn_L64", "oracle_kda_L16", "oracle_kda_L64"])
+def test_decode_trajectory_matches_golden(name):
+    """Full decode (step + flush every call) over the committed golden trajectories: every output within tolerance."""
+    import os
+    from tests.fixtures import from_bits, state_from_npz
+    z = from_bits(np.load(os.path.join(os.path.dirname(__file__), "golden", name + ".npz")))
+    st0 = state_from_npz(z, "init_")
+    NS, HV, H, K, V, L, R, kda = [int(x) for x in z["dims"]]
+    ssm, lq = G.to_gpu(st0, H=H)
+    A_log = torch.from_numpy(z["A_log"]).to(G.DEV)
+    dt_bias = torch.from_numpy(z["dt_bias"].reshape(-1)).to(G.DEV)
+    idx = torch.from_numpy(z["idx"].astype(np.int32)).to(G.DEV)
+    for t in range(z["mixed"].shape[0]):
+        mixed, a, b, _, _, _ = G.inputs_gpu(z["mixed"][t], z["a"][t], z["b"][t], z["A_log"], z["dt_bias"], z["idx"])
+        out = torch.empty(idx.shape[0], HV, V, dtype=torch.bfloat16, device=G.DEV)
+        lq.decode(ssm, mixed, a, b, A_log, dt_bias, idx, out)
+        torch.cuda.synchronize()
+        np.testing.assert_allclose(out.float().cpu().numpy(), z["o"][t], rtol=RT, atol=AT, err_msg="step %d" % t)
+    g = G.from_gpu(ssm, lq)
+    assert np.array_equal(g["hcnt"], z["final_hcnt"])
+    frac, mx = G.code_mismatch(g["Sq"], z["final_Sq"])
+    assert frac <= 1e-2, (frac, mx)
