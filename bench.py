@@ -1,0 +1,259 @@
+"""Benchmark of the INT8 GDN decode path on one MI355X.
+
+Workload (config 1): GDN layer, B = 64 rows, HV = 32 value heads sharing H = 16 key heads, K = V = 128, window W = 64,
+R = 4 Compensator Tokens, int8 state + fp32 scales; every call = decode step + end-of-window flush (the flush does work
+on one call in 64).  Synthetic inputs with the config-0 distributions (q, k ~ N(0,1) l2-normalised, v ~ N(0,1), log-gate
+g ~ U(-0.1, 0), beta = sigmoid(N(0,1)); states N(0, 0.02^2) quantised once), resident in HBM before timing.
+
+Measurement:
+  * `value` = amortised microseconds per decode call (step + flush, flushes included), from HIP events around graph
+    replays of the decode loop.  The loop rotates NSET disjoint slot sets (> 1 GB of state) so the 256 MB MALL
+    cannot hold the working set between uses of a set.
+  * roofline of the dominant kernel (the step): algorithmic bytes per launch (layout-independent minimum) over the
+    average launch duration, from HIP events around graphs of 64 back-to-back step launches.
+  * the same step on a dense bf16 state (`lq_dense_step`) as the baseline, and the CPU oracle on config 0.
+Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 128] [--no-cpu]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "int8 GDN/KDA decode-step µs + achieved HBM GB/s at B=64,H=32,d=128"
+HBM_PEAK_GBPS = 8000.0
+
+
+def step_bytes(N, HV, H, K, V, R, h, bits=8):
+    """Algorithmic bytes of one GDN step launch with h valid window entries per head (layout-independent minimum):
+    per value head codes, Sk/Sv, U^T|Q^T, v/o/u-append, scalars, buffered u_j and w_j; per key head q/k in, k append,
+    buffered k_j."""
+    return N * (HV * (V * K * bits // 8 + 4 * (K + V) + 2 * R * (K + V) + 6 * V + 20 + (2 * V + 4) * h)
+                + H * (6 * K + 2 * K * h))
+
+
+def flush_bytes(N, HV, H, K, V, R, W, bits=8):
+    """Algorithmic bytes of one flush launch on which every head of the N rows is due."""
+    return N * (HV * (2 * (V * K * bits // 8 + 4 * (K + V) + 2 * R * (K + V)) + W * (2 * V + 4)) + H * W * 2 * K)
+
+
+def dense_bytes(N, HV, H, K, V, elem=2):
+    return N * (HV * (2 * elem * V * K + 4 * V + 4) + H * 4 * K)
+
+
+def cpu_baseline(max_seconds=20.0):
+    """The CPU oracle (numpy, one thread) on config 0: GDN B=1, HV=H=16, d=128, W=64, R=4; steps until ~max_seconds
+    or 256 steps."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import lq_oracle as O
+    from tests.fixtures import gate_params, make_inputs, make_state
+    rng = np.random.default_rng(1000)
+    NS, HV, H, L = 2, 16, 16, 64
+    with threadpool_limits(limits=1):
+        st, S, Q0 = make_state(rng, NS, HV, H, L=L)
+        A_log, dt_bias = gate_params(HV)
+        idx = np.array([1])
+        pool = [make_inputs(rng, 1, HV, H) for _ in range(8)]
+        t0 = time.perf_counter()
+        n = 0
+        while n < 256:
+            mixed, a, b = pool[n % 8]
+            O.gdn_step(st, mixed, a, b, A_log, dt_bias, idx)
+            O.flush(st, Q0, idx)
+            n += 1
+            if time.perf_counter() - t0 > max_seconds and n % 64 == 0:
+                break
+        dt = time.perf_counter() - t0
+    return dict(value=round(dt / n * 1e6, 1), unit="us/step", cores=1, kind="port",
+                sample="config 0 (GDN B=1, HV=H=16, d=128, W=64, R=4): %d decode steps incl. %d flushes, numpy oracle, "
+                       "1 thread" % (n, n // 64))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1024)
+    ap.add_argument("--warmup", type=int, default=128)
+    ap.add_argument("--sets", type=int, default=8, help="disjoint slot sets rotated through (MALL defeat)")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-only", action="store_true", help="only the decode loop (for rocprofv3 runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path (the decode path shards heads across "
+              "GPUs with no exchange step; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from leapquant_amd import kernels as KN
+    from leapquant_amd.state import LeapQuantState
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, HV, H, K, V, L, R = 64, 32, 16, 128, 128, 64, 4
+    NSET = args.sets
+    NS = B * NSET + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1001)
+
+    # ---- state: N(0, 0.02^2) fp32 per head, quantised on the GPU ----
+    ssm = torch.empty(NS, HV, V, K, device=dev)
+    ssm.normal_(0.0, 0.02, generator=g)
+    lq = LeapQuantState(ssm, H, L=L, R=R)
+    all_slots = torch.arange(1, NS, device=dev, dtype=torch.int32)
+    lq.quantize(ssm, all_slots)
+    sets = [torch.arange(1 + B * k, 1 + B * (k + 1), device=dev, dtype=torch.int32) for k in range(NSET)]
+
+    # ---- input pool (config-0 distributions), resident in HBM ----
+    P = 16
+    pool = []
+    for _ in range(P):
+        q = torch.randn(B, H, K, device=dev, generator=g)
+        k = torch.randn(B, H, K, device=dev, generator=g)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn(B, HV, V, device=dev, generator=g)
+        mixed = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], 1).to(torch.bfloat16).contiguous()
+        gl = -0.1 * torch.rand(B, HV, device=dev, generator=g)
+        gl = gl.clamp(max=-1e-4)
+        a = torch.log(torch.expm1(-gl)).to(torch.bfloat16)
+        b = torch.randn(B, HV, device=dev, generator=g).to(torch.bfloat16)
+        pool.append((mixed, a, b))
+    A_log = torch.zeros(HV, device=dev)
+    dt_bias = torch.zeros(HV, device=dev)
+    out = torch.empty(B, HV, V, device=dev, dtype=torch.bfloat16)
+
+    def decode(s):
+        mixed, a, b = pool[s % P]
+        lq.decode(ssm, mixed, a, b, A_log, dt_bias, sets[s % NSET], out)
+
+    v = lq.views(ssm)
+
+    def step_only(s, kset):
+        mixed, a, b = pool[s % P]
+        lq.kstep(v["q32"], v["Sk"], v["Sv"], v["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.hcnt, mixed, a, b,
+                 A_log, dt_bias, v["uq"], sets[kset], out)
+
+    def flush_only(kset):
+        lq.kflush(v["q32"], v["Sk"], v["Sv"], v["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gd, lq.hcnt,
+                  v["sq16"], v["uq"], lq.Q0, sets[kset])
+
+    stream = torch.cuda.Stream()
+    torch.cuda.synchronize()
+
+    def capture(fn, n):
+        gr = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gr, stream=stream):
+            for i in range(n):
+                fn(i)
+        return gr
+
+    # ---- main loop: decode (step + flush) in graphs of 64 calls ----
+    CH = 64
+    # the graph's call i uses set i % NSET and input i % P; it is replayed as a block, so the rotation repeats
+    gdec = capture(decode, CH)
+    rem = args.steps % CH
+    grem = capture(decode, rem) if rem else None
+    torch.cuda.synchronize()                                      # capturing executes nothing
+    nw = -(-args.warmup // CH)
+    for _ in range(nw):
+        gdec.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(args.steps // CH):
+            gdec.replay()
+        if grem is not None:
+            grem.replay()
+        e1.record(stream)
+    e1.synchronize()
+    torch.cuda.synchronize()
+    ms_total = e0.elapsed_time(e1)
+    us_per_step = ms_total * 1e3 / args.steps
+    if args.profile_only:
+        print(json.dumps({"profile_only": True, "us_per_step": us_per_step}))
+        return
+
+    # ---- step-only and flush timings per set (fresh windows): graphs of 64 step launches, then the flush ----
+    lq.quantize(ssm, all_slots)                                   # every window back to h = 0
+    gsteps = [capture(lambda i, kk=kk: step_only(i, kk), CH) for kk in range(NSET)]
+    gflush = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
+    gidle = capture(lambda i: flush_only(0), CH)                  # 64 flush launches with no head due
+    torch.cuda.synchronize()
+    rounds = 3
+    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
+            torch.cuda.Event(enable_timing=True)) for _ in range(NSET)] for _ in range(rounds)]
+    with torch.cuda.stream(stream):
+        for r in range(rounds):
+            for kk in range(NSET):
+                a0, a1, a2 = ev[r][kk]
+                a0.record(stream)
+                gsteps[kk].replay()
+                a1.record(stream)
+                gflush[kk].replay()
+                a2.record(stream)
+        i0, i1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        i0.record(stream)
+        gidle.replay()
+        i1.record(stream)
+    torch.cuda.synchronize()
+    st_ms = [ev[r][kk][0].elapsed_time(ev[r][kk][1]) for r in range(1, rounds) for kk in range(NSET)]
+    fl_ms = [ev[r][kk][1].elapsed_time(ev[r][kk][2]) for r in range(1, rounds) for kk in range(NSET)]
+    step_us = sum(st_ms) / len(st_ms) * 1e3 / CH
+    flush_due_us = sum(fl_ms) / len(fl_ms) * 1e3
+    flush_idle_us = i0.elapsed_time(i1) * 1e3 / CH
+    bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(CH)) / CH      # mean over h = 0..63
+    bytes_flush = flush_bytes(B, HV, H, K, V, R, L)
+    achieved = bytes_step / (step_us * 1e-6) / 1e9
+    amort_bytes = bytes_step + bytes_flush / L
+
+    # ---- bf16-state baseline (same step on a dense bf16 state), rotated sets ----
+    del gsteps, gflush, gidle, gdec, grem
+    Sd = torch.empty(NS, HV, V, K, device=dev, dtype=torch.bfloat16)
+    Sd.normal_(0.0, 0.02, generator=g)
+
+    def dense(i):
+        mixed, a, b = pool[i % P]
+        KN.dense_step(Sd, mixed, a, b, A_log, dt_bias, sets[i % NSET], out, H)
+
+    gd = capture(dense, CH)
+    gd.replay()
+    torch.cuda.synchronize()
+    d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        d0.record(stream)
+        for _ in range(4):
+            gd.replay()
+        d1.record(stream)
+    torch.cuda.synchronize()
+    bf16_us = d0.elapsed_time(d1) * 1e3 / (4 * CH)
+    bf16_gbps = dense_bytes(B, HV, H, K, V) / (bf16_us * 1e-6) / 1e9
+    del gd, Sd
+
+    res = {
+        "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
+        "warmup": nw * CH, "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "vs_baseline": None, "dtype": "int8", "data": "synthetic",
+        "config": {"workload": "GDN decode, BASELINE config 1: B=64, HV=32 value / H=16 key heads, d=128, W=64, R=4, "
+                               "int8 state + fp32 scales, step + flush per call, %d rotated slot sets" % NSET,
+                   "batch": B, "value_heads": HV, "key_heads": H, "head_dim": K, "window": L, "rank": R},
+        "achieved_gbps": round(amort_bytes / (us_per_step * 1e-6) / 1e9, 1),
+        "step_us": round(step_us, 3), "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
+        "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
+        "speedup_vs_bf16_step": round(bf16_us / step_us, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "gdn_step_kernel<2>", "bytes_per_launch": int(bytes_step)},
+    }
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

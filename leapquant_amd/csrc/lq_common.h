@@ -93,6 +93,20 @@ __device__ __forceinline__ float beta_of(float b) {
 }
 __device__ __forceinline__ float rsqrt_rn(double x) { return (float)(1.0 / sqrt(x)); }
 
+// fp32 versions for the per-(row, head) and per-channel gates of the decode steps (<= 2 ulp of the fp64 forms)
+__device__ __forceinline__ float softplus20f(float x) { return x <= (float)LQ_SOFTPLUS_THRESHOLD ? log1pf(expf(x)) : x; }
+__device__ __forceinline__ float gdn_alpha_f(float a, float dtb, float alog) {
+  return expf(-expf(alog) * softplus20f(a + dtb));
+}
+__device__ __forceinline__ float beta_f(float b) { return bfround(1.0f / (1.0f + expf(-b))); }
+__device__ __forceinline__ float rsqrtf_rn(float x) { return 1.0f / sqrtf(x); }
+
+// ---- direct global -> LDS loads (gfx950 global_load_lds_dwordx4): lane l's 16 bytes land at lds_wave_base + 16 l ----
+__device__ __forceinline__ void lds_load16(const void* gsrc, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------
 struct Block {
   const int8_t* Sq;   // [V][K]

@@ -48,24 +48,39 @@ __device__ __forceinline__ void dot16_i8(uint4 w, const float* kf, const float* 
   }
 }
 
+template <int G>
 struct StepShared {
-  float2 dkq[LMAX];        // (dk_j, dq_j): buffered key j against kn / qn (GDN: shared by the key head)
-  float2 duq[4][4];        // (dU_r, dQ_r) per value head g, factor r
-  float w[4][LMAX];        // gated entry weights w_j per value head
+  bf16_t ub[G][LMAX][VD];  // the window's u_j rows per value head (staged by direct global -> LDS loads)
+  f16_t uq[G][4][KD + VD]; // U^T | Q^T per value head
+  float2 dkq[LMAX];        // (dk_j, dq_j): buffered key j against kn / qn (shared by the key head)
+  float2 duq[G][4];        // (dU_r, dQ_r) per value head g, factor r
+  float w[G][LMAX];        // gated entry weights w_j per value head
+  float4 kn[KD / 4];       // normalised key and query (not kept in registers across the tile stream)
+  float4 qn[KD / 4];
 };
 
 // ------------------------------------------------------------------------------------------------------------------
 // GDN step  (kernels.py:129-144 gate / beta, 236-279 norms and weights, 380-585 stream, dots and appends)
+//
+// Per workgroup (row n, key head hk), 128 threads per value head g.  Order of the memory traffic:
+//   idx -> {int8 tile (registers), hcnt} -> {u_j rows and U^T|Q^T (direct to LDS), scales, q, k, v}
+//   -> GEMV on the tile -> barrier -> buffered keys k_j (registers) against kn / qn -> barrier -> per-row output.
+// At <= 128 VGPRs four 256-thread workgroups fit on a CU, so the whole B = 64 x H = 16 grid is resident at once.
 // ------------------------------------------------------------------------------------------------------------------
 template <int G>
-__global__ __launch_bounds__(128 * G) void gdn_step_kernel(lq_state st, lq_step_io io) {
-  __shared__ StepShared sh;
+__global__ __launch_bounds__(128 * G) __attribute__((amdgpu_waves_per_eu(4)))
+void gdn_step_kernel(lq_state st, lq_step_io io) {
+  __shared__ StepShared<G> sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
   const int hk = blockIdx.x - n * H;
   const int tid = threadIdx.x;
-  const int g = tid >> 7;       // value head of this thread within the key head
+  // value head of this thread within the key head: wave-uniform, so per-head scalars come through scalar loads that
+  // do not wait behind the tile's vector loads
+  const int g = __builtin_amdgcn_readfirstlane(tid >> 7);
   const int lt = tid & 127;     // thread within the value head
+  const int wi = __builtin_amdgcn_readfirstlane(lt >> 6);   // wave within the value head
+  const int lane = tid & 63;
   const int rg = lt >> 3;       // row group: rows 8 rg .. 8 rg + 7 of the int8 tile
   const int cc = lt & 7;        // column chunk: columns 16 cc .. 16 cc + 15
   const int hv = hk * G + g;
@@ -77,21 +92,31 @@ __global__ __launch_bounds__(128 * G) void gdn_step_kernel(lq_state st, lq_step_
     out[lt] = 0;
     return;
   }
-  const long long sh_ = (long long)slot * HV + hv;
-  const int h = st.hcnt[sh_];
-  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
-
-  // ---- loads: the int8 tile first (the long pole), then the small operands ----
   const char* base = block_base(st, slot, hv);
-  uint4 code[8];
+  uint4 code[8];                // the int8 tile first: the long pole
   {
     const uint4* cp = (const uint4*)base + (8 * rg) * 8 + cc;
 #pragma unroll
     for (int i = 0; i < 8; ++i) code[i] = cp[i * 8];
   }
+  const long long sh_ = (long long)slot * HV + hv;
+  const int h = st.hcnt[sh_];
+  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
+  int hmax = h;
+#pragma unroll
+  for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, (int)st.hcnt[(long long)slot * HV + hk * G + g2]);
+  hmax = min(hmax, L);
+
+  // ---- window values u_j (j < h) and the factors straight to LDS, 1 KiB per wave instruction ----
+  {
+    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
+    const int nch = live ? (h + 3) >> 2 : 0;      // 4 rows of 256 B per chunk; chunk rows >= h are never read
+    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
+    const char* uqg = base + VD * KD + 4 * (KD + VD);
+    lds_load16(uqg + wi * 1024 + 16 * lane, (char*)&sh.uq[g][0][0] + wi * 1024);
+  }
   const float* Skp = (const float*)(base + VD * KD);
   const float* Svp = Skp + KD;
-  const f16_t* UQp = (const f16_t*)(Svp + VD);
   float sk[16];
   {
     const float4* p = (const float4*)(Skp + 16 * cc);
@@ -112,8 +137,8 @@ __global__ __launch_bounds__(128 * G) void gdn_step_kernel(lq_state st, lq_step_
   const float vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
   const float P = st.Pbuf[sh_];
-  const float alpha = gdn_alpha(bf2f(((const bf16_t*)io.a)[(long long)n * HV + hv]), io.dt_bias[hv], io.A_log[hv]);
-  const float beta = beta_of(bf2f(((const bf16_t*)io.b)[(long long)n * HV + hv]));
+  const float alpha = gdn_alpha_f(bf2f(((const bf16_t*)io.a)[(long long)n * HV + hv]), io.dt_bias[hv], io.A_log[hv]);
+  const float beta = beta_f(bf2f(((const bf16_t*)io.b)[(long long)n * HV + hv]));
   float* Wp = st.Wbuf + sh_ * L;
   float wmine = 0.f;
   if (live && lt < h) {         // w_j = Wbuf[j] alpha for the live entries (kernels.py:270-274)
@@ -130,70 +155,98 @@ __global__ __launch_bounds__(128 * G) void gdn_step_kernel(lq_state st, lq_step_
     nkq = fmaf(kv[i], qv[i], nkq);
   }
   nq = sum8(nq); nk = sum8(nk); nkq = sum8(nkq);
-  const float inq = rsqrt_rn((double)nq + LQ_NORM_EPS) * io.scale;
-  const float ink = rsqrt_rn((double)nk + LQ_NORM_EPS);
+  const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
+  const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
   const float kappa = nkq * inq * ink;
-  float kn[16], qn[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) { kn[i] = kv[i] * ink; qn[i] = qv[i] * inq; }
-
-  // ---- buffer dots (shared per key head) and factor dots (per value head), one 8-lane group per row ----
-  int hmax = h;
-#pragma unroll
-  for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, (int)st.hcnt[(long long)slot * HV + hk * G + g2]);
-  hmax = min(hmax, L);
+  // ---- checkpoint stream: m = deq(Sq) kn, y = deq(Sq) qn with kf = kn Sk / 127 (kernels.py:255-256) ----
+  float mq = 0.f, yq = 0.f;     // this lane keeps row 8 rg + cc = lt
   {
-    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
-    const int ntask = hmax + G * R;
-    for (int t = g * 16 + rg; t < ntask; t += 16 * G) {
-      float x[16];
-      if (t < hmax) {
-        const uint4* p = (const uint4*)(Kb + (long long)t * KD + 16 * cc);
-        unpack8(p[0], x); unpack8(p[1], x + 8);
-      } else {
-        const int tt = t - hmax, g2 = tt / R, r = tt - g2 * R;
-        const f16_t* U = (const f16_t*)(block_base(st, slot, hk * G + g2) + VD * KD + 4 * (KD + VD)) + r * (KD + VD);
-        const uint4* p = (const uint4*)(U + 16 * cc);
-        unpack8h(p[0], x); unpack8h(p[1], x + 8);
-      }
-      float dk = 0.f, dq = 0.f;
+    float kn[16], qn[16];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) { dk = fmaf(x[i], kn[i], dk); dq = fmaf(x[i], qn[i], dq); }
-      dk = sum8(dk); dq = sum8(dq);
-      if (cc == 0) {
-        if (t < hmax) sh.dkq[t] = make_float2(dk, dq);
-        else { const int tt = t - hmax; sh.duq[tt / R][tt % R] = make_float2(dk, dq); }
+    for (int i = 0; i < 16; ++i) { kn[i] = kv[i] * ink; qn[i] = qv[i] * inq; }
+    if (tid < 8) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        sh.kn[4 * cc + i] = make_float4(kn[4 * i], kn[4 * i + 1], kn[4 * i + 2], kn[4 * i + 3]);
+        sh.qn[4 * cc + i] = make_float4(qn[4 * i], qn[4 * i + 1], qn[4 * i + 2], qn[4 * i + 3]);
       }
     }
+    float kf[16], qf[16];
+    const float inv = 1.0f / LQ_QMAX;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { kf[i] = (kn[i] * sk[i]) * inv; qf[i] = (qn[i] * sk[i]) * inv; }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      float m = 0.f, y = 0.f;
+      dot16_i8(code[i], kf, qf, m, y);
+      m = sum8(m);
+      y = sum8(y);
+      if (cc == i) { mq = m; yq = y; }
+    }
   }
-
-  // ---- checkpoint stream: m = deq(Sq) kn, y = deq(Sq) qn with kf = kn Sk / 127 (kernels.py:255-256) ----
-  float kf[16], qf[16];
-  const float inv = 1.0f / LQ_QMAX;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) { kf[i] = (kn[i] * sk[i]) * inv; qf[i] = (qn[i] * sk[i]) * inv; }
-  float mrow_[8], yrow_[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float m = 0.f, y = 0.f;
-    dot16_i8(code[i], kf, qf, m, y);
-    mrow_[i] = sum8(m);
-    yrow_[i] = sum8(y);
-  }
-  float mq = mrow_[0], yq = yrow_[0];     // this lane keeps row 8 rg + cc = lt
-#pragma unroll
-  for (int i = 1; i < 8; ++i) { if (cc == i) { mq = mrow_[i]; yq = yrow_[i]; } }
   mq *= sv;
   yq *= sv;
 
+  wait_vm();
+  __syncthreads();              // u_j rows, factors and w_j are in LDS
+
+  // ---- buffered-key dots (once per key head) and factor dots (per value head), one 8-lane group per row ----
+  {
+    float kn[16], qn[16];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float4 a = sh.kn[4 * cc + i], b = sh.qn[4 * cc + i];
+      kn[4 * i] = a.x; kn[4 * i + 1] = a.y; kn[4 * i + 2] = a.z; kn[4 * i + 3] = a.w;
+      qn[4 * i] = b.x; qn[4 * i + 1] = b.y; qn[4 * i + 2] = b.z; qn[4 * i + 3] = b.w;
+    }
+    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
+    constexpr int MAXT = (LMAX + 4 * G + 16 * G - 1) / (16 * G);
+    const int ntask = hmax + G * R;
+    const int t0 = g * 16 + rg;
+    constexpr int PF = MAXT < 3 ? MAXT : 3;     // rows prefetched per batch
+#pragma unroll
+    for (int i0 = 0; i0 < MAXT; i0 += PF) {
+    uint4 kw[PF][2];
+#pragma unroll
+    for (int i = i0; i < i0 + PF && i < MAXT; ++i) {
+      const int t = t0 + 16 * G * i;
+      if (t < hmax) {
+        const uint4* p = (const uint4*)(Kb + (long long)t * KD + 16 * cc);
+        kw[i - i0][0] = p[0];
+        kw[i - i0][1] = p[1];
+      }
+    }
+#pragma unroll
+    for (int i = i0; i < i0 + PF && i < MAXT; ++i) {
+      const int t = t0 + 16 * G * i;
+      if (t < ntask) {
+        float x[16];
+        if (t < hmax) {
+          unpack8(kw[i - i0][0], x); unpack8(kw[i - i0][1], x + 8);
+        } else {
+          const int tt = t - hmax, g2 = tt / R, r = tt - g2 * R;
+          const uint4* p = (const uint4*)(&sh.uq[g2][r][16 * cc]);
+          unpack8h(p[0], x); unpack8h(p[1], x + 8);
+        }
+        float dk = 0.f, dq = 0.f;
+#pragma unroll
+        for (int e = 0; e < 16; ++e) { dk = fmaf(x[e], kn[e], dk); dq = fmaf(x[e], qn[e], dq); }
+        dk = sum8(dk); dq = sum8(dq);
+        if (cc == 0) {
+          if (t < hmax) sh.dkq[t] = make_float2(dk, dq);
+          else { const int tt = t - hmax; sh.duq[tt / R][tt % R] = make_float2(dk, dq); }
+        }
+      }
+    }
+    }
+  }
   __syncthreads();
   if (!live) { out[lt] = 0; return; }
 
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
-  const bf16_t* Ub = (const bf16_t*)st.Ubuf + sh_ * L * VD + lt;
   float a4 = 0.f, a5 = 0.f;
   for (int j = 0; j < h; ++j) {
-    const float ub = bf2f(Ub[(long long)j * VD]);
+    const float ub = bf2f(sh.ub[g][j][lt]);
     const float wj = sh.w[g][j];
     const float2 d = sh.dkq[j];
     a4 = fmaf(ub, wj * d.x, a4);
@@ -201,7 +254,7 @@ __global__ __launch_bounds__(128 * G) void gdn_step_kernel(lq_state st, lq_step_
   }
   float a6 = 0.f, a7 = 0.f;
   for (int r = 0; r < R; ++r) {
-    const float qt = h2f(UQp[r * (KD + VD) + KD + lt]);
+    const float qt = h2f(sh.uq[g][r][KD + lt]);
     const float2 d = sh.duq[g][r];
     a6 = fmaf(qt, d.x, a6);
     a7 = fmaf(qt, d.y, a7);
