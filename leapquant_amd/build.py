@@ -27,7 +27,7 @@ def hipcc():
 def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     cc = hipcc()
-    flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
+    flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-inline-asm",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
     objs = []
     for s in SOURCES:

@@ -19,10 +19,9 @@ __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint3
 
 // fp32 -> bf16, round to nearest even (NaN kept quiet)
 __device__ __forceinline__ bf16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (bf16_t)((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (bf16_t)(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  return (bf16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r);   // branch-free
 }
 __device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
 
@@ -94,7 +93,11 @@ __device__ __forceinline__ float beta_of(float b) {
 __device__ __forceinline__ float rsqrt_rn(double x) { return (float)(1.0 / sqrt(x)); }
 
 // fp32 versions for the per-(row, head) and per-channel gates of the decode steps (<= 2 ulp of the fp64 forms)
-__device__ __forceinline__ float softplus20f(float x) { return x <= (float)LQ_SOFTPLUS_THRESHOLD ? log1pf(expf(x)) : x; }
+// branch-free (a branch here makes the compiler's wait-count analysis wait for every load in flight at the join)
+__device__ __forceinline__ float softplus20f(float x) {
+  const float t = log1pf(expf(fminf(x, (float)LQ_SOFTPLUS_THRESHOLD)));
+  return x <= (float)LQ_SOFTPLUS_THRESHOLD ? t : x;
+}
 __device__ __forceinline__ float gdn_alpha_f(float a, float dtb, float alog) {
   return expf(-expf(alog) * softplus20f(a + dtb));
 }
@@ -102,9 +105,16 @@ __device__ __forceinline__ float beta_f(float b) { return bfround(1.0f / (1.0f +
 __device__ __forceinline__ float rsqrtf_rn(float x) { return 1.0f / sqrtf(x); }
 
 // ---- direct global -> LDS loads (gfx950 global_load_lds_dwordx4): lane l's 16 bytes land at lds_wave_base + 16 l ----
+// Issued through inline asm: the compiler's own form makes every such load wait for all loads in flight (it cannot
+// tell that successive loads write disjoint LDS).  The caller waits (s_waitcnt vmcnt(0)) before reading the LDS data.
+// Nothing else in these kernels keeps a value in M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gsrc, (__attribute__((address_space(3))) void*)lds_wave_base, 16, 0, 0);
+  const unsigned lds = (unsigned)(size_t)(__attribute__((address_space(3))) char*)(char*)lds_wave_base;
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gsrc), "s"(lds) : "memory", "m0");
 }
+#pragma clang diagnostic pop
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------

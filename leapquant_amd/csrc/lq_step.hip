@@ -48,24 +48,61 @@ __device__ __forceinline__ void dot16_i8(uint4 w, const float* kf, const float* 
   }
 }
 
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// kf / qf as three signed int8 digits of a 24-bit fixed-point value relative to the vector's max:
+// X = rint(x / max * 127 * 2^16) = d0 2^16 + d1 2^8 + d2, |d0| <= 127, d1, d2 in [-128, 127].
+constexpr float DIGIT_SCALE = 127.0f * 65536.0f;
+__device__ __forceinline__ void digits3(float x, float rmax, int8_t& d0, int8_t& d1, int8_t& d2) {
+  const int X = (int)rintf((x * rmax) * DIGIT_SCALE);
+  const int e2 = (int)(int8_t)(X & 0xff);
+  const int X1 = (X - e2) >> 8;
+  const int e1 = (int)(int8_t)(X1 & 0xff);
+  d0 = (int8_t)((X1 - e1) >> 8);
+  d1 = (int8_t)e1;
+  d2 = (int8_t)e2;
+}
+// DPP row shifts (within 16 lanes): lane i reads lane i - s
+template <int S>
+__device__ __forceinline__ float row_shr(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x110 + S, 0xf, 0xf, false));
+}
+// DPP quad broadcast of lane k of each quad
+template <int K>
+__device__ __forceinline__ float quad_bcast(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), K * 0x55, 0xf, 0xf, false));
+}
+constexpr float KSPLIT = 64.0f;   // kn / qn scaled by 2^6 before the fp16 hi / lo split (keeps the lo part normal)
+
 template <int G>
 struct StepShared {
-  bf16_t ub[G][LMAX][VD];  // the window's u_j rows per value head (staged by direct global -> LDS loads)
-  f16_t uq[G][4][KD + VD]; // U^T | Q^T per value head
-  float2 dkq[LMAX];        // (dk_j, dq_j): buffered key j against kn / qn (shared by the key head)
-  float2 duq[G][4];        // (dU_r, dQ_r) per value head g, factor r
+  bf16_t ub[G][LMAX][VD];  // the window's u_j rows per value head (direct global -> LDS loads)
+  int8_t dig[G][6][KD];    // int8 GEMV B operand: k digits 0-2, q digits 0-2
+  bf16_t bkq[6][KD];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
+  f16_t hkq[4][KD];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
+  float2 mq[G][VD];        // GEMV rows (k, q) in digit units
+  float2 dkq[LMAX];        // (dk_j, dq_j) of buffered key j (shared by the key head)
+  float2 duq[G][4];        // (dU_r, dQ_r) per value head, factor r
   float w[G][LMAX];        // gated entry weights w_j per value head
-  float4 kn[KD / 4];       // normalised key and query (not kept in registers across the tile stream)
-  float4 qn[KD / 4];
+  float sc[G][8];          // per value head: alpha, beta, kappa, kmax, qmax
 };
 
 // ------------------------------------------------------------------------------------------------------------------
 // GDN step  (kernels.py:129-144 gate / beta, 236-279 norms and weights, 380-585 stream, dots and appends)
 //
-// Per workgroup (row n, key head hk), 128 threads per value head g.  Order of the memory traffic:
-//   idx -> {int8 tile (registers), hcnt} -> {u_j rows and U^T|Q^T (direct to LDS), scales, q, k, v}
-//   -> GEMV on the tile -> barrier -> buffered keys k_j (registers) against kn / qn -> barrier -> per-row output.
-// At <= 128 VGPRs four 256-thread workgroups fit on a CU, so the whole B = 64 x H = 16 grid is resident at once.
+// One workgroup per (row n, key head hk) with 2 waves per value head g; wave (g, wi) owns tile rows 64 wi .. 64 wi + 63.
+// Every dot product runs on the matrix cores:
+//   * m = deq(Sq) kn, y = deq(Sq) qn: the int8 tile goes from HBM straight into the A operand of
+//     v_mfma_i32_16x16x64_i8; B holds kf = kn Sk / 127 and qf = qn Sk / 127 as three int8 digits each (24-bit fixed
+//     point relative to max |kf|, max |qf|), so both GEMVs accumulate exactly in int32;
+//   * dk_j = K_j kn, dq_j = K_j qn: bf16 MFMA with kn, qn split in three bf16 terms (products exact, fp32 sums);
+//   * dU_r = U^T_r kn, dQ_r = U^T_r qn: fp16 MFMA with 64 kn, 64 qn split in two fp16 terms.
+// The per-head scalar work (norms, gate, beta, digits) runs in one wave per value head.  The window's u_j rows reach
+// LDS by direct global -> LDS loads.  <= 128 VGPRs and < 40 KiB LDS: four workgroups per CU, the whole B = 64 x H = 16
+// grid resident at once.
 // ------------------------------------------------------------------------------------------------------------------
 template <int G>
 __global__ __launch_bounds__(128 * G) __attribute__((amdgpu_waves_per_eu(4)))
@@ -75,14 +112,12 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   const int n = blockIdx.x / H;
   const int hk = blockIdx.x - n * H;
   const int tid = threadIdx.x;
-  // value head of this thread within the key head: wave-uniform, so per-head scalars come through scalar loads that
-  // do not wait behind the tile's vector loads
-  const int g = __builtin_amdgcn_readfirstlane(tid >> 7);
-  const int lt = tid & 127;     // thread within the value head
-  const int wi = __builtin_amdgcn_readfirstlane(lt >> 6);   // wave within the value head
+  const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave in the workgroup
+  const int g = wv >> 1;        // value head of this wave within the key head
+  const int wi = wv & 1;        // its tile half: rows 64 wi ..
+  const int lt = tid & 127;     // thread within the value head (the row it owns in the output phase)
   const int lane = tid & 63;
-  const int rg = lt >> 3;       // row group: rows 8 rg .. 8 rg + 7 of the int8 tile
-  const int cc = lt & 7;        // column chunk: columns 16 cc .. 16 cc + 15
+  const int n16 = lane & 15, q4 = lane >> 4;                 // MFMA lane coordinates
   const int hv = hk * G + g;
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
@@ -92,13 +127,15 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     out[lt] = 0;
     return;
   }
+  // Every load below is unconditional (clamped addresses) and none sits in a divergent block: a load whose result is
+  // merged at the end of an exec-masked block makes the compiler wait for ALL loads in flight, the tile included.
+  // Order: the scalar work's operands, then the int8 tile, then the window.  Loads return in order, so the per-head
+  // scalar work overlaps the tile's transfer.
   const char* base = block_base(st, slot, hv);
-  uint4 code[8];                // the int8 tile first: the long pole
-  {
-    const uint4* cp = (const uint4*)base + (8 * rg) * 8 + cc;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = cp[i * 8];
-  }
+  const float* Skp = (const float*)(base + VD * KD);
+  const float* Svp = Skp + KD;
+  const f16_t* UQp = (const f16_t*)(Svp + VD);
+  const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   const long long sh_ = (long long)slot * HV + hv;
   const int h = st.hcnt[sh_];
   const bool live = h < L;      // a full window is never stepped (the flush follows every step)
@@ -106,144 +143,213 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
 #pragma unroll
   for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, (int)st.hcnt[(long long)slot * HV + hk * G + g2]);
   hmax = min(hmax, L);
-
-  // ---- window values u_j (j < h) and the factors straight to LDS, 1 KiB per wave instruction ----
-  {
-    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
-    const int nch = live ? (h + 3) >> 2 : 0;      // 4 rows of 256 B per chunk; chunk rows >= h are never read
-    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
-    const char* uqg = base + VD * KD + 4 * (KD + VD);
-    lds_load16(uqg + wi * 1024 + 16 * lane, (char*)&sh.uq[g][0][0] + wi * 1024);
-  }
-  const float* Skp = (const float*)(base + VD * KD);
-  const float* Svp = Skp + KD;
-  float sk[16];
-  {
-    const float4* p = (const float4*)(Skp + 16 * cc);
+  float* Wp = st.Wbuf + sh_ * L;
+  bf16_t kxr[2], qxr[2];
+  float skx[2], wx[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float4 t = p[i];
-      sk[4 * i] = t.x; sk[4 * i + 1] = t.y; sk[4 * i + 2] = t.z; sk[4 * i + 3] = t.w;
+  for (int e = 0; e < 2; ++e) {
+    const int c = lane + 64 * e;
+    kxr[e] = mrow[H * KD + hk * KD + c];
+    qxr[e] = mrow[hk * KD + c];
+    skx[e] = Skp[c];
+    wx[e] = Wp[min(c, L - 1)];
+  }
+  const bf16_t araw = ((const bf16_t*)io.a)[(long long)n * HV + hv];
+  const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
+  const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
+  __builtin_amdgcn_sched_barrier(0);   // keep the loads above ahead of the tile in issue order
+  i32x4 afr[4][2];              // the int8 tile (the long pole): A fragments, row 64 wi + 16 rt + n16
+  {
+    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+  }
+  // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
+  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
+  bf16x8 kfr[KT][4];
+  {
+    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int j = 16 * (wv + 2 * G * t) + n16;
+      const int jr = j < hmax ? j : 0;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
     }
   }
-  const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
-  float qv[16], kv[16];
+  // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA (last wave)
+  f16x8 ufr[4];
+  const bool fwave = wv == 2 * G - 1;
   {
-    const uint4* qp = (const uint4*)(mrow + hk * KD + 16 * cc);
-    const uint4* kp = (const uint4*)(mrow + H * KD + hk * KD + 16 * cc);
-    unpack8(qp[0], qv); unpack8(qp[1], qv + 8);
-    unpack8(kp[0], kv); unpack8(kp[1], kv + 8);
+    const int m = n16 < G * R ? n16 : 0, g2 = m / R, r = m - g2 * R;
+    const f16_t* U = (const f16_t*)(block_base(st, slot, hk * G + g2) + VD * KD + 4 * (KD + VD)) + r * (KD + VD);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
   }
   const float vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
+  float qt[4];                  // Q^T[r][lt]
+#pragma unroll
+  for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   const float P = st.Pbuf[sh_];
-  const float alpha = gdn_alpha_f(bf2f(((const bf16_t*)io.a)[(long long)n * HV + hv]), io.dt_bias[hv], io.A_log[hv]);
-  const float beta = beta_f(bf2f(((const bf16_t*)io.b)[(long long)n * HV + hv]));
-  float* Wp = st.Wbuf + sh_ * L;
-  float wmine = 0.f;
-  if (live && lt < h) {         // w_j = Wbuf[j] alpha for the live entries (kernels.py:270-274)
-    wmine = Wp[lt] * alpha;
-    sh.w[g][lt] = wmine;
+
+  // ---- per value head scalar work, one wave (wi = 0): gate, beta, norms, digits, key-dot operands ----
+  if (wi == 0) {
+    const float alpha = gdn_alpha_f(bf2f(araw), dtb, alog);
+    const float beta = beta_f(bf2f(braw));
+    const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
+    float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
+    nq = fmaf(qx[1], qx[1], nq); nk = fmaf(kx[1], kx[1], nk); nkq = fmaf(kx[1], qx[1], nkq);
+    nq = sum64(nq); nk = sum64(nk); nkq = sum64(nkq);
+    const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
+    const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
+    const float kappa = nkq * inq * ink;
+    const float inv = 1.0f / LQ_QMAX;
+    float kn[2], qn[2], kf[2], qf[2];
+    float kmax = 0.f, qmax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      kn[e] = kx[e] * ink;
+      qn[e] = qx[e] * inq;
+      kf[e] = (kn[e] * skx[e]) * inv;          // kernels.py:255-256
+      qf[e] = (qn[e] * skx[e]) * inv;
+      kmax = fmaxf(kmax, fabsf(kf[e]));
+      qmax = fmaxf(qmax, fabsf(qf[e]));
+    }
+    kmax = fmaxf(max64(kmax), 1e-30f);
+    qmax = fmaxf(max64(qmax), 1e-30f);
+    const float rk = 1.0f / kmax, rq = 1.0f / qmax;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = lane + 64 * e;
+      int8_t d0, d1, d2;
+      digits3(kf[e], rk, d0, d1, d2);
+      sh.dig[g][0][c] = d0; sh.dig[g][1][c] = d1; sh.dig[g][2][c] = d2;
+      digits3(qf[e], rq, d0, d1, d2);
+      sh.dig[g][3][c] = d0; sh.dig[g][4][c] = d1; sh.dig[g][5][c] = d2;
+      if (g == 0) {
+        // key-dot operands: x = hi + mid + lo exactly representable sums of bf16 (products with bf16 keys exact)
+        const float xs[2] = {kn[e], qn[e]};
+#pragma unroll
+        for (int v2 = 0; v2 < 2; ++v2) {
+          const float x = xs[v2];
+          const bf16_t hi = f2bf(x);
+          const float r1 = x - bf2f(hi);
+          const bf16_t mid = f2bf(r1);
+          const bf16_t lo = f2bf(r1 - bf2f(mid));
+          sh.bkq[3 * v2][c] = hi; sh.bkq[3 * v2 + 1][c] = mid; sh.bkq[3 * v2 + 2][c] = lo;
+          const float xs64 = x * KSPLIT;
+          const f16_t fh = f2h(xs64);
+          sh.hkq[2 * v2][c] = fh;
+          sh.hkq[2 * v2 + 1][c] = f2h(xs64 - h2f(fh));
+        }
+        if (live) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + c] = f2bf(kn[e]);   // key append
+      }
+      const float wj = wx[e] * alpha;
+      if (live && c < h) {      // w_j = Wbuf[j] alpha (kernels.py:270-274), written back in place
+        sh.w[g][c] = wj;
+        Wp[c] = wj;
+      }
+    }
+    if (lane == 0) {
+      sh.sc[g][0] = alpha; sh.sc[g][1] = beta; sh.sc[g][2] = kappa; sh.sc[g][3] = kmax; sh.sc[g][4] = qmax;
+    }
   }
 
-  // ---- l2 norms of q and k: every 8-lane row group holds the whole vectors (16 columns per lane) ----
-  float nq = 0.f, nk = 0.f, nkq = 0.f;
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    nq = fmaf(qv[i], qv[i], nq);
-    nk = fmaf(kv[i], kv[i], nk);
-    nkq = fmaf(kv[i], qv[i], nkq);
-  }
-  nq = sum8(nq); nk = sum8(nk); nkq = sum8(nkq);
-  const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
-  const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
-  const float kappa = nkq * inq * ink;
-  // ---- checkpoint stream: m = deq(Sq) kn, y = deq(Sq) qn with kf = kn Sk / 127 (kernels.py:255-256) ----
-  float mq = 0.f, yq = 0.f;     // this lane keeps row 8 rg + cc = lt
+  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction.  Straight-line code (a load loop
+  // makes the compiler wait for every load in flight): chunks past the window re-read chunk 0 (an L2 hit) into LDS
+  // rows >= h, which are never read.
   {
-    float kn[16], qn[16];
+    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
+    const int nch = live ? (h + 3) >> 2 : 0;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) { kn[i] = kv[i] * ink; qn[i] = qv[i] * inq; }
-    if (tid < 8) {
+    for (int i = 0; i < LMAX / 8; ++i) {
+      const int c = wi + 2 * i;
+      if (4 * c < L) lds_load16(ubg + (c < nch ? c : 0) * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
+    }
+  }
+  wait_vm();
+  __syncthreads();              // digits, dot operands, scalars, u_j rows and w_j are in LDS
+
+  // ---- int8 GEMV on the matrix cores.  B columns: 0 / 4 / 8 = k digits 0 / 1 / 2, 1 / 5 / 9 = q digits, others 0 ----
+  {
+    i32x4 bfr[2];
+    const int drow = (n16 & 3) * 3 + (n16 >> 2);              // table row of column n16 (valid for n16 < 10, n16 & 3 < 2)
+    const bool bcol = (n16 & 3) < 2 && n16 < 10;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const i32x4 b = *(const i32x4*)&sh.dig[g][bcol ? drow : 0][64 * ks + 16 * q4];
+      bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      i32x4 acc = {0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][0], bfr[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][1], bfr[1], acc, 0, 0, 0);
+      // lane (n16, q4) holds rows 64 wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        sh.kn[4 * cc + i] = make_float4(kn[4 * i], kn[4 * i + 1], kn[4 * i + 2], kn[4 * i + 3]);
-        sh.qn[4 * cc + i] = make_float4(qn[4 * i], qn[4 * i + 1], qn[4 * i + 2], qn[4 * i + 3]);
+        const float c0 = (float)acc[i];
+        const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
+        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[g][64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
       }
-    }
-    float kf[16], qf[16];
-    const float inv = 1.0f / LQ_QMAX;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { kf[i] = (kn[i] * sk[i]) * inv; qf[i] = (qn[i] * sk[i]) * inv; }
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      float m = 0.f, y = 0.f;
-      dot16_i8(code[i], kf, qf, m, y);
-      m = sum8(m);
-      y = sum8(y);
-      if (cc == i) { mq = m; yq = y; }
     }
   }
-  mq *= sv;
-  yq *= sv;
-
-  wait_vm();
-  __syncthreads();              // u_j rows, factors and w_j are in LDS
-
-  // ---- buffered-key dots (once per key head) and factor dots (per value head), one 8-lane group per row ----
+  // ---- buffered-key dots: this wave's K tiles against bf16 (hi, mid, lo) of kn (columns 0-2) and qn (4-6) ----
   {
-    float kn[16], qn[16];
+    bf16x8 bk[4];
+    const bool bcol = (n16 & 3) < 3 && n16 < 8;
+    const int brow = bcol ? (n16 >> 2) * 3 + (n16 & 3) : 0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 b = *(const bf16x8*)&sh.bkq[brow][32 * ks + 8 * q4];
+      bk[ks] = bcol ? b : bf16x8{};
+    }
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int j0 = 16 * (wv + 2 * G * t);
+      if (j0 < hmax) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[t][ks], bk[ks], acc, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
+          const int j = j0 + 4 * q4 + i;
+          if ((n16 == 0 || n16 == 4) && j < hmax) ((float*)&sh.dkq[j])[n16 >> 2] = s;
+        }
+      }
+    }
+  }
+  // ---- factor dots (last wave): U^T rows of the G heads against fp16 (hi, lo) of 64 kn (columns 0, 1), 64 qn (2, 3) ----
+  if (fwave) {
+    f16x8 bh[4];
+    const bool bcol = n16 < 4;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 b = *(const f16x8*)&sh.hkq[bcol ? n16 : 0][32 * ks + 8 * q4];
+      bh[ks] = bcol ? b : f16x8{};
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ufr[ks], bh[ks], acc, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float4 a = sh.kn[4 * cc + i], b = sh.qn[4 * cc + i];
-      kn[4 * i] = a.x; kn[4 * i + 1] = a.y; kn[4 * i + 2] = a.z; kn[4 * i + 3] = a.w;
-      qn[4 * i] = b.x; qn[4 * i + 1] = b.y; qn[4 * i + 2] = b.z; qn[4 * i + 3] = b.w;
-    }
-    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
-    constexpr int MAXT = (LMAX + 4 * G + 16 * G - 1) / (16 * G);
-    const int ntask = hmax + G * R;
-    const int t0 = g * 16 + rg;
-    constexpr int PF = MAXT < 3 ? MAXT : 3;     // rows prefetched per batch
-#pragma unroll
-    for (int i0 = 0; i0 < MAXT; i0 += PF) {
-    uint4 kw[PF][2];
-#pragma unroll
-    for (int i = i0; i < i0 + PF && i < MAXT; ++i) {
-      const int t = t0 + 16 * G * i;
-      if (t < hmax) {
-        const uint4* p = (const uint4*)(Kb + (long long)t * KD + 16 * cc);
-        kw[i - i0][0] = p[0];
-        kw[i - i0][1] = p[1];
-      }
-    }
-#pragma unroll
-    for (int i = i0; i < i0 + PF && i < MAXT; ++i) {
-      const int t = t0 + 16 * G * i;
-      if (t < ntask) {
-        float x[16];
-        if (t < hmax) {
-          unpack8(kw[i - i0][0], x); unpack8(kw[i - i0][1], x + 8);
-        } else {
-          const int tt = t - hmax, g2 = tt / R, r = tt - g2 * R;
-          const uint4* p = (const uint4*)(&sh.uq[g2][r][16 * cc]);
-          unpack8h(p[0], x); unpack8h(p[1], x + 8);
-        }
-        float dk = 0.f, dq = 0.f;
-#pragma unroll
-        for (int e = 0; e < 16; ++e) { dk = fmaf(x[e], kn[e], dk); dq = fmaf(x[e], qn[e], dq); }
-        dk = sum8(dk); dq = sum8(dq);
-        if (cc == 0) {
-          if (t < hmax) sh.dkq[t] = make_float2(dk, dq);
-          else { const int tt = t - hmax; sh.duq[tt / R][tt % R] = make_float2(dk, dq); }
-        }
-      }
-    }
+      const float s = (acc[i] + dpp<DPP_XOR1>(acc[i])) * (1.0f / KSPLIT);               // hi + lo (lanes 0 / 2)
+      const int m = 4 * q4 + i;
+      if ((n16 == 0 || n16 == 2) && m < G * R) ((float*)&sh.duq[m / R][m % R])[n16 >> 1] = s;
     }
   }
   __syncthreads();
   if (!live) { out[lt] = 0; return; }
 
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
+  const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
+  const float2 mqr = sh.mq[g][lt];
+  const float mq = (mqr.x * (sh.sc[g][3] * (1.0f / DIGIT_SCALE))) * sv;
+  const float yq = (mqr.y * (sh.sc[g][4] * (1.0f / DIGIT_SCALE))) * sv;
   float a4 = 0.f, a5 = 0.f;
   for (int j = 0; j < h; ++j) {
     const float ub = bf2f(sh.ub[g][j][lt]);
@@ -254,23 +360,17 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   }
   float a6 = 0.f, a7 = 0.f;
   for (int r = 0; r < R; ++r) {
-    const float qt = h2f(sh.uq[g][r][KD + lt]);
     const float2 d = sh.duq[g][r];
-    a6 = fmaf(qt, d.x, a6);
-    a7 = fmaf(qt, d.y, a7);
+    a6 = fmaf(qt[r], d.x, a6);
+    a7 = fmaf(qt[r], d.y, a7);
   }
   const float pn = P * alpha;
   const float u = beta * (vin - (pn * (mq + a6) + a4));
   const float y = pn * (yq + a7) + a5 + kappa * u;
   out[lt] = f2bf(y);
   ((bf16_t*)st.Ubuf)[(sh_ * L + h) * VD + lt] = f2bf(u);
-  if (g == 0) {
-    const float kc = bf2f(mrow[H * KD + hk * KD + lt]) * ink;
-    ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + lt] = f2bf(kc);
-  }
-  if (lt < h) Wp[lt] = wmine;
-  if (lt == h) Wp[h] = 1.0f;
   if (lt == 0) {
+    Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
   }
