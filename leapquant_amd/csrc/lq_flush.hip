@@ -3,9 +3,11 @@
 // Semantics: /root/reference/leapquant/kernels.py:1077-2033 (flush), 2126-2242 (quantize), 2041-2123 (dequant),
 // 2246-2331 (lowrank).  Layout of the checkpoint and window buffer: include/lq.h.
 //
-// One workgroup of 256 threads (4 waves) per (slot, value head).  The head's 128 x 128 matrix lives in registers in the
-// accumulator layout of v_mfma_f32_16x16x32_bf16: wave w owns key channels c in [32w, 32w + 32), lane l holds
-//     acc[mt][nt][i] = M[c][v],   c = 32 w + 16 mt + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
+// One workgroup of 512 threads (8 waves) per (slot, value head) (the flush is persistent: a workgroup takes its due
+// heads one after another; quantize / dequant / lowrank take one head each).  The head's 128 x 128 matrix lives in
+// registers in the accumulator layout of v_mfma_f32_16x16x32_bf16: wave w owns key channels c in [16w, 16w + 16),
+// lane l holds
+//     acc[nt][i] = M[c][v],   c = 16 w + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
 // The window rebuild (a rank-L GEMM, ~29 flop/byte at L = 64) runs on MFMA with bf16 hi/lo operands exactly where the
 // reference splits; the rank-R subspace products, CholeskyQR2, residual, smoothing and requantisation are VALU work on
 // that layout with DPP / LDS reductions.  Due heads are found on the device (hcnt == L), so the fixed grid is
@@ -17,79 +19,99 @@ namespace {
 constexpr int KD = 128, VD = 128;
 constexpr int LPMAX = 64;            // largest window
 constexpr int OPS = LPMAX + 8;       // operand row stride (bf16): 144 B rows
-constexpr int FT = 256;              // threads per workgroup
+constexpr int FT = 512;              // threads per workgroup
+constexpr int NW = FT / 64;          // waves
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 struct Tile {
-  f32x4 a[2][8];
+  f32x4 a[8];
 };
 
 struct FlushShared {
-  bf16_t op[3][KD][OPS];       // rebuild operands [c or v][j]
+  union {
+    bf16_t op[3][KD][OPS];     // rebuild operands [c or v][j]
+    struct {                   // after the rebuild
+      f32x4 qpart[NW][VD];     // per-wave partials of the row reductions
+      float rowmax[NW][VD];
+    } r;
+  };
   float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
   float svr[VD];               // row factor of the dequant (Sv pn / qmax, KDA: Sv / qmax)
-  float pc[KD];                // KDA: exp(Pbuf)
   float w[LPMAX];
   float uo[4][KD];             // old U^T (KDA: fp16(U^T pc)), rows >= R zero
   float qo[4][VD];             // old Q^T, rows >= R zero
   f32x4 qv[VD];                // current Q operand [v][r] (fp16-rounded Q0, then Q16); fp32 Q before CholeskyQR
   f32x4 pp[KD];                // P16, then U16 [c][r]
-  f32x4 qpart[4][VD];          // per-wave partials of the row reductions
-  float rowmax[4][VD];
+  unsigned long long due;      // persistent flush: due mask of the current candidate chunk
 };
 
-__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// Thread index as seen by the per-head code.  Re-read through an empty asm at the start of every head so that the
+// persistent flush loop cannot hoist the ~100 per-lane LDS addresses derived from it (and keep them all live).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int lane_id() { return opaque_tid() & 63; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(opaque_tid() >> 6); }
 
-// out[k][r] = sum_v M[c_k][v] X[v][r] for the lane's 8 key channels c_k (k = 4 mt + i), complete in every lane
-__device__ __forceinline__ void colred(const Tile& t, const f32x4* X, f32x4 out[8]) {
+// wave-uniform reductions: DPP within each 16-lane row, then the 4 row results through readlane (no LDS traffic)
+__device__ __forceinline__ float rl(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+__device__ __forceinline__ float sum64u(float x) {
+  x = sum16(x);
+  return ((rl(x, 0) + rl(x, 16)) + rl(x, 32)) + rl(x, 48);
+}
+__device__ __forceinline__ float max64u(float x) {
+  x = max16(x);
+  return fmaxf(fmaxf(rl(x, 0), rl(x, 16)), fmaxf(rl(x, 32), rl(x, 48)));
+}
+
+// fn(i, s): s[r] = sum_v M[c_i][v] X[v][r] for the lane's 4 key channels c_i = 16 w + 4 (l >> 4) + i (complete in
+// every lane of the 16-lane row)
+template <class F>
+__device__ __forceinline__ void colred(const Tile& t, const f32x4* X, F fn) {
   const int l = lane_id();
   f32x4 xv[8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) xv[nt] = X[16 * nt + (l & 15)];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
+  for (int i = 0; i < 4; ++i) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 s = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const float m = t.a[mt][nt][i];
-        s[0] = fmaf(m, xv[nt][0], s[0]);
-        s[1] = fmaf(m, xv[nt][1], s[1]);
-        s[2] = fmaf(m, xv[nt][2], s[2]);
-        s[3] = fmaf(m, xv[nt][3], s[3]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = sum16(s[r]);
-      out[4 * mt + i] = s;
+    for (int nt = 0; nt < 8; ++nt) {
+      const float m = t.a[nt][i];
+      s[0] = fmaf(m, xv[nt][0], s[0]);
+      s[1] = fmaf(m, xv[nt][1], s[1]);
+      s[2] = fmaf(m, xv[nt][2], s[2]);
+      s[3] = fmaf(m, xv[nt][3], s[3]);
     }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = sum16(s[r]);
+    fn(i, s);
   }
 }
 
-// part[w][v][r] = sum over this wave's 32 channels c of M[c][v] Y[c][r]  (caller sums the 4 waves)
+// part[w][v][r] = sum over this wave's 16 channels c of M[c][v] Y[c][r]  (caller sums the NW waves)
 __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*part)[VD]) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
-  f32x4 yc[2][4];
+  f32x4 yc[4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) yc[mt][i] = Y[32 * w + 16 * mt + 4 * q + i];
+  for (int i = 0; i < 4; ++i) yc[i] = Y[16 * w + 4 * q + i];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float m = t.a[mt][nt][i];
-        s[0] = fmaf(m, yc[mt][i][0], s[0]);
-        s[1] = fmaf(m, yc[mt][i][1], s[1]);
-        s[2] = fmaf(m, yc[mt][i][2], s[2]);
-        s[3] = fmaf(m, yc[mt][i][3], s[3]);
-      }
+    for (int i = 0; i < 4; ++i) {
+      const float m = t.a[nt][i];
+      s[0] = fmaf(m, yc[i][0], s[0]);
+      s[1] = fmaf(m, yc[i][1], s[1]);
+      s[2] = fmaf(m, yc[i][2], s[2]);
+      s[3] = fmaf(m, yc[i][3], s[3]);
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       s[r] += __shfl_xor(s[r], 16);
@@ -99,17 +121,15 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
   }
 }
 
-// R x R product sum_x A[a][x] B[x][r] over 128 x (A row-major [4][128], B [128] of f32x4), computed by one wave
+// R x R product sum_x A[a][x] B[x][r] over 128 x (A row-major [4][128], B [128] of f32x4), every wave
 __device__ __forceinline__ void small_gram(const float (*A)[128], const f32x4* B, float M[4][4]) {
   const int l = lane_id();
+  const f32x4 b0 = B[l], b1 = B[l + 64];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
+    const float a0 = A[a][l], a1 = A[a][l + 64];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      float s = A[a][l] * B[l][r];
-      s = fmaf(A[a][l + 64], B[l + 64][r], s);
-      M[a][r] = sum64(s);
-    }
+    for (int r = 0; r < 4; ++r) M[a][r] = sum64u(fmaf(a1, b1[r], a0 * b0[r]));
   }
 }
 
@@ -120,7 +140,7 @@ __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c <= r; ++c) gg[k++] = sum64(fmaf(p0[r], p0[c], p1[r] * p1[c]));
+    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
   float ll[10];
   ll[0] = rsqrt_rn(fmaxf(gg[0], 1e-30f));
   ll[1] = gg[1] * ll[0];
@@ -147,34 +167,35 @@ __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
 __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
   for (int j = 0; j < R; ++j) {
     for (int c = 0; c < j; ++c) {
-      const float sc = sum64(fmaf(p0[c], p0[j], p1[c] * p1[j]));
+      const float sc = sum64u(fmaf(p0[c], p0[j], p1[c] * p1[j]));
       p0[j] = p0[j] - sc * p0[c];
       p1[j] = p1[j] - sc * p1[c];
     }
-    const float nrm = sum64(fmaf(p0[j], p0[j], p1[j] * p1[j]));
+    const float nrm = sum64u(fmaf(p0[j], p0[j], p1[j] * p1[j]));
     const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
     p0[j] *= rs;
     p1[j] *= rs;
   }
 }
 
-// Tile init with the dequantised checkpoint codes  x svr[v] x skl[c]  (codes read in place from the state block)
-__device__ __forceinline__ void tile_from_codes(Tile& t, const int8_t* Sq, const float* svr, const float* skl) {
+// the 8 code words of the lane's tile entries (issued early; consumed by tile_from_words)
+__device__ __forceinline__ void load_code_words(uint32_t wds[8], const int8_t* Sq) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt) {
-    const int c0 = 32 * w + 16 * mt + 4 * q;
-    float kc[4];
+  for (int nt = 0; nt < 8; ++nt) wds[nt] = *(const uint32_t*)(Sq + (16 * nt + (l & 15)) * KD + 16 * w + 4 * q);
+}
+// Tile init with the dequantised checkpoint codes  x svr[v] x skl[c]
+__device__ __forceinline__ void tile_from_words(Tile& t, const uint32_t wds[8], const float* svr, const float* skl) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  const int c0 = 16 * w + 4 * q;
+  float kc[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
+  for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-      const uint32_t word = *(const uint32_t*)(Sq + v * KD + c0);
-      const float rv = svr[v];
+  for (int nt = 0; nt < 8; ++nt) {
+    const float rv = svr[16 * nt + (l & 15)];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = ((float)(int)(int8_t)(word >> (8 * i)) * rv) * kc[i];
-    }
+    for (int i = 0; i < 4; ++i) t.a[nt][i] = ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * rv) * kc[i];
   }
 }
 
@@ -182,84 +203,121 @@ __device__ __forceinline__ void tile_from_codes(Tile& t, const int8_t* Sq, const
 __device__ __forceinline__ void rebuild_mfma(Tile& t, const bf16_t (*A)[OPS], const bf16_t (*B)[OPS], int nks) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
   for (int ks = 0; ks < nks; ++ks) {
-    bf16x8 af[2];
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt) af[mt] = *(const bf16x8*)&A[32 * w + 16 * mt + (l & 15)][32 * ks + 8 * q];
+    const bf16x8 af = *(const bf16x8*)&A[16 * w + (l & 15)][32 * ks + 8 * q];
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       const bf16x8 bfr = *(const bf16x8*)&B[16 * nt + (l & 15)][32 * ks + 8 * q];
-#pragma unroll
-      for (int mt = 0; mt < 2; ++mt) t.a[mt][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[mt], bfr, t.a[mt][nt], 0, 0, 0);
+      t.a[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, t.a[nt], 0, 0, 0);
     }
   }
 }
 
-// Stage the window into the MFMA operands.  GDN (kda = false): op0[c][j] = K_j[c], op1 / op2 [v][j] = hi / lo of
-// w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c] with D_j the product of the
-// later entries' decays (kernels.py:1453-1463), op2[v][j] = u_j[v].  Entries j >= h and the padding to 32 are zero.
-__device__ void stage_window(FlushShared& sh, const lq_state& st, int slot, int hv, int h, int LP, bool kda) {
-  const int tid = threadIdx.x;
+// Window rows of one head, loaded up front (unconditional, clamped addresses; rows >= h and the padding to LP carry
+// zero weight): item it = (row j = it % LP, 8-column chunk (it / LP)).  Two items per thread cover LP <= 64.
+constexpr int WIN_ITEMS = LPMAX * 16 / FT;
+struct WinRegs {
+  uint4 k[WIN_ITEMS], u[WIN_ITEMS];
+};
+__device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int slot, int hv, int h, int LP) {
+  const int tid = opaque_tid();
   const int G = st.HV / st.H, hk = hv / G, L = st.L;
   const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD;
   const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * VD;
-  if (!kda) {
-    for (int it = tid; it < LP * 16; it += FT) {       // (j, 8-column chunk)
-      const int j = it >> 4, c8 = (it & 15) * 8;
-      uint4 kw = make_uint4(0, 0, 0, 0), uw = make_uint4(0, 0, 0, 0);
-      if (j < h) {
-        kw = *(const uint4*)(Kb + (long long)j * KD + c8);
-        uw = *(const uint4*)(Ub + (long long)j * VD + c8);
-      }
-      const float wj = j < h ? sh.w[j] : 0.f;
-      const uint32_t ku[4] = {kw.x, kw.y, kw.z, kw.w}, uu[4] = {uw.x, uw.y, uw.z, uw.w};
+  const int nit = LP * 16;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const bf16_t kb = (bf16_t)(ku[e >> 1] >> (16 * (e & 1)));
-        const bf16_t ub = (bf16_t)(uu[e >> 1] >> (16 * (e & 1)));
+  for (int k = 0; k < WIN_ITEMS; ++k) {
+    const int it = min(tid + FT * k, nit - 1);
+    const int j = it % LP, c8 = (it / LP) * 8;
+    const int jr = j < h ? j : 0;
+    r.k[k] = *(const uint4*)(Kb + (long long)jr * KD + c8);
+    r.u[k] = *(const uint4*)(Ub + (long long)jr * VD + c8);
+  }
+}
+// GDN operands: op0[c][j] = K_j[c], op1 / op2 [v][j] = hi / lo of w_j u_j[v] (kernels.py:1501-1511); KDA: op2[v][j] = u_j[v]
+// (the KDA key operands are written by stage_kda_keys)
+__device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP, bool kda) {
+  const int tid = opaque_tid();
+  const int nit = LP * 16;
+#pragma unroll
+  for (int k = 0; k < WIN_ITEMS; ++k) {
+    const int it = min(tid + FT * k, nit - 1);
+    const int j = it % LP, c8 = (it / LP) * 8;
+    const float wj = j < h ? sh.w[j] : 0.f;
+    const uint32_t ku[4] = {r.k[k].x, r.k[k].y, r.k[k].z, r.k[k].w};
+    const uint32_t uu[4] = {r.u[k].x, r.u[k].y, r.u[k].z, r.u[k].w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bf16_t kb = (bf16_t)(ku[e >> 1] >> (16 * (e & 1)));
+      const bf16_t ub = (bf16_t)(uu[e >> 1] >> (16 * (e & 1)));
+      if (!kda) {
         sh.op[0][c8 + e][j] = kb;
         const float wu = wj * bf2f(ub);
         const bf16_t hi = f2bf(wu);
         sh.op[1][c8 + e][j] = hi;
         sh.op[2][c8 + e][j] = f2bf(wu - bf2f(hi));
+      } else {
+        sh.op[2][c8 + e][j] = j < h ? ub : (bf16_t)0;
       }
     }
-  } else {
-    if (tid < KD) {                                     // thread per key channel: backward decay product
-      const int c = tid;
-      const f16_t* Gb = (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD + c;
-      float dcur = 1.0f;
-      for (int j = LP - 1; j >= 0; --j) {
-        bf16_t hi = 0, lo = 0;
-        if (j < h) {
-          const float kd = bf2f(Kb[(long long)j * KD + c]) * (sh.w[j] * dcur);
-          hi = f2bf(kd);
-          lo = f2bf(kd - bf2f(hi));
-          dcur = dcur * h2f(Gb[(long long)j * KD]);
-        }
-        sh.op[0][c][j] = hi;
-        sh.op[1][c][j] = lo;
+  }
+}
+// KDA key operands: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < L} e_i[c] (kernels.py:1453-1463).
+// Thread per channel c; the column's keys and decays come in batches of 16 entries (loads first, then the scan).
+__device__ __forceinline__ void stage_kda_keys(FlushShared& sh, const lq_state& st, int slot, int hv, int h, int LP) {
+  const int c = opaque_tid();
+  if (c >= KD) return;
+  const int G = st.HV / st.H, hk = hv / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD + c;
+  const f16_t* Gb = (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD + c;
+  float dcur = 1.0f;
+  for (int j0 = LP - 16; j0 >= 0; j0 -= 16) {
+    bf16_t kr[16];
+    f16_t er[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int j = j0 + e, jr = j < h ? j : 0;
+      kr[e] = Kb[(long long)jr * KD];
+      er[e] = Gb[(long long)jr * KD];
+    }
+#pragma unroll
+    for (int e = 15; e >= 0; --e) {
+      const int j = j0 + e;
+      bf16_t hi = 0, lo = 0;
+      const float kd = bf2f(kr[e]) * (sh.w[j] * dcur);
+      if (j < h) {
+        hi = f2bf(kd);
+        lo = f2bf(kd - bf2f(hi));
+        dcur = dcur * h2f(er[e]);
       }
-    } else {
-      const int v = tid - KD;
-      for (int j = 0; j < LP; ++j) sh.op[2][v][j] = j < h ? Ub[(long long)j * VD + v] : (bf16_t)0;
+      sh.op[0][c][j] = hi;
+      sh.op[1][c][j] = lo;
     }
   }
 }
 
+// per-wave partial sums of the row reductions -> the full sum for row v (threads v < 128)
+__device__ __forceinline__ f32x4 sum_parts(const f32x4 (*part)[VD], int v) {
+  f32x4 s = part[0][v];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s += part[w][v];
+  return s;
+}
+__device__ __forceinline__ float max_parts(const float (*part)[VD], int v) {
+  float m = part[0][v];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) m = fmaxf(m, part[w][v]);
+  return m;
+}
+
 // ------------------------------------------------------------------------------------------------------------------
-// flush (kernels.py:1077-2033)
+// flush (kernels.py:1077-2033): one due (slot, head)
 // ------------------------------------------------------------------------------------------------------------------
 template <bool KDA>
-__global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx,
-                                                   float qmax) {
-  __shared__ FlushShared sh;
+__device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+                           float qmax) {
   const int HV = st.HV, L = st.L, R = st.R;
-  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
-  const int slot = idx[n];
-  if (slot <= 0) return;
   const long long sh_ = (long long)slot * HV + hv;
-  if (st.hcnt[sh_] != L) return;                      // due = slot > 0 and a full window (kernels.py:1200)
-  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4;
   char* base = block_base(st, slot, hv);
   int8_t* Sq = (int8_t*)base;
   float* Sk = (float*)(base + VD * KD);
@@ -267,38 +325,58 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
   f16_t* UQ = (f16_t*)(Sv + VD);
   const int LP = (L + 31) & ~31;
 
-  // ---- stage 1: scalars, old factors and scales to LDS ----
+  // ---- stage 1: every load of the head up front (scalars, scales, factors, window rows, code words) ----
   float pn = 1.f, rpn = 1.f;
   if (!KDA) {
     pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);               // kernels.py:1471
     rpn = 1.0f / pn;                                  // kernels.py:1477
   }
+  const int cv = tid & 127;                           // column (tid < 128) or row (128 <= tid < 256) of the stage-1 loads
+  const bool colt = tid < KD;
+  const float scv = colt ? Sk[cv] : Sv[cv];
+  float uqv[4], q0v[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
+    q0v[a] = Q0[cv * R + min(a, R - 1)];
+  }
+  const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinRegs win;
+  load_window(win, st, slot, hv, L, LP);
+  uint32_t wds[8];
+  load_code_words(wds, Sq);
+
   if (tid < KD) {
-    const int c = tid;
+    const int c = cv;
     float pcv = 1.f;
-    if (KDA) { pcv = (float)exp((double)st.Pbuf[sh_ * KD + c]); sh.pc[c] = pcv; }   // kernels.py:1451
-    sh.skl[c] = KDA ? Sk[c] * pcv : Sk[c];                                          // kernels.py:1519
+    if (KDA) pcv = (float)exp((double)pbc);                                          // kernels.py:1451
+    sh.skl[c] = KDA ? scv * pcv : scv;                                                // kernels.py:1519
+#pragma unroll
     for (int a = 0; a < 4; ++a) {
-      float u = a < R ? h2f(UQ[a * (KD + VD) + c]) : 0.f;
+      float u = a < R ? uqv[a] : 0.f;
       if (KDA) u = hround(u * pcv);                                                   // kernels.py:1464-1465
       sh.uo[a][c] = u;
     }
-  } else {
-    const int v = tid - KD;
-    sh.svr[v] = KDA ? Sv[v] * (1.0f / qmax) : Sv[v] * (pn / qmax);                  // kernels.py:1468, 1483
-    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? h2f(UQ[a * (KD + VD) + KD + v]) : 0.f;
-    f32x4 q0v;
-    for (int r = 0; r < 4; ++r) q0v[r] = r < R ? hround(Q0[v * R + r]) : 0.f;   // kernels.py:1573-1577
-    sh.qv[v] = q0v;
+  } else if (tid < KD + VD) {
+    const int v = cv;
+    sh.svr[v] = KDA ? scv * (1.0f / qmax) : scv * (pn / qmax);                       // kernels.py:1468, 1483
+#pragma unroll
+    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? uqv[a] : 0.f;
+    f32x4 q0;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) q0[r] = r < R ? hround(q0v[r]) : 0.f;             // kernels.py:1573-1577
+    sh.qv[v] = q0;
   }
-  if (tid < LPMAX) sh.w[tid] = tid < L ? st.Wbuf[sh_ * L + tid] : 0.f;
+  if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
   __syncthreads();
-  stage_window(sh, st, slot, hv, L, LP, KDA);
+  store_window(sh, win, L, LP, KDA);
+  if (KDA) stage_kda_keys(sh, st, slot, hv, L, LP);
   __syncthreads();
 
   // ---- stage 2: B = deq(S0) (+ decay) + window, fp16 (kernels.py:1483-1571) ----
   Tile t;
-  tile_from_codes(t, Sq, sh.svr, sh.skl);
+  tile_from_words(t, wds, sh.svr, sh.skl);
   if (!KDA) {
     rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
     rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
@@ -307,49 +385,38 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
     rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
   }
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = hround(t.a[mt][nt][i]);
+    for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(t.a[nt][i]);
 
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
   // P = B^T Q + pn U_old (Q_old^T Q), fp16
   auto p_step = [&]() {
     float M[4][4];
     small_gram(sh.qo, sh.qv, M);                      // Q_old^T Q (every wave)
-    f32x4 pc8[8];
-    colred(t, sh.qv, pc8);
-    if ((l & 15) == 0) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const int c = 32 * w + 16 * (k >> 2) + 4 * q + (k & 3);
+    colred(t, sh.qv, [&](int i, f32x4 s) {
+      const int c = 16 * w + 4 * q + i;
+      if ((l & 15) == 0) {
         f32x4 p;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float corr = sh.uo[0][c] * M[0][r] + sh.uo[1][c] * M[1][r] + sh.uo[2][c] * M[2][r] + sh.uo[3][c] * M[3][r];
-          p[r] = r < R ? hround(pc8[k][r] + pn * corr) : 0.f;
+          p[r] = r < R ? hround(s[r] + pn * corr) : 0.f;
         }
         sh.pp[c] = p;
       }
-    }
+    });
   };
   p_step();
-  __syncthreads();
+  __syncthreads();                                    // P16 complete; every wave is past the rebuild (op region free)
   // Q = B P16 + pn Q_old (U_old^T P16)
-  rowred(t, sh.pp, sh.qpart);
-  __syncthreads();
-  if (tid < VD) {
-    const int v = tid;
-    f32x4 s = sh.qpart[0][v] + sh.qpart[1][v] + sh.qpart[2][v] + sh.qpart[3][v];
-    sh.qpart[0][v] = s;
-  }
+  rowred(t, sh.pp, sh.r.qpart);
   float M2[4][4];
   small_gram(sh.uo, sh.pp, M2);
   __syncthreads();
   if (tid < VD) {
     const int v = tid;
-    f32x4 s = sh.qpart[0][v];
+    f32x4 s = sum_parts(sh.r.qpart, v);
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       s[r] += pn * (sh.qo[0][v] * M2[0][r] + sh.qo[1][v] * M2[1][r] + sh.qo[2][v] * M2[2][r] + sh.qo[3][v] * M2[3][r]);
@@ -373,84 +440,68 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
   __syncthreads();
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
-  {
-    f32x4 qov[8], qnv[8];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-      qov[nt] = f32x4{sh.qo[0][v], sh.qo[1][v], sh.qo[2][v], sh.qo[3][v]};
-      qnv[nt] = sh.qv[v];
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    const f32x4 qnv = sh.qv[v];
+    const f32x4 qov = f32x4{sh.qo[0][v], sh.qo[1][v], sh.qo[2][v], sh.qo[3][v]};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 16 * w + 4 * q + i;
+      const f32x4 unc = sh.pp[c];
+      float e = KDA ? t.a[nt][i] : t.a[nt][i] * rpn;
+      e = fmaf(qov[0], sh.uo[0][c], e);
+      e = fmaf(qov[1], sh.uo[1][c], e);
+      e = fmaf(qov[2], sh.uo[2][c], e);
+      e = fmaf(qov[3], sh.uo[3][c], e);
+      if (!KDA) e = e * pn;
+      e = fmaf(-qnv[0], unc[0], e);
+      e = fmaf(-qnv[1], unc[1], e);
+      e = fmaf(-qnv[2], unc[2], e);
+      e = fmaf(-qnv[3], unc[3], e);
+      t.a[nt][i] = hround(e);
     }
-#pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = 32 * w + 16 * mt + 4 * q + i;
-        const f32x4 uoc = f32x4{sh.uo[0][c], sh.uo[1][c], sh.uo[2][c], sh.uo[3][c]};
-        const f32x4 unc = sh.pp[c];
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          float e = KDA ? t.a[mt][nt][i] : t.a[mt][nt][i] * rpn;
-          e = fmaf(qov[nt][0], uoc[0], e);
-          e = fmaf(qov[nt][1], uoc[1], e);
-          e = fmaf(qov[nt][2], uoc[2], e);
-          e = fmaf(qov[nt][3], uoc[3], e);
-          if (!KDA) e = e * pn;
-          e = fmaf(-qnv[nt][0], unc[0], e);
-          e = fmaf(-qnv[nt][1], unc[1], e);
-          e = fmaf(-qnv[nt][2], unc[2], e);
-          e = fmaf(-qnv[nt][3], unc[3], e);
-          t.a[mt][nt][i] = hround(e);
-        }
-      }
   }
 
   // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
-  float rsk[8];
+  float rsk[4];
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int i = 0; i < 4; ++i) {
+    float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) s += fabsf(t.a[mt][nt][i]);
-      s = sum16(s);
-      const float msum = s * (1.0f / VD);
-      rsk[4 * mt + i] = fminf(rsqrt_rn(msum), 1.0f / LQ_EPS);
-      if ((l & 15) == 0) Sk[32 * w + 16 * mt + 4 * q + i] = fmaxf(sqrtf(msum), LQ_EPS);
-    }
+    for (int nt = 0; nt < 8; ++nt) s += fabsf(t.a[nt][i]);
+    s = sum16(s);
+    const float msum = s * (1.0f / VD);
+    rsk[i] = fminf(rsqrtf_rn(msum), 1.0f / LQ_EPS);
+    if ((l & 15) == 0) Sk[16 * w + 4 * q + i] = fmaxf(sqrtf(msum), LQ_EPS);
+  }
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        t.a[mt][nt][i] *= rsk[4 * mt + i];
-        m = fmaxf(m, fabsf(t.a[mt][nt][i]));
-      }
+    for (int i = 0; i < 4; ++i) {
+      t.a[nt][i] *= rsk[i];
+      m = fmaxf(m, fabsf(t.a[nt][i]));
+    }
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
-    if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
+    if (q == 0) sh.r.rowmax[w][16 * nt + (l & 15)] = m;
   }
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
-    const float rmax = fmaxf(fmaxf(fmaxf(sh.rowmax[0][v], sh.rowmax[1][v]), fmaxf(sh.rowmax[2][v], sh.rowmax[3][v])), LQ_EPS);
+    const float rmax = fmaxf(max_parts(sh.r.rowmax, v), LQ_EPS);
     const float rq = qmax * (1.0f / rmax);
     if (w == 0 && q == 0) Sv[v] = rmax;
+    uint32_t word = 0;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t bits = __float_as_uint(__builtin_fmaf(t.a[mt][nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
-        word |= (bits & 0xffu) << (8 * i);
-      }
-      *(uint32_t*)(Sq + v * KD + 32 * w + 16 * mt + 4 * q) = word;
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t bits = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+      word |= (bits & 0xffu) << (8 * i);
     }
+    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = word;
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
   if (tid < KD) {
@@ -461,7 +512,7 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
       f16_t* Gb = (f16_t*)st.Gbuf + sh_ * L * KD + c;
       for (int j = 0; j < L; ++j) Gb[(long long)j * KD] = 0x3c00;   // fp16 1.0
     }
-  } else {
+  } else if (tid < KD + VD) {
     const int v = tid - KD;
     for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
   }
@@ -469,6 +520,42 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
   if (tid == 0) {
     if (!KDA) st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
+  }
+  __syncthreads();                                    // LDS reuse by the next head of this workgroup
+}
+
+// Persistent flush: workgroup b checks the candidates p = b + gridDim.x k (row n = p / HV, head p % HV) 64 at a time
+// (wave 0, one per lane), and processes the due ones (slot > 0, hcnt == L; kernels.py:1200) one after another.  A call
+// in which no head is due costs one short launch of ~2 workgroups per CU.
+template <bool KDA>
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
+void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax) {
+  __shared__ FlushShared sh;
+  const int HV = st.HV, L = st.L;
+  const int total = N * HV;
+  const int stride = gridDim.x;
+  for (int base = blockIdx.x; base < total; base += 64 * stride) {
+    if (threadIdx.x < 64) {
+      const int p = base + stride * (int)threadIdx.x;
+      bool due = false;
+      if (p < total) {
+        const int n = p / HV, hv = p - n * HV;
+        const int slot = idx[n];
+        due = slot > 0 && st.hcnt[(long long)slot * HV + hv] == L;
+      }
+      const unsigned long long m = __ballot(due);
+      if (threadIdx.x == 0) sh.due = m;
+    }
+    __syncthreads();
+    unsigned long long m = sh.due;
+    __syncthreads();
+    while (m) {
+      const int b = __ffsll((long long)m) - 1;
+      m &= m - 1;
+      const int p = base + stride * b;
+      const int n = p / HV, hv = p - n * HV;
+      flush_head<KDA>(sh, st, Q0, idx[n], hv, qmax);
+    }
   }
 }
 
@@ -478,13 +565,13 @@ __global__ __launch_bounds__(FT) void flush_kernel(lq_state st, const float* __r
 struct QuantShared {
   f32x4 qv[VD];
   f32x4 pp[KD];
-  f32x4 qpart[4][VD];
-  float rowmax[4][VD];
+  f32x4 qpart[NW][VD];
+  float rowmax[NW][VD];
   float sk[KD];
 };
 
-__global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* __restrict__ Q0,
-                                                      const int* __restrict__ idx, float qmax) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
+void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax) {
   __shared__ QuantShared sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
@@ -496,13 +583,10 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
   const float* S = (const float*)base;
   Tile t;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-      const float4 x = *(const float4*)(S + v * KD + 32 * w + 16 * mt + 4 * q);
-      t.a[mt][nt] = f32x4{x.x, x.y, x.z, x.w};
-    }
+  for (int nt = 0; nt < 8; ++nt) {
+    const float4 x = *(const float4*)(S + (16 * nt + (l & 15)) * KD + 16 * w + 4 * q);
+    t.a[nt] = f32x4{x.x, x.y, x.z, x.w};
+  }
   if (tid < VD) {
     f32x4 q0v;
     for (int r = 0; r < 4; ++r) q0v[r] = r < R ? Q0[tid * R + r] : 0.f;
@@ -510,12 +594,7 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
   }
   __syncthreads();
   // P = S^T Q, MGS; Q = S P, MGS (ITERS = 1)
-  f32x4 pc8[8];
-  colred(t, sh.qv, pc8);
-  if ((l & 15) == 0) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = pc8[k];
-  }
+  colred(t, sh.qv, [&](int i, f32x4 s) { if ((l & 15) == 0) sh.pp[16 * w + 4 * q + i] = s; });
   __syncthreads();
   if (w == 0) {
     f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
@@ -527,23 +606,23 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
   rowred(t, sh.pp, sh.qpart);
   __syncthreads();
   if (w == 0) {
-    f32x4 p0 = sh.qpart[0][l] + sh.qpart[1][l] + sh.qpart[2][l] + sh.qpart[3][l];
-    f32x4 p1 = sh.qpart[0][l + 64] + sh.qpart[1][l + 64] + sh.qpart[2][l + 64] + sh.qpart[3][l + 64];
+    f32x4 p0 = sum_parts(sh.qpart, l), p1 = sum_parts(sh.qpart, l + 64);
     mgs(p0, p1, R);
     sh.qv[l] = p0;
     sh.qv[l + 64] = p1;
   }
   __syncthreads();
   // U = fp16(S^T Q), Q16 = fp16(Q)
-  colred(t, sh.qv, pc8);
+  f32x4 ucol[4];
+  colred(t, sh.qv, [&](int i, f32x4 s) { ucol[i] = s; });
   __syncthreads();
   if ((l & 15) == 0) {
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
+    for (int i = 0; i < 4; ++i) {
       f32x4 u;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(pc8[k][r]) : 0.f;
-      sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = u;
+      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(ucol[i][r]) : 0.f;
+      sh.pp[16 * w + 4 * q + i] = u;
     }
   }
   if (tid < VD) {
@@ -554,40 +633,32 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
   }
   __syncthreads();
   // E = S - Q U^T (fp32), column scales
-  {
-    f32x4 qnv[8];
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) qnv[nt] = sh.qv[16 * nt + (l & 15)];
+  for (int i = 0; i < 4; ++i) {
+    const f32x4 unc = sh.pp[16 * w + 4 * q + i];
+    float s = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
+    for (int nt = 0; nt < 8; ++nt) {
+      const f32x4 qnv = sh.qv[16 * nt + (l & 15)];
+      float e = t.a[nt][i];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const f32x4 unc = sh.pp[32 * w + 16 * mt + 4 * q + i];
-        float s = 0.f;
-#pragma unroll
-        for (int nt = 0; nt < 8; ++nt) {
-          float e = t.a[mt][nt][i];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) e = fmaf(-qnv[nt][r], unc[r], e);
-          t.a[mt][nt][i] = e;
-          s += fabsf(e);
-        }
-        s = sum16(s);
-        const float skc = fmaxf(sqrtf(s / (float)VD), LQ_EPS);      // kernels.py:2222
-        if ((l & 15) == 0) sh.sk[32 * w + 16 * mt + 4 * q + i] = skc;
-      }
+      for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
+      t.a[nt][i] = e;
+      s += fabsf(e);
+    }
+    s = sum16(s);
+    const float skc = fmaxf(sqrtf(s / (float)VD), LQ_EPS);      // kernels.py:2222
+    if ((l & 15) == 0) sh.sk[16 * w + 4 * q + i] = skc;
   }
   __syncthreads();
-  float skr[8];
+  float skr[4];
 #pragma unroll
-  for (int k = 0; k < 8; ++k) skr[k] = sh.sk[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)];
+  for (int i = 0; i < 4; ++i) skr[i] = sh.sk[16 * w + 4 * q + i];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[mt][nt][i] / skr[4 * mt + i]));   // kernels.py:2224-2227
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] / skr[i]));   // kernels.py:2224-2227
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
     if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
@@ -601,24 +672,21 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
-    const float svv = fmaxf(fmaxf(fmaxf(sh.rowmax[0][v], sh.rowmax[1][v]), fmaxf(sh.rowmax[2][v], sh.rowmax[3][v])), LQ_EPS);
+    const float svv = fmaxf(max_parts(sh.rowmax, v), LQ_EPS);
+    uint32_t word = 0;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float x = (t.a[mt][nt][i] / (skr[4 * mt + i] * svv)) * qmax;   // kernels.py:2229
-        const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
-        word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
-      }
-      *(uint32_t*)(Sq + v * KD + 32 * w + 16 * mt + 4 * q) = word;
+    for (int i = 0; i < 4; ++i) {
+      const float x = (t.a[nt][i] / (skr[i] * svv)) * qmax;   // kernels.py:2229
+      const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
+      word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
     }
+    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = word;
     if (w == 0 && q == 0) Sv[v] = svv;
   }
   if (tid < KD) {
     Sk[tid] = sh.sk[tid];
     for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + tid] = f2h(sh.pp[tid][r]);
-  } else {
+  } else if (tid < KD + VD) {
     const int v = tid - KD;
     for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
   }
@@ -632,7 +700,8 @@ __global__ __launch_bounds__(FT) void quantize_kernel(lq_state st, const float* 
 // ------------------------------------------------------------------------------------------------------------------
 // prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place
 // ------------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(FT) void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
+void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   __shared__ FlushShared sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
@@ -647,54 +716,56 @@ __global__ __launch_bounds__(FT) void dequant_kernel(lq_state st, const int* __r
   const f16_t* UQ = (const f16_t*)(Sv + VD);
   const int h = min(st.hcnt[sh_], L);
   const float P = st.Pbuf[sh_];
-  const int LP = h > 0 ? ((h + 31) & ~31) : 0;
+  const int LP = h > 0 ? ((h + 31) & ~31) : 32;
+  const int cv = tid & 127;
+  const bool colt = tid < KD;
+  const float scv = colt ? Sk[cv] : Sv[cv];
+  float uqv[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinRegs win;
+  load_window(win, st, slot, hv, h, LP);
+  uint32_t wds[8];
+  load_code_words(wds, Sq);
   if (tid < KD) {
-    sh.skl[tid] = Sk[tid];
-    for (int a = 0; a < 4; ++a) sh.uo[a][tid] = a < R ? h2f(UQ[a * (KD + VD) + tid]) : 0.f;
-  } else {
-    const int v = tid - KD;
-    sh.svr[v] = Sv[v];
-    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? h2f(UQ[a * (KD + VD) + KD + v]) : 0.f;
+    sh.skl[cv] = scv;
+    for (int a = 0; a < 4; ++a) sh.uo[a][cv] = a < R ? uqv[a] : 0.f;
+  } else if (tid < KD + VD) {
+    sh.svr[cv] = scv;
+    for (int a = 0; a < 4; ++a) sh.qo[a][cv] = a < R ? uqv[a] : 0.f;
   }
-  if (tid < LPMAX) sh.w[tid] = tid < h ? st.Wbuf[sh_ * L + tid] : 0.f;
+  if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
   __syncthreads();
-  if (LP > 0) stage_window(sh, st, slot, hv, h, LP, false);
+  store_window(sh, win, h, LP, false);
   Tile t;
   {
     const float inv = 1.0f / qmax;
+    const int c0 = 16 * w + 4 * q;
 #pragma unroll
-    for (int mt = 0; mt < 2; ++mt) {
-      const int c0 = 32 * w + 16 * mt + 4 * q;
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const float rv = sh.svr[v];
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        const int v = 16 * nt + (l & 15);
-        const uint32_t word = *(const uint32_t*)(Sq + v * KD + c0);
-        const float rv = sh.svr[v];
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + i;
+        float x = (((float)(int)(int8_t)(wds[nt] >> (8 * i)) * inv) * sh.skl[c]) * rv;   // kernels.py:2107
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = c0 + i;
-          float x = (((float)(int)(int8_t)(word >> (8 * i)) * inv) * sh.skl[c]) * rv;    // kernels.py:2107
-#pragma unroll
-          for (int a = 0; a < 4; ++a) x = fmaf(sh.qo[a][v], sh.uo[a][c], x);           // kernels.py:2109-2111
-          t.a[mt][nt][i] = x * P;                                                       // kernels.py:2113
-        }
+        for (int a = 0; a < 4; ++a) x = fmaf(sh.qo[a][v], sh.uo[a][c], x);            // kernels.py:2109-2111
+        t.a[nt][i] = x * P;                                                             // kernels.py:2113
       }
     }
   }
   __syncthreads();
-  if (LP > 0) {
-    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
-    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
-  }
+  rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+  rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
   __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
   float* S = (float*)base;
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-      *(float4*)(S + v * KD + 32 * w + 16 * mt + 4 * q) = make_float4(t.a[mt][nt][0], t.a[mt][nt][1], t.a[mt][nt][2], t.a[mt][nt][3]);
-    }
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    *(float4*)(S + v * KD + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
+  }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {
     st.Pbuf[sh_] = 1.f;
@@ -705,34 +776,28 @@ __global__ __launch_bounds__(FT) void dequant_kernel(lq_state st, const int* __r
 // ------------------------------------------------------------------------------------------------------------------
 // low-rank factoriser (kernels.py:2246-2314): x [n][K][V]; P = MGS(x Q), Q = MGS(x^T P) x iters; U = x Q
 // ------------------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(FT) void lowrank_kernel(const float* __restrict__ x, const float* __restrict__ Q0,
-                                                     float* __restrict__ U, float* __restrict__ Qo, int R, int iters) {
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
+void lowrank_kernel(const float* __restrict__ x, const float* __restrict__ Q0, float* __restrict__ U,
+                    float* __restrict__ Qo, int R, int iters) {
   __shared__ QuantShared sh;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   const float* X = x + (long long)b * KD * VD;
   Tile t;                                             // t[c][v] = x[c][v]
 #pragma unroll
-  for (int mt = 0; mt < 2; ++mt)
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t.a[mt][nt][i] = X[(32 * w + 16 * mt + 4 * q + i) * VD + v];
-    }
+    for (int i = 0; i < 4; ++i) t.a[nt][i] = X[(16 * w + 4 * q + i) * VD + v];
+  }
   if (tid < VD) {
     f32x4 q0v;
     for (int r = 0; r < 4; ++r) q0v[r] = r < R ? Q0[tid * R + r] : 0.f;
     sh.qv[tid] = q0v;
   }
   __syncthreads();
-  f32x4 pc8[8];
   for (int it = 0; it < iters; ++it) {
-    colred(t, sh.qv, pc8);                            // P = x Q
-    if ((l & 15) == 0) {
-#pragma unroll
-      for (int k = 0; k < 8; ++k) sh.pp[32 * w + 16 * (k >> 2) + 4 * q + (k & 3)] = pc8[k];
-    }
+    colred(t, sh.qv, [&](int i, f32x4 s) { if ((l & 15) == 0) sh.pp[16 * w + 4 * q + i] = s; });   // P = x Q
     __syncthreads();
     if (w == 0) {
       f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
@@ -744,24 +809,34 @@ __global__ __launch_bounds__(FT) void lowrank_kernel(const float* __restrict__ x
     rowred(t, sh.pp, sh.qpart);                       // Q = x^T P
     __syncthreads();
     if (w == 0) {
-      f32x4 p0 = sh.qpart[0][l] + sh.qpart[1][l] + sh.qpart[2][l] + sh.qpart[3][l];
-      f32x4 p1 = sh.qpart[0][l + 64] + sh.qpart[1][l + 64] + sh.qpart[2][l + 64] + sh.qpart[3][l + 64];
+      f32x4 p0 = sum_parts(sh.qpart, l), p1 = sum_parts(sh.qpart, l + 64);
       mgs(p0, p1, R);
       sh.qv[l] = p0;
       sh.qv[l + 64] = p1;
     }
     __syncthreads();
   }
-  colred(t, sh.qv, pc8);                              // U = x Q
-  if ((l & 15) == 0) {
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const int c = 32 * w + 16 * (k >> 2) + 4 * q + (k & 3);
-      for (int r = 0; r < R; ++r) U[((long long)b * KD + c) * R + r] = pc8[k][r];
+  colred(t, sh.qv, [&](int i, f32x4 s) {              // U = x Q
+    if ((l & 15) == 0) {
+      const int c = 16 * w + 4 * q + i;
+      for (int r = 0; r < R; ++r) U[((long long)b * KD + c) * R + r] = s[r];
     }
-  }
+  });
   if (tid < VD)
     for (int r = 0; r < R; ++r) Qo[((long long)b * VD + tid) * R + r] = sh.qv[tid][r];
+}
+
+// compute units of the current device (cached per device; the persistent kernels size their grids by it)
+int num_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cache[dev] = n;
+  }
+  return cache[dev];
 }
 
 int check_block_state(const lq_state* st, bool need_buf) {
@@ -781,9 +856,10 @@ extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || (kda && !st->Gbuf)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  dim3 grid((unsigned)(N * st->HV));
-  if (kda) flush_kernel<true><<<grid, FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
-  else flush_kernel<false><<<grid, FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
+  const int total = N * st->HV;
+  const int g = total < 2 * num_cus() ? total : 2 * num_cus();   // persistent: two workgroups per CU at most
+  if (kda) flush_kernel<true><<<dim3((unsigned)g), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, N, qmax);
+  else flush_kernel<false><<<dim3((unsigned)g), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, N, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
