@@ -10,7 +10,9 @@ Measurement:
     replays of the decode loop.  The loop rotates NSET disjoint slot sets (> 1 GB of state) so the 256 MB MALL
     cannot hold the working set between uses of a set.
   * roofline of the dominant kernel (the step): algorithmic bytes per launch (layout-independent minimum) over the
-    average launch duration, from HIP events around graphs of 64 back-to-back step launches.
+    average launch duration, from HIP events around graph replays of step launches that rotate the same slot sets
+    (every window runs h = 0..63); traffic = the HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters
+    read for this same command, calibrated on the 64 MiB copies it ends with.
   * the same step on a dense bf16 state (`lq_dense_step`) as the baseline, and the CPU oracle on config 0.
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 128] [--no-cpu]
 """
@@ -43,6 +45,16 @@ def flush_bytes(N, HV, H, K, V, R, W, bits=8):
 
 def dense_bytes(N, HV, H, K, V, elem=2):
     return N * (HV * (2 * elem * V * K + 4 * V + 4) + H * 4 * K)
+
+
+def traffic_bytes():
+    """HBM bytes per step launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each scaled
+    by what the counter reads for the 64 MiB copies above (None when the summary is absent)."""
+    p = os.path.join(ROOT, "profiles", "gdn_step_B64_traffic.json")
+    if not os.path.exists(p):
+        return None
+    with open(p) as f:
+        return json.load(f).get("hbm_bytes_per_launch")
 
 
 def cpu_baseline(max_seconds=20.0):
@@ -81,11 +93,14 @@ def main():
     ap.add_argument("--warmup", type=int, default=128)
     ap.add_argument("--sets", type=int, default=8, help="disjoint slot sets rotated through (MALL defeat)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile-only", action="store_true", help="only the decode loop (for rocprofv3 runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path (the decode path shards heads across "
               "GPUs with no exchange step; see the design notes)", file=sys.stderr)
+        sys.exit(2)
+    if 64 % args.sets:
+        print("--sets must divide 64 (each graph of 64 launches gives every set the same number of steps)",
+              file=sys.stderr)
         sys.exit(2)
 
     import torch
@@ -144,7 +159,6 @@ def main():
 
     stream = torch.cuda.Stream()
     torch.cuda.synchronize()
-
     def capture(fn, n):
         gr = torch.cuda.CUDAGraph()
         with torch.cuda.graph(gr, stream=stream):
@@ -175,36 +189,33 @@ def main():
     torch.cuda.synchronize()
     ms_total = e0.elapsed_time(e1)
     us_per_step = ms_total * 1e3 / args.steps
-    if args.profile_only:
-        print(json.dumps({"profile_only": True, "us_per_step": us_per_step}))
-        return
 
-    # ---- step-only and flush timings per set (fresh windows): graphs of 64 step launches, then the flush ----
+    # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
+    # of the NSET sets 64 / NSET steps; NSET replays take every window from h = 0 to h = 64, then every head is due) ----
     lq.quantize(ssm, all_slots)                                   # every window back to h = 0
-    gsteps = [capture(lambda i, kk=kk: step_only(i, kk), CH) for kk in range(NSET)]
+    gsteps = capture(lambda i: step_only(i, i % NSET), CH)
     gflush = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
     gidle = capture(lambda i: flush_only(0), CH)                  # 64 flush launches with no head due
     torch.cuda.synchronize()
     rounds = 3
-    ev = [[(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True),
-            torch.cuda.Event(enable_timing=True)) for _ in range(NSET)] for _ in range(rounds)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(NSET + 2)] for _ in range(rounds)]
     with torch.cuda.stream(stream):
         for r in range(rounds):
+            ev[r][0].record(stream)
+            for _ in range(NSET):
+                gsteps.replay()
+            ev[r][1].record(stream)
             for kk in range(NSET):
-                a0, a1, a2 = ev[r][kk]
-                a0.record(stream)
-                gsteps[kk].replay()
-                a1.record(stream)
                 gflush[kk].replay()
-                a2.record(stream)
+                ev[r][kk + 2].record(stream)
         i0, i1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         i0.record(stream)
         gidle.replay()
         i1.record(stream)
     torch.cuda.synchronize()
-    st_ms = [ev[r][kk][0].elapsed_time(ev[r][kk][1]) for r in range(1, rounds) for kk in range(NSET)]
-    fl_ms = [ev[r][kk][1].elapsed_time(ev[r][kk][2]) for r in range(1, rounds) for kk in range(NSET)]
-    step_us = sum(st_ms) / len(st_ms) * 1e3 / CH
+    st_ms = [ev[r][0].elapsed_time(ev[r][1]) for r in range(1, rounds)]
+    fl_ms = [ev[r][kk + 1].elapsed_time(ev[r][kk + 2]) for r in range(1, rounds) for kk in range(NSET)]
+    step_us = sum(st_ms) / len(st_ms) * 1e3 / (CH * NSET)
     flush_due_us = sum(fl_ms) / len(fl_ms) * 1e3
     flush_idle_us = i0.elapsed_time(i1) * 1e3 / CH
     bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(CH)) / CH      # mean over h = 0..63
@@ -235,6 +246,15 @@ def main():
     bf16_gbps = dense_bytes(B, HV, H, K, V) / (bf16_us * 1e-6) / 1e9
     del gd, Sd
 
+    # ---- 8 copies of 64 MiB: the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters when this
+    # same command runs under rocprofv3 --pmc (bytes per launch of the step: profiles/gdn_step_B64_traffic.json) ----
+    src = torch.empty(64 * 2 ** 20 // 4, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(8):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+
     res = {
         "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": nw * CH, "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
@@ -247,7 +267,7 @@ def main():
         "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
         "speedup_vs_bf16_step": round(bf16_us / step_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(),
                      "kernel": "gdn_step_kernel<2>", "bytes_per_launch": int(bytes_step)},
     }
     if not args.no_cpu:
