@@ -16,7 +16,8 @@
  *        Pbuf f32  [NS][HV][KA]    GDN (KA = 1): decay of the checkpoint, init 1;  KDA (KA = K): cumulative log-gate, init 0
  *        Gbuf fp16 [NS][HV][L][K]  KDA only: per-entry step decay exp(g_j), init 1
  *        hcnt i32  [NS][HV]        valid entries in the window
- *   A row n of a call with idx[n] <= 0 is a padding row: its outputs are zero and no state is written.
+ *   A row n of a call with idx[n] <= 0 is a padding row: its outputs are zero and no state is written.  A slot
+ *   idx[n] >= NS (outside the cache) is treated the same way, so no index reaches memory outside the tensors.
  */
 #ifndef LQ_H
 #define LQ_H
@@ -78,7 +79,7 @@ int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* strea
  * iteration from Q0 [V][R] with CholeskyQR2, fp16 factors, smoothed residual requantised to codes in [-qmax, qmax]
  * (127: INT8; 31: 6-bit in the same int8 container), window reset.  Due heads are found on the device.
  * Replaces make_flush(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx)
- * (kernels.py:1077-2033, launched at state.py:115-116).  Requires K = V = 128, 1 <= L <= 64, R == 4. */
+ * (kernels.py:1077-2033, launched at state.py:115-116).  Requires K = V = 128, 1 <= L <= 64, 1 <= R <= 4. */
 int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream);
 
 /* Standalone quantize of the fp32 states of the slots idx[n] > 0 (read from the same ssm blocks the checkpoint then

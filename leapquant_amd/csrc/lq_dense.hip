@@ -15,7 +15,7 @@ __global__ __launch_bounds__(128 * G) void dense_step_kernel(void* S, int NS, in
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
   const int slot = io.idx[n];
-  if (slot <= 0) { out[lt] = 0; return; }
+  if (slot <= 0 || slot >= NS) { out[lt] = 0; return; }
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   float qv[16], kv[16];
 #pragma unroll

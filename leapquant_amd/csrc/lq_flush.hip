@@ -541,7 +541,7 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
       if (p < total) {
         const int n = p / HV, hv = p - n * HV;
         const int slot = idx[n];
-        due = slot > 0 && st.hcnt[(long long)slot * HV + hv] == L;
+        due = slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L;
       }
       const unsigned long long m = __ballot(due);
       if (threadIdx.x == 0) sh.due = m;
@@ -576,7 +576,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
   const int slot = idx[n];
-  if (slot <= 0) return;
+  if (slot <= 0 || slot >= st.NS) return;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   char* base = block_base(st, slot, hv);
@@ -706,7 +706,7 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
   const int slot = idx[n];
-  if (slot <= 0) return;
+  if (slot <= 0 || slot >= st.NS) return;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   char* base = block_base(st, slot, hv);

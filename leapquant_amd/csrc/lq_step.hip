@@ -4,11 +4,12 @@
 // and of the window buffer is described in include/lq.h.
 //
 // Mapping (MI355X-first, not the reference's persistent TMA/mbarrier pipeline): one workgroup per (row n, key head hk),
-// 128 threads per value head (G = HV / H value heads share the key head's q, k and buffered keys).  The int8 tile of a
-// value head (16 KiB) is streamed straight into registers with 16-byte loads, dequantised with the column scale folded
-// into the key/query operand, and both GEMVs (m = deq(Sq) k, y = deq(Sq) q) run in one pass on the VALU; each row is
-// owned by 8 lanes (16 columns each) whose partial sums meet in DPP reductions.  Only the h valid window rows are read,
-// and the buffered keys are read once per key head.  No MFMA: the step is ~1 flop/byte.
+// the G = HV / H value heads sharing the key head's q, k and buffered keys in the same workgroup, so the buffered keys
+// are read once per key head and only the h valid window rows are read.
+//   * GDN: two waves per value head; every dot product on the matrix cores (int8 MFMA for the two GEMVs against the
+//     16 KiB int8 tile, bf16 / fp16 MFMA for the window-key and factor dots), fed by 16-byte loads issued up front.
+//   * KDA: 128 threads per value head on the VALU; each tile row is owned by 8 lanes (16 columns each) whose partial
+//     sums meet in DPP reductions, the per-channel gate folded into the key operand.
 #include "lq_common.h"
 
 namespace {
@@ -123,7 +124,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
 
   const int slot = io.idx[n];
-  if (slot <= 0) {              // padding row (kernels.py:374-378)
+  if (slot <= 0 || slot >= st.NS) {   // padding row (kernels.py:374-378); a slot outside the cache counts as one
     out[lt] = 0;
     return;
   }
@@ -399,7 +400,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
   const int slot = io.idx[n];
-  if (slot <= 0) { out[lt] = 0; return; }
+  if (slot <= 0 || slot >= st.NS) { out[lt] = 0; return; }
   const long long sh_ = (long long)slot * HV + hv;
   const int h = st.hcnt[sh_];
   if (h >= L) { out[lt] = 0; return; }    // uniform over the workgroup
@@ -559,10 +560,12 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 
 static int check_step(const lq_state* st, const lq_step_io* io) {
   if (!st || !io) return LQ_ERR_ARG;
-  if (st->K != KD || st->V != VD || st->L < 1 || st->L > LMAX || st->R < 0 || st->R > 4) return LQ_ERR_ARG;
-  if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || io->N < 0) return LQ_ERR_ARG;
+  if (st->K != KD || st->V != VD || st->L < 1 || st->L > LMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0 || io->N < 0) return LQ_ERR_ARG;
   if (!st->ssm || !st->Kbuf || !st->Ubuf || !st->Wbuf || !st->Pbuf || !st->hcnt) return LQ_ERR_ARG;
-  if (st->slot_stride < (long long)st->HV * st->V * st->K) return LQ_ERR_ARG;
+  // 16-byte loads of the int8 rows and of the scale / factor block need a 16-byte aligned block start
+  if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3) || ((uintptr_t)st->ssm & 15))
+    return LQ_ERR_ARG;
   if (io->N > 0 && (!io->mixed || !io->a || !io->b || !io->A_log || !io->dt_bias || !io->idx || !io->out))
     return LQ_ERR_ARG;
   return LQ_OK;

@@ -33,8 +33,15 @@ def _stream(t):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+def _dev(t):
+    """Device address of a tensor; the kernels dereference it on the GPU, so a host tensor is an error here."""
+    if not t.is_cuda:
+        raise ValueError("liblq takes GPU tensors only, got a %s tensor" % t.device)
+    return t.data_ptr()
+
+
 def _p(t):
-    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+    return ctypes.c_void_p(_dev(t)) if t is not None else ctypes.c_void_p(0)
 
 
 def _need(t, dtype, shape, name):
@@ -56,8 +63,8 @@ def _check_dims(K, V, L, R):
 def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R):
     """lq_state of a layer: `Sq` is any view whose data pointer is the checkpoint of (slot 0, head 0), i.e. the fp32
     cache's data pointer."""
-    return _lib.LqState(Sq.data_ptr(), SS, Kbuf.data_ptr(), Ubuf.data_ptr(), Wbuf.data_ptr(), Pbuf.data_ptr(),
-                        Gbuf.data_ptr() if Gbuf is not None else 0, hcnt.data_ptr(), NS, HV, H, K, V, L, R)
+    return _lib.LqState(_dev(Sq), SS, _dev(Kbuf), _dev(Ubuf), _dev(Wbuf), _dev(Pbuf),
+                        _dev(Gbuf) if Gbuf is not None else 0, _dev(hcnt), NS, HV, H, K, V, L, R)
 
 
 def _check_view(Sq, NS, HV, V, K, SS):
@@ -69,8 +76,8 @@ def _check_view(Sq, NS, HV, V, K, SS):
 
 def _step_io(mixed, a, b, A_log, dt_bias, idx, o, scale):
     N = idx.shape[0]
-    return _lib.LqStepIO(mixed.data_ptr(), a.data_ptr(), b.data_ptr(), A_log.data_ptr(), dt_bias.data_ptr(),
-                         idx.data_ptr(), o.data_ptr(), N, float(scale))
+    return _lib.LqStepIO(_dev(mixed), _dev(a), _dev(b), _dev(A_log), _dev(dt_bias), _dev(idx), _dev(o), N,
+                         float(scale))
 
 
 def _check_step_inputs(N, HV, H, K, V, mixed, a, b, A_log, dt_bias, idx, o, KA):
@@ -204,7 +211,7 @@ def make_quantize(NS, HV, K, V, L, SS, R=4, ITERS=1, threads=128, qmax=QMAX):
         _need(Wbuf, torch.float32, (NS, HV, L), "Wbuf")
         _need(Q0, torch.float32, (V, R), "Q0")
         _need(idx, torch.int32, (N,), "idx")
-        st = _lib.LqState(S0.data_ptr(), SS, 0, 0, Wbuf.data_ptr(), Pbuf.data_ptr(), 0, hcnt.data_ptr(),
+        st = _lib.LqState(_dev(S0), SS, 0, 0, _dev(Wbuf), _dev(Pbuf), 0, _dev(hcnt),
                           NS, HV, HV, K, V, L, R)
         _lib.check(L_.lq_quantize(ctypes.byref(st), _p(Q0), _p(idx), N, ctypes.c_float(qmax), _stream(idx)),
                    "lq_quantize")

@@ -147,7 +147,7 @@ class LeapQuantState:
                        "lq_kda_step")
         else:
             _lib.check(L.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), stream), "lq_gdn_step")
-        _lib.check(L.lq_flush(ctypes.byref(st), ctypes.c_void_p(self.Q0.data_ptr()), ctypes.c_void_p(idx.data_ptr()),
+        _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx),
                               N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
 
     @property

@@ -12,9 +12,14 @@ def to_gpu(st, H=None, qmax=127.0, glb=0.0):
     H = st["Kbuf"].shape[1] if H is None else H
     L = st["Wbuf"].shape[-1]
     R = st["UQ"].shape[2]
-    kda = bool(st["kda"])
     ssm = torch.zeros(NS, HV, V, K, device=DEV)
-    lq = LeapQuantState(ssm, H, kda=kda, gate_lower_bound=glb, L=L, R=R, qmax=qmax)
+    lq = LeapQuantState(ssm, H, kda=bool(st["kda"]), gate_lower_bound=glb, L=L, R=R, qmax=qmax)
+    load_state(lq, ssm, st)
+    return ssm, lq
+
+
+def load_state(lq, ssm, st):
+    """Copy an oracle state into the checkpoint views of ssm and the window buffers of an existing LeapQuantState."""
     v = lq.views(ssm)
     v["Sq"].copy_(torch.from_numpy(st["Sq"]))
     v["Sk"].copy_(torch.from_numpy(st["Sk"]))
@@ -24,11 +29,10 @@ def to_gpu(st, H=None, qmax=127.0, glb=0.0):
     lq.Ubuf.copy_(torch.from_numpy(st["Ubuf"]).to(torch.bfloat16))
     lq.Wbuf.copy_(torch.from_numpy(st["Wbuf"]))
     lq.Pbuf.copy_(torch.from_numpy(st["Pbuf"]))
-    if kda:
+    if lq.kda:
         lq.Gbuf.copy_(torch.from_numpy(st["Gbuf"]))
     lq.hcnt.copy_(torch.from_numpy(st["hcnt"]))
     torch.cuda.synchronize()
-    return ssm, lq
 
 
 def from_gpu(ssm, lq):

@@ -1,0 +1,233 @@
+"""CPU tests of the drop-in boundary: liblq.so loads and exports exactly what include/lq.h declares, every entry point
+rejects bad arguments before touching the GPU, and the Python mirror of the reference API (leapquant/kernels.py,
+leapquant/state.py) checks shapes, devices and layouts the way the reference's asserts do.  No kernel is launched."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+import torch
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "lq.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from leapquant_amd import _lib
+    if not os.path.exists(_lib.LIB_PATH):
+        from leapquant_amd import build
+        build.build()
+    return _lib.lib()
+
+
+def declared():
+    src = open(HEADER).read()
+    return set(re.findall(r"^int\s+(lq_\w+)\s*\(", src, flags=re.M))
+
+
+def test_header_and_binding_agree():
+    from leapquant_amd import _lib
+    assert declared() == set(_lib.SIGNATURES)
+    m = re.search(r"#define\s+LQ_ABI_VERSION\s+(\d+)", open(HEADER).read())
+    assert int(m.group(1)) == _lib.ABI_VERSION
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from leapquant_amd import _lib
+    out = subprocess.run(["nm", "-D", "--defined-only", _lib.LIB_PATH], capture_output=True, text=True, check=True).stdout
+    exported = {ln.split()[-1] for ln in out.splitlines() if ln.strip()}
+    missing = declared() - exported
+    assert not missing, missing
+    for name in declared():
+        assert hasattr(lib, name)
+    assert lib.lq_abi_version() == _lib.ABI_VERSION
+
+
+def _state(**kw):
+    from leapquant_amd import _lib
+    d = dict(ssm=16, slot_stride=4 * 128 * 128, Kbuf=32, Ubuf=48, Wbuf=64, Pbuf=80, Gbuf=96, hcnt=112,
+             NS=8, HV=4, H=2, K=128, V=128, L=16, R=4)
+    d.update(kw)
+    return _lib.LqState(**d)
+
+
+def _io(**kw):
+    from leapquant_amd import _lib
+    d = dict(mixed=16, a=32, b=48, A_log=64, dt_bias=80, idx=96, out=112, N=0, scale=128 ** -0.5)
+    d.update(kw)
+    return _lib.LqStepIO(**d)
+
+
+BAD_STATES = [dict(K=64), dict(V=64), dict(L=0), dict(L=65), dict(R=0), dict(R=5), dict(H=0), dict(HV=3),
+              dict(NS=0), dict(slot_stride=100), dict(slot_stride=4 * 128 * 128 + 1), dict(ssm=8), dict(ssm=None),
+              dict(hcnt=None), dict(Wbuf=None)]
+
+
+@pytest.mark.parametrize("bad", BAD_STATES)
+def test_entry_points_reject_bad_state(lib, bad):
+    """N = 0 calls with one bad field: each entry point returns LQ_ERR_ARG (-1) without a launch."""
+    st = _state(**bad)
+    io = _io()
+    z = ctypes.c_void_p(0)
+    assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == -1
+    assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == -1
+    assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == -1
+    if "Kbuf" not in bad and "Ubuf" not in bad:
+        assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, ctypes.c_float(127.0),
+                               z) == -1
+
+
+def test_entry_points_accept_empty_calls(lib):
+    """A valid state with N = 0 rows is a no-op that succeeds (no HIP call is made)."""
+    st, io = _state(), _io()
+    z = ctypes.c_void_p(0)
+    assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == 0
+    assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == 0
+    assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1, ctypes.c_float(31.0), z) == 0
+    assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_lowrank(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 128, 128,
+                          4, 3, z) == 0
+
+
+def test_other_argument_errors(lib):
+    z = ctypes.c_void_p(0)
+    st = _state()
+    # rows but null input pointers
+    assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(_io(N=4, mixed=None)), z) == -1
+    assert lib.lq_gdn_step(None, ctypes.byref(_io()), z) == -1
+    assert lib.lq_gdn_step(ctypes.byref(st), None, z) == -1
+    # KDA needs Gbuf
+    assert lib.lq_kda_step(ctypes.byref(_state(Gbuf=None)), ctypes.byref(_io()), ctypes.c_float(0.0), z) == -1
+    assert lib.lq_flush(ctypes.byref(_state(Gbuf=None)), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1,
+                        ctypes.c_float(127.0), z) == -1
+    # GDN step: HV / H must be 1, 2 or 4
+    assert lib.lq_gdn_step(ctypes.byref(_state(HV=24, H=3)), ctypes.byref(_io(N=1)), z) == -1
+    # code range
+    for q in (0.5, 128.0, float("nan")):
+        assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 0, ctypes.c_float(q), z) == -1
+        assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 1, ctypes.c_float(q), z) == -1
+    assert lib.lq_flush(ctypes.byref(st), None, ctypes.c_void_p(16), 1, 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), -1, 0, ctypes.c_float(127.0), z) == -1
+    # lowrank limits
+    p = ctypes.c_void_p(16)
+    assert lib.lq_lowrank(p, p, p, p, 1, 64, 128, 4, 3, z) == -1
+    assert lib.lq_lowrank(p, p, p, p, 1, 128, 128, 5, 3, z) == -1
+    assert lib.lq_lowrank(p, p, p, p, 1, 128, 128, 4, 0, z) == -1
+    assert lib.lq_lowrank(None, p, p, p, 1, 128, 128, 4, 3, z) == -1
+    # dense baseline
+    io = _io()
+    assert lib.lq_dense_step(p, 2, 8, 4, 2, 128, 128, ctypes.byref(io), z) == -1
+    assert lib.lq_dense_step(None, 0, 8, 4, 2, 128, 128, ctypes.byref(io), z) == -1
+    assert lib.lq_dense_step(p, 0, 8, 4, 2, 128, 128, ctypes.byref(io), z) == 0
+
+
+def test_python_wrapper_raises_on_status():
+    from leapquant_amd import _lib
+    _lib.check(0, "x")
+    with pytest.raises(RuntimeError, match="bad argument"):
+        _lib.check(-1, "lq_gdn_step")
+    with pytest.raises(RuntimeError, match="HIP launch error"):
+        _lib.check(-2, "lq_flush")
+
+
+def test_state_views_alias_the_checkpoint_layout():
+    """state.py:29-40: Sq at byte 0, Sk at V K, Sv at V K + 4 K, UQ at V K + 4 K + 4 V of every (slot, head) block."""
+    from leapquant_amd.state import state_views
+    NS, HV, V, K, R = 3, 2, 128, 128, 4
+    ssm = torch.zeros(NS, HV, V, K)
+    v = state_views(ssm, R)
+    base = ssm.data_ptr()
+    blk = V * K * 4
+    for s in range(NS):
+        for h in range(HV):
+            o = base + (s * HV + h) * blk
+            assert v["Sq"][s, h].data_ptr() == o
+            assert v["q32"][s, h].data_ptr() == o
+            assert v["sq16"][s, h].data_ptr() == o
+            assert v["Sk"][s, h].data_ptr() == o + V * K
+            assert v["skv"][s, h].data_ptr() == o + V * K
+            assert v["Sv"][s, h].data_ptr() == o + V * K + 4 * K
+            assert v["uq"][s, h].data_ptr() == o + V * K + 4 * K + 4 * V
+    assert v["uq"].shape == (NS, HV, R, K + V) and v["uq"].dtype == torch.float16
+    # writes through the views land in the fp32 tensor's bytes and nowhere past the checkpoint
+    v["Sq"][1, 1].fill_(-1)
+    v["uq"][1, 1].fill_(1.0)
+    raw = ssm[1, 1].view(torch.uint8).reshape(-1)
+    end = V * K + 4 * K + 4 * V + 2 * R * (K + V)
+    assert int(raw[:V * K].ne(255).sum()) == 0
+    assert int(raw[end:].ne(0).sum()) == 0
+    assert int(ssm[0].view(torch.uint8).ne(0).sum()) == 0
+
+
+def test_state_rejects_what_the_reference_rejects(lib):
+    from leapquant_amd.state import LeapQuantState
+    with pytest.raises(AssertionError):
+        LeapQuantState(torch.zeros(2, 2, 128, 128, dtype=torch.float16), 2)
+    with pytest.raises(AssertionError):
+        LeapQuantState(torch.zeros(2, 2, 128, 256)[..., ::2], 2)        # inner dims not packed
+    st = LeapQuantState(torch.zeros(2, 4, 128, 128), 2, L=16)
+    assert st.Kbuf.shape == (2, 2, 16, 128) and st.Ubuf.shape == (2, 4, 16, 128)
+    assert float(st.Pbuf.min()) == 1.0 and st.hcnt.dtype == torch.int32
+    k = LeapQuantState(torch.zeros(2, 4, 128, 128), 4, kda=True, L=16)
+    assert k.Pbuf.shape == (2, 4, 128) and float(k.Pbuf.abs().max()) == 0.0
+    assert k.Gbuf.dtype == torch.float16 and float(k.Gbuf.min()) == 1.0
+    ref_q0 = torch.randn(128, 4, generator=torch.Generator().manual_seed(0))
+    assert torch.equal(st.Q0.cpu(), ref_q0)
+
+
+def test_host_tensors_never_reach_the_kernels(lib):
+    """The product path refuses host tensors (their addresses would be dereferenced on the GPU)."""
+    from leapquant_amd.state import LeapQuantState
+    ssm = torch.zeros(3, 4, 128, 128)
+    st = LeapQuantState(ssm, 2, L=16)
+    N = 2
+    mixed = torch.zeros(N, 2 * 2 * 128 + 4 * 128, dtype=torch.bfloat16)
+    a = torch.zeros(N, 4, dtype=torch.bfloat16)
+    b = torch.zeros(N, 4, dtype=torch.bfloat16)
+    out = torch.zeros(N, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="GPU tensors only"):
+        st.decode(ssm, mixed, a, b, torch.zeros(4), torch.zeros(4), torch.tensor([1, 2]), out)
+
+
+def test_factories_check_static_shapes(lib):
+    from leapquant_amd import kernels as KN
+    with pytest.raises(AssertionError):
+        KN.make_gdn_step(4, 32, 16, 64, 128, 16, 32 * 128 * 128)
+    with pytest.raises(AssertionError):
+        KN.make_gdn_step(4, 32, 16, 128, 128, 65, 32 * 128 * 128)
+    with pytest.raises(AssertionError):
+        KN.make_gdn_step(4, 24, 3, 128, 128, 16, 24 * 128 * 128)     # GQA 8
+    with pytest.raises(AssertionError):
+        KN.make_flush(4, 32, 128, 128, 16, 32 * 128 * 128, R=5)
+    # schedule knobs of the reference are accepted
+    KN.make_gdn_step(4, 32, 16, 128, 128, 16, 32 * 128 * 128, SMS=132, NSTAGE=6, NCG=3, NNW=2, MAXIT=128)
+    KN.make_flush(4, 32, 128, 128, 16, 32 * 128 * 128, SMS=132, NCG=3, MAXIT=128, PAD=8, MMT="bf16")
+    assert (KN.QMAX, KN.EPS, KN.SOFTPLUS_THRESHOLD) == (127.0, 1e-12, 20.0)
+
+
+def test_get_state_registry(lib):
+    """One LeapQuantState per cache tensor identity; a re-allocated cache drops the old buffers (state.py:172-189)."""
+    from leapquant_amd import state as S
+
+    class Layer:
+        pass
+
+    ssm = torch.zeros(2, 4, 128, 128)
+    l1, l2 = Layer(), Layer()
+    a = S.get_state(l1, ssm, H=2, L=16)
+    assert S.get_state(l1, ssm, H=2, L=16) is a
+    assert S.get_state(l2, ssm, H=2, L=16) is a               # two layers on one cache view share it
+    ssm2 = torch.zeros(2, 4, 128, 128)
+    b = S.get_state(l1, ssm2, H=2, L=16)
+    assert b is not a and b.key == S._ident(ssm2)
+
+    class PrefixLayer:
+        class cache_config:
+            mamba_cache_mode = "all"
+
+    with pytest.raises(RuntimeError, match="prefix caching"):
+        S.get_state(PrefixLayer(), torch.zeros(2, 4, 128, 128), H=2, L=16)
