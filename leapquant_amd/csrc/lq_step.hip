@@ -85,7 +85,7 @@ struct StepShared {
   bf16_t bkq[6][KD];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
   f16_t hkq[4][KD];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
   float2 mq[G][VD];        // GEMV rows (k, q) in digit units
-  float2 dkq[LMAX];        // (dk_j, dq_j) of buffered key j (shared by the key head)
+  float2 cwq[G][LMAX];     // (w_j dk_j, w_j dq_j) per value head: buffered entry j's coefficients in A4 / A5
   float2 duq[G][4];        // (dU_r, dQ_r) per value head, factor r
   float w[G][LMAX];        // gated entry weights w_j per value head
   float sc[G][8];          // per value head: alpha, beta, kappa, kmax, qmax
@@ -138,12 +138,10 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   const f16_t* UQp = (const f16_t*)(Svp + VD);
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   const long long sh_ = (long long)slot * HV + hv;
-  const int h = st.hcnt[sh_];
-  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
-  int hmax = h;
-#pragma unroll
-  for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, (int)st.hcnt[(long long)slot * HV + hk * G + g2]);
-  hmax = min(hmax, L);
+  // Window fills of the G value heads: a vector load (lane l reads head hk G + min(l, G - 1)), issued first.  Vector
+  // loads complete in order, so waiting for it waits for nothing issued later; a scalar load here would make the
+  // compiler wait for every scalar load in flight before the first use of any.
+  const int hlane = st.hcnt[(long long)slot * HV + hk * G + min(lane, G - 1)];
   float* Wp = st.Wbuf + sh_ * L;
   bf16_t kxr[2], qxr[2];
   float skx[2], wx[2];
@@ -158,28 +156,6 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   const bf16_t araw = ((const bf16_t*)io.a)[(long long)n * HV + hv];
   const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
   const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
-  __builtin_amdgcn_sched_barrier(0);   // keep the loads above ahead of the tile in issue order
-  i32x4 afr[4][2];              // the int8 tile (the long pole): A fragments, row 64 wi + 16 rt + n16
-  {
-    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
-  }
-  // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
-  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
-  bf16x8 kfr[KT][4];
-  {
-    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      const int j = 16 * (wv + 2 * G * t) + n16;
-      const int jr = j < hmax ? j : 0;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
-    }
-  }
   // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA (last wave)
   f16x8 ufr[4];
   const bool fwave = wv == 2 * G - 1;
@@ -195,8 +171,55 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   const float P = st.Pbuf[sh_];
+  __builtin_amdgcn_sched_barrier(0);   // the small loads above are issued before the wait for the window fills
+  const int h = __builtin_amdgcn_readlane(hlane, g);
+  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
+  int hmax = h;
+#pragma unroll
+  for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, __builtin_amdgcn_readlane(hlane, g2));
+  hmax = min(hmax, L);
+  // The big loads, in the order the work after them needs them: the window (values u_j into LDS, then the buffered
+  // keys), and the int8 tile last.  Everything built on the window -- key dots, A4 / A5 -- runs while the tile still
+  // streams; after the tile's last bytes only the GEMV, the delta rule and the stores remain.
+  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction (the loop holds no compiler-visible
+  // load, so it adds no wait)
+  {
+    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
+    const int nch = live ? (h + 3) >> 2 : 0;
+    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
+  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
+  bf16x8 kfr[KT][4];
+  {
+    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int j = 16 * (wv + 2 * G * t) + n16;
+      const int jr = j < hmax ? j : 0;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
+    }
+  }
+  i32x4 afr[4][2];              // the int8 tile: A fragments, row 64 wi + 16 rt + n16
+  {
+    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+  }
+  // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
+  // stores at the end, so this count is exact)
+  constexpr int AFTER_WINDOW = 4 * KT + 8;
+  __builtin_amdgcn_sched_barrier(0);
 
-  // ---- per value head scalar work, one wave (wi = 0): gate, beta, norms, digits, key-dot operands ----
+  // ---- per value head scalar work, one wave (wi = 0): gate, beta, norms, digits, key-dot operands.  Its global
+  //      writes (key append, gated weights) wait until the end, so that nothing joins the window / tile loads in the
+  //      vector memory counter before the window's wait ----
+  bf16_t kapp[2] = {0, 0};
+  float wjv[2] = {0.f, 0.f};
   if (wi == 0) {
     const float alpha = gdn_alpha_f(bf2f(araw), dtb, alog);
     const float beta = beta_f(bf2f(braw));
@@ -246,58 +269,19 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
           sh.hkq[2 * v2][c] = fh;
           sh.hkq[2 * v2 + 1][c] = f2h(xs64 - h2f(fh));
         }
-        if (live) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + c] = f2bf(kn[e]);   // key append
+        kapp[e] = f2bf(kn[e]);
       }
       const float wj = wx[e] * alpha;
-      if (live && c < h) {      // w_j = Wbuf[j] alpha (kernels.py:270-274), written back in place
-        sh.w[g][c] = wj;
-        Wp[c] = wj;
-      }
+      wjv[e] = wj;              // w_j = Wbuf[j] alpha (kernels.py:270-274), written back at the end
+      if (live && c < h) sh.w[g][c] = wj;
     }
     if (lane == 0) {
       sh.sc[g][0] = alpha; sh.sc[g][1] = beta; sh.sc[g][2] = kappa; sh.sc[g][3] = kmax; sh.sc[g][4] = qmax;
     }
   }
 
-  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction.  Straight-line code (a load loop
-  // makes the compiler wait for every load in flight): chunks past the window re-read chunk 0 (an L2 hit) into LDS
-  // rows >= h, which are never read.
-  {
-    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
-    const int nch = live ? (h + 3) >> 2 : 0;
-#pragma unroll
-    for (int i = 0; i < LMAX / 8; ++i) {
-      const int c = wi + 2 * i;
-      if (4 * c < L) lds_load16(ubg + (c < nch ? c : 0) * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
-    }
-  }
-  wait_vm();
-  __syncthreads();              // digits, dot operands, scalars, u_j rows and w_j are in LDS
+  __syncthreads();              // digits, dot operands, scalars and w_j are in LDS (the barrier waits for no global load)
 
-  // ---- int8 GEMV on the matrix cores.  B columns: 0 / 4 / 8 = k digits 0 / 1 / 2, 1 / 5 / 9 = q digits, others 0 ----
-  {
-    i32x4 bfr[2];
-    const int drow = (n16 & 3) * 3 + (n16 >> 2);              // table row of column n16 (valid for n16 < 10, n16 & 3 < 2)
-    const bool bcol = (n16 & 3) < 2 && n16 < 10;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const i32x4 b = *(const i32x4*)&sh.dig[g][bcol ? drow : 0][64 * ks + 16 * q4];
-      bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
-      i32x4 acc = {0, 0, 0, 0};
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][0], bfr[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][1], bfr[1], acc, 0, 0, 0);
-      // lane (n16, q4) holds rows 64 wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float c0 = (float)acc[i];
-        const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
-        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[g][64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
-      }
-    }
-  }
   // ---- buffered-key dots: this wave's K tiles against bf16 (hi, mid, lo) of kn (columns 0-2) and qn (4-6) ----
   {
     bf16x8 bk[4];
@@ -319,7 +303,10 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
         for (int i = 0; i < 4; ++i) {
           const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
           const int j = j0 + 4 * q4 + i;
-          if ((n16 == 0 || n16 == 4) && j < hmax) ((float*)&sh.dkq[j])[n16 >> 2] = s;
+          if ((n16 == 0 || n16 == 4) && j < hmax) {
+#pragma unroll
+            for (int g2 = 0; g2 < G; ++g2) ((float*)&sh.cwq[g2][j])[n16 >> 2] = sh.w[g2][j] * s;
+          }
         }
       }
     }
@@ -343,21 +330,19 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
       if ((n16 == 0 || n16 == 2) && m < G * R) ((float*)&sh.duq[m / R][m % R])[n16 >> 1] = s;
     }
   }
-  __syncthreads();
+  // this wave's u_j rows have landed in LDS (they precede the keys and the tile in the counter) ...
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
+  __syncthreads();              // ... and the other wave's, with the key and factor dots of every wave
   if (!live) { out[lt] = 0; return; }
 
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
   const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
-  const float2 mqr = sh.mq[g][lt];
-  const float mq = (mqr.x * (sh.sc[g][3] * (1.0f / DIGIT_SCALE))) * sv;
-  const float yq = (mqr.y * (sh.sc[g][4] * (1.0f / DIGIT_SCALE))) * sv;
   float a4 = 0.f, a5 = 0.f;
   for (int j = 0; j < h; ++j) {
     const float ub = bf2f(sh.ub[g][j][lt]);
-    const float wj = sh.w[g][j];
-    const float2 d = sh.dkq[j];
-    a4 = fmaf(ub, wj * d.x, a4);
-    a5 = fmaf(ub, wj * d.y, a5);
+    const float2 c = sh.cwq[g][j];
+    a4 = fmaf(ub, c.x, a4);
+    a5 = fmaf(ub, c.y, a5);
   }
   float a6 = 0.f, a7 = 0.f;
   for (int r = 0; r < R; ++r) {
@@ -365,6 +350,34 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     a6 = fmaf(qt[r], d.x, a6);
     a7 = fmaf(qt[r], d.y, a7);
   }
+  // ---- int8 GEMV on the matrix cores (the tile is the last data to arrive).  B columns: 0 / 4 / 8 = k digits 0 / 1 / 2, 1 / 5 / 9 = q digits, others 0 ----
+  {
+    i32x4 bfr[2];
+    const int drow = (n16 & 3) * 3 + (n16 >> 2);              // table row of column n16 (valid for n16 < 10, n16 & 3 < 2)
+    const bool bcol = (n16 & 3) < 2 && n16 < 10;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const i32x4 b = *(const i32x4*)&sh.dig[g][bcol ? drow : 0][64 * ks + 16 * q4];
+      bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      i32x4 acc = {0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][0], bfr[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][1], bfr[1], acc, 0, 0, 0);
+      // lane (n16, q4) holds rows 64 wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float c0 = (float)acc[i];
+        const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
+        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[g][64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
+      }
+    }
+  }
+  // rows 64 wi .. 64 wi + 63 of the GEMV are this wave's own rows: LDS round trip within the wave, no barrier
+  const float2 mqr = sh.mq[g][lt];
+  const float mq = (mqr.x * (sh.sc[g][3] * (1.0f / DIGIT_SCALE))) * sv;
+  const float yq = (mqr.y * (sh.sc[g][4] * (1.0f / DIGIT_SCALE))) * sv;
   const float pn = P * alpha;
   const float u = beta * (vin - (pn * (mq + a6) + a4));
   const float y = pn * (yq + a7) + a5 + kappa * u;
@@ -374,6 +387,14 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
+  }
+  if (wi == 0) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = lane + 64 * e;
+      if (g == 0) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + c] = kapp[e];   // key append
+      if (c < h) Wp[c] = wjv[e];
+    }
   }
 }
 
