@@ -400,13 +400,36 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
 
 // ------------------------------------------------------------------------------------------------------------------
 // KDA step  (kernels.py:694-1075): per-channel gate; decayed buffered keys; pc folded into the checkpoint operands.
-// One workgroup per (row n, value head hv), 128 threads.
+//
+// One workgroup of two waves per (row n, value head hv); wave wi owns tile rows 64 wi .. 64 wi + 63.  The window --
+// values u_j, keys K_j of the key head and the per-entry step decays e_j -- reaches LDS by direct global -> LDS loads
+// issued before the int8 tile, so the decay scan, the key dots and A4 / A5 run while the tile streams.
+//   * gate (kernels.py:704-712, 802, 887-896): g = glb sigmoid(e^A_log (a + dt_bias)) (glb != 0) or
+//     -e^A_log softplus(a + dt_bias); gn = P + g, pc = exp(gn), en = exp(g);
+//   * m = deq(Sq) diag(pc) kn, y = deq(Sq) diag(pc) qn: int8 MFMA against kf = kn Sk pc / 127, qf = qn Sk pc / 127 as
+//     three int8 digits each (kernels.py:900-901);
+//   * decayed keys K~_j = bf16(K_j en prod_{j<i<h} e_i) by a backward scan per channel (kernels.py:966-979), then
+//     dk_j = w_j K~_j kn, dq_j = w_j K~_j qn on bf16 MFMA (kn, qn in three bf16 terms; kernels.py:1031-1035);
+//   * dU_r = U^T_r (pc kn), dQ_r = U^T_r (pc qn) on fp16 MFMA (kernels.py:1036-1047);
+//   * u = beta (v - (m + A6 + A4)), y = y_q + A7 + A5 + kappa u (kernels.py:1065-1066).
 // ------------------------------------------------------------------------------------------------------------------
 struct KdaShared {
-  bf16_t kt[LMAX][KD];     // decayed keys  bf16(K_j * en * prod_{j<i<h} e_i)
-  float pc[KD];
-  float2 dkq[LMAX];
-  float2 duq[4];
+  bf16_t ub[LMAX][VD];      // window values u_j
+  union {
+    bf16_t kb[LMAX][KD];    // window keys K_j (of the key head), read by the decay scan only
+    struct {
+      float2 mq[VD];        // GEMV rows (k, q) in digit units
+      float2 cwq[LMAX];     // (w_j dk_j, w_j dq_j)
+    } post;                 // written after the scan
+  };
+  f16_t gk[LMAX][KD];       // window step decays e_j; the scan overwrites entry j with the decayed key K~_j (bf16)
+  int8_t dig[6][KD];        // int8 GEMV B operand: k digits 0-2, q digits 0-2
+  bf16_t bkq[6][KD];        // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
+  f16_t hkq[4][KD];         // factor-dot B operand: fp16 hi / lo of 64 pc kn, then of 64 pc qn
+  float2 duq[4];            // (dU_r, dQ_r)
+  float w[LMAX];            // entry weights w_j = Wbuf[j]
+  float en[KD];             // exp(g) per channel: the scan's first factor
+  float sc[8];              // beta, kappa, kmax, qmax
 };
 
 __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io io, float glb) {
@@ -417,163 +440,274 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   const int hv = blockIdx.x - n * HV;
   const int hk = hv / G;
   const int lt = threadIdx.x;
-  const int rg = lt >> 3, cc = lt & 7;
+  const int wi = __builtin_amdgcn_readfirstlane(lt >> 6);
+  const int lane = lt & 63;
+  const int n16 = lane & 15, q4 = lane >> 4;
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
   const int slot = io.idx[n];
-  if (slot <= 0 || slot >= st.NS) { out[lt] = 0; return; }
+  if (slot <= 0 || slot >= st.NS) { out[lt] = 0; return; }   // padding row (kernels.py:374-378)
   const long long sh_ = (long long)slot * HV + hv;
-  const int h = st.hcnt[sh_];
-  if (h >= L) { out[lt] = 0; return; }    // uniform over the workgroup
-
   const char* base = block_base(st, slot, hv);
-  uint4 code[8];
-  {
-    const uint4* cp = (const uint4*)base + (8 * rg) * 8 + cc;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) code[i] = cp[i * 8];
-  }
   const float* Skp = (const float*)(base + VD * KD);
   const float* Svp = Skp + KD;
   const f16_t* UQp = (const f16_t*)(Svp + VD);
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
-
-  // ---- per-channel gate for channel c = lt (kernels.py:704-712, 802, 887-896) ----
-  {
-    const int c = lt;
-    const double xg = (double)(bf2f(((const bf16_t*)io.a)[((long long)n * HV + hv) * KD + c]) + io.dt_bias[hv * KD + c]);
-    const double ea = exp((double)io.A_log[hv]);
-    double gdec;
-    if (glb != 0.f) gdec = (double)glb / (1.0 + exp(-ea * xg));
-    else gdec = -ea * softplus20(xg);
-    const float pb = st.Pbuf[sh_ * KD + c];
-    const float gn = (float)((double)pb + gdec);
-    const float pcv = (float)exp((double)gn);
-    const float en = (float)exp(gdec);
-    sh.pc[c] = pcv;
-    // decayed keys, backward over the live entries (entries j >= h carry e_j = 1 by the flush's reset)
-    const bf16_t* Kb = (const bf16_t*)st.Kbuf + (((long long)slot * H + hk) * L) * KD + c;
-    const f16_t* Gb = (const f16_t*)st.Gbuf + (sh_ * L) * KD + c;
-    float dcur = en;
-    for (int j = h - 1; j >= 0; --j) {
-      const float kb = bf2f(Kb[(long long)j * KD]);
-      sh.kt[j][c] = f2bf(kb * dcur);
-      dcur = dcur * h2f(Gb[(long long)j * KD]);
-    }
-    __syncthreads();
-    // state writes of the gate (after every lane has read its Pbuf / Gbuf entries)
-    st.Pbuf[sh_ * KD + c] = gn;
-    ((f16_t*)st.Gbuf)[(sh_ * L + h) * KD + c] = f2h(en);
-  }
-
-  float sk[16], pcl[16];
-  {
-    const float4* p = (const float4*)(Skp + 16 * cc);
+  // Window fill: a vector load (lane l reads head (hv + l) mod HV of the same slot; lane 0 the head itself), issued
+  // first so that waiting for it waits for nothing issued later.
+  const int hlane = st.hcnt[(long long)slot * HV + (hv + lane) % HV];
+  // per-channel operands of channels c = lane, lane + 64 (scalar wave) and of row lt (all lanes)
+  bf16_t kxr[2], qxr[2], axr[2];
+  float skx[2], dtx[2], pbx[2], wx[2];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float4 t = p[i];
-      sk[4 * i] = t.x; sk[4 * i + 1] = t.y; sk[4 * i + 2] = t.z; sk[4 * i + 3] = t.w;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) pcl[i] = sh.pc[16 * cc + i];
+  for (int e = 0; e < 2; ++e) {
+    const int c = lane + 64 * e;
+    kxr[e] = mrow[H * KD + hk * KD + c];
+    qxr[e] = mrow[hk * KD + c];
+    axr[e] = ((const bf16_t*)io.a)[((long long)n * HV + hv) * KD + c];
+    skx[e] = Skp[c];
+    dtx[e] = io.dt_bias[hv * KD + c];
+    pbx[e] = st.Pbuf[sh_ * KD + c];
+    wx[e] = st.Wbuf[sh_ * L + min(c, L - 1)];
   }
-  float qv[16], kv[16];
+  const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
+  const float alog = io.A_log[hv];
+  f16x8 ufr[4];                 // factor rows U^T_r (fp16): A fragment row m = r of the factor-dot MFMA
   {
-    const uint4* qp = (const uint4*)(mrow + hk * KD + 16 * cc);
-    const uint4* kp = (const uint4*)(mrow + H * KD + hk * KD + 16 * cc);
-    unpack8(qp[0], qv); unpack8(qp[1], qv + 8);
-    unpack8(kp[0], kv); unpack8(kp[1], kv + 8);
+    const int r = n16 < R ? n16 : 0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) ufr[ks] = *(const f16x8*)(UQp + r * (KD + VD) + 32 * ks + 8 * q4);
   }
   const float vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
-  const float beta = beta_of(bf2f(((const bf16_t*)io.b)[(long long)n * HV + hv]));
-
-  float nq = 0.f, nk = 0.f, nkq = 0.f;
+  float qt[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    nq = fmaf(qv[i], qv[i], nq);
-    nk = fmaf(kv[i], kv[i], nk);
-    nkq = fmaf(kv[i], qv[i], nkq);
-  }
-  nq = sum8(nq); nk = sum8(nk); nkq = sum8(nkq);
-  const float inq = rsqrt_rn((double)nq + LQ_NORM_EPS) * io.scale;
-  const float ink = rsqrt_rn((double)nk + LQ_NORM_EPS);
-  const float kappa = nkq * inq * ink;
-  float kn[16], qn[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) { kn[i] = kv[i] * ink; qn[i] = qv[i] * inq; }
-
-  // ---- decayed-key dots (w_j folded in, kernels.py:1031-1035) and pc-scaled factor dots (1036-1047) ----
-  const float* Wp = st.Wbuf + sh_ * L;
-  for (int t = rg; t < h + R; t += 16) {
-    float x[16];
-    if (t < h) {
-      const uint4* p = (const uint4*)(&sh.kt[t][16 * cc]);
-      unpack8(p[0], x); unpack8(p[1], x + 8);
-    } else {
-      const uint4* p = (const uint4*)(UQp + (t - h) * (KD + VD) + 16 * cc);
-      unpack8h(p[0], x); unpack8h(p[1], x + 8);
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] *= pcl[i];
-    }
-    float dk = 0.f, dq = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { dk = fmaf(x[i], kn[i], dk); dq = fmaf(x[i], qn[i], dq); }
-    dk = sum8(dk); dq = sum8(dq);
-    if (cc == 0) {
-      if (t < h) { const float w = Wp[t]; sh.dkq[t] = make_float2(w * dk, w * dq); }
-      else sh.duq[t - h] = make_float2(dk, dq);
+  for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
+  __builtin_amdgcn_sched_barrier(0);
+  const int h = __builtin_amdgcn_readlane(hlane, 0);
+  if (h >= L) { out[lt] = 0; return; }    // a full window is never stepped (the flush follows every step)
+  // window rows j < h straight to LDS, 1 KiB (4 rows) per wave instruction; then the int8 tile
+  {
+    const int nch = (h + 3) >> 2;
+    const char* ug = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
+    const char* kg = (const char*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD);
+    const char* gg = (const char*)((const f16_t*)st.Gbuf + sh_ * L * KD);
+    for (int c = wi; c < nch; c += 2) {
+      lds_load16(ug + c * 1024 + 16 * lane, (char*)&sh.ub[0][0] + c * 1024);
+      lds_load16(kg + c * 1024 + 16 * lane, (char*)&sh.kb[0][0] + c * 1024);
+      lds_load16(gg + c * 1024 + 16 * lane, (char*)&sh.gk[0][0] + c * 1024);
     }
   }
-
-  // ---- checkpoint stream with kf = kn Sk / 127 pc (kernels.py:900-901) ----
-  float kf[16], qf[16];
-  const float inv = 1.0f / LQ_QMAX;
+  __builtin_amdgcn_sched_barrier(0);
+  i32x4 afr[4][2];
+  {
+    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    kf[i] = ((kn[i] * sk[i]) * inv) * pcl[i];
-    qf[i] = ((qn[i] * sk[i]) * inv) * pcl[i];
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
   }
-  float mrow_[8], yrow_[8];
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    float m = 0.f, y = 0.f;
-    dot16_i8(code[i], kf, qf, m, y);
-    mrow_[i] = sum8(m);
-    yrow_[i] = sum8(y);
-  }
-  float mq = mrow_[0], yq = yrow_[0];
-#pragma unroll
-  for (int i = 1; i < 8; ++i) { if (cc == i) { mq = mrow_[i]; yq = yrow_[i]; } }
-  mq *= sv;
-  yq *= sv;
-  __syncthreads();
+  constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the window's LDS loads: the tile
+  __builtin_amdgcn_sched_barrier(0);
 
-  const bf16_t* Ub = (const bf16_t*)st.Ubuf + sh_ * L * VD + lt;
+  // ---- scalar wave: per-channel gate, norms, digits, dot operands ----
+  float gnv[2] = {0.f, 0.f}, env[2] = {0.f, 0.f};
+  if (wi == 0) {
+    const float ea = expf(alog);
+    const float beta = beta_f(bf2f(braw));
+    float pcv[2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const float xg = bf2f(axr[e]) + dtx[e];
+      const float g = glb != 0.f ? glb / (1.0f + expf(-ea * xg)) : -ea * softplus20f(xg);
+      gnv[e] = pbx[e] + g;
+      pcv[e] = expf(gnv[e]);
+      env[e] = expf(g);
+      sh.en[lane + 64 * e] = env[e];
+    }
+    const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
+    float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
+    nq = fmaf(qx[1], qx[1], nq); nk = fmaf(kx[1], kx[1], nk); nkq = fmaf(kx[1], qx[1], nkq);
+    nq = sum64(nq); nk = sum64(nk); nkq = sum64(nkq);
+    const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
+    const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
+    const float kappa = nkq * inq * ink;
+    const float inv = 1.0f / LQ_QMAX;
+    float kn[2], qn[2], kf[2], qf[2];
+    float kmax = 0.f, qmax = 0.f;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      kn[e] = kx[e] * ink;
+      qn[e] = qx[e] * inq;
+      kf[e] = ((kn[e] * skx[e]) * inv) * pcv[e];       // kernels.py:900-901
+      qf[e] = ((qn[e] * skx[e]) * inv) * pcv[e];
+      kmax = fmaxf(kmax, fabsf(kf[e]));
+      qmax = fmaxf(qmax, fabsf(qf[e]));
+    }
+    kmax = fmaxf(max64(kmax), 1e-30f);
+    qmax = fmaxf(max64(qmax), 1e-30f);
+    const float rk = 1.0f / kmax, rq = 1.0f / qmax;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = lane + 64 * e;
+      int8_t d0, d1, d2;
+      digits3(kf[e], rk, d0, d1, d2);
+      sh.dig[0][c] = d0; sh.dig[1][c] = d1; sh.dig[2][c] = d2;
+      digits3(qf[e], rq, d0, d1, d2);
+      sh.dig[3][c] = d0; sh.dig[4][c] = d1; sh.dig[5][c] = d2;
+      const float xs[2] = {kn[e], qn[e]};
+#pragma unroll
+      for (int v2 = 0; v2 < 2; ++v2) {
+        const float x = xs[v2];
+        const bf16_t hi = f2bf(x);
+        const float r1 = x - bf2f(hi);
+        const bf16_t mid = f2bf(r1);
+        const bf16_t lo = f2bf(r1 - bf2f(mid));
+        sh.bkq[3 * v2][c] = hi; sh.bkq[3 * v2 + 1][c] = mid; sh.bkq[3 * v2 + 2][c] = lo;
+        const float xs64 = (x * pcv[e]) * KSPLIT;
+        const f16_t fh = f2h(xs64);
+        sh.hkq[2 * v2][c] = fh;
+        sh.hkq[2 * v2 + 1][c] = f2h(xs64 - h2f(fh));
+      }
+      if (c < L) sh.w[c] = wx[e];
+    }
+    if (lane == 0) { sh.sc[0] = beta; sh.sc[1] = kappa; sh.sc[2] = kmax; sh.sc[3] = qmax; }
+  }
+  // this wave's window rows have landed in LDS (they precede only the tile in the counter) ...
+  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
+  __syncthreads();              // ... and the other wave's, with the gate, digits and dot operands
+
+  // ---- decay scan, channel c = lt, backward over the live entries, 8 entries per pass (reads first) ----
+  {
+    const int c = lt;
+    float dcur = sh.en[c];
+    int j1 = h;                 // entries j1 - 8 .. j1 - 1 in this pass
+    for (; j1 >= 8; j1 -= 8) {
+      float kbv[8], ev[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        kbv[i] = bf2f(sh.kb[j1 - 1 - i][c]);
+        ev[i] = h2f(sh.gk[j1 - 1 - i][c]);
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        ((bf16_t*)&sh.gk[j1 - 1 - i][0])[c] = f2bf(kbv[i] * dcur);
+        dcur = dcur * ev[i];
+      }
+    }
+    for (int j = j1 - 1; j >= 0; --j) {
+      const float kbv = bf2f(sh.kb[j][c]);
+      const float ev = h2f(sh.gk[j][c]);
+      ((bf16_t*)&sh.gk[j][0])[c] = f2bf(kbv * dcur);
+      dcur = dcur * ev;
+    }
+  }
+  __syncthreads();              // decayed keys of every channel are in LDS
+
+  // ---- decayed-key dots: 16-row tiles t = wi, wi + 2, ... of K~ against bf16 (hi, mid, lo) of kn (0-2), qn (4-6) ----
+  {
+    bf16x8 bk[4];
+    const bool bcol = (n16 & 3) < 3 && n16 < 8;
+    const int brow = bcol ? (n16 >> 2) * 3 + (n16 & 3) : 0;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 b = *(const bf16x8*)&sh.bkq[brow][32 * ks + 8 * q4];
+      bk[ks] = bcol ? b : bf16x8{};
+    }
+    for (int t = wi; 16 * t < h; t += 2) {
+      const int j0 = 16 * t;
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 a = *(const bf16x8*)((const bf16_t*)&sh.gk[j0 + n16][0] + 32 * ks + 8 * q4);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bk[ks], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
+        const int j = j0 + 4 * q4 + i;
+        if ((n16 == 0 || n16 == 4) && j < h) ((float*)&sh.post.cwq[j])[n16 >> 2] = sh.w[j] * s;
+      }
+    }
+  }
+  // ---- factor dots (wave 1): U^T rows against fp16 (hi, lo) of 64 pc kn (columns 0, 1) and 64 pc qn (2, 3) ----
+  if (wi == 1) {
+    f16x8 bh[4];
+    const bool bcol = n16 < 4;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 b = *(const f16x8*)&sh.hkq[bcol ? n16 : 0][32 * ks + 8 * q4];
+      bh[ks] = bcol ? b : f16x8{};
+    }
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ufr[ks], bh[ks], acc, 0, 0, 0);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s = (acc[i] + dpp<DPP_XOR1>(acc[i])) * (1.0f / KSPLIT);               // hi + lo (lanes 0 / 2)
+      const int r = 4 * q4 + i;
+      if ((n16 == 0 || n16 == 2) && r < R) ((float*)&sh.duq[r])[n16 >> 1] = s;
+    }
+  }
+  __syncthreads();              // key dots and factor dots are in LDS
+
+  // ---- row v = lt: buffered entries, rank-R part, then the GEMV (the tile arrives last) and the delta rule ----
   float a4 = 0.f, a5 = 0.f;
   for (int j = 0; j < h; ++j) {
-    const float ub = bf2f(Ub[(long long)j * VD]);
-    const float2 d = sh.dkq[j];
-    a4 = fmaf(ub, d.x, a4);
-    a5 = fmaf(ub, d.y, a5);
+    const float ubv = bf2f(sh.ub[j][lt]);
+    const float2 cc = sh.post.cwq[j];
+    a4 = fmaf(ubv, cc.x, a4);
+    a5 = fmaf(ubv, cc.y, a5);
   }
   float a6 = 0.f, a7 = 0.f;
   for (int r = 0; r < R; ++r) {
-    const float qt = h2f(UQp[r * (KD + VD) + KD + lt]);
-    a6 = fmaf(qt, sh.duq[r].x, a6);
-    a7 = fmaf(qt, sh.duq[r].y, a7);
+    const float2 d = sh.duq[r];
+    a6 = fmaf(qt[r], d.x, a6);
+    a7 = fmaf(qt[r], d.y, a7);
   }
+  {
+    i32x4 bfr[2];
+    const int drow = (n16 & 3) * 3 + (n16 >> 2);
+    const bool bcol = (n16 & 3) < 2 && n16 < 10;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const i32x4 b = *(const i32x4*)&sh.dig[bcol ? drow : 0][64 * ks + 16 * q4];
+      bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt) {
+      i32x4 acc = {0, 0, 0, 0};
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][0], bfr[0], acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][1], bfr[1], acc, 0, 0, 0);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float c0 = (float)acc[i];
+        const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
+        if (n16 == 8 || n16 == 9) ((float*)&sh.post.mq[64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
+      }
+    }
+  }
+  // rows 64 wi .. 64 wi + 63 of the GEMV are this wave's own rows: LDS round trip within the wave, no barrier
+  const float beta = sh.sc[0], kappa = sh.sc[1];
+  const float2 mqr = sh.post.mq[lt];
+  const float mq = (mqr.x * (sh.sc[2] * (1.0f / DIGIT_SCALE))) * sv;
+  const float yq = (mqr.y * (sh.sc[3] * (1.0f / DIGIT_SCALE))) * sv;
   const float u = beta * (vin - (mq + a6 + a4));        // kernels.py:1065
   const float y = yq + a7 + a5 + kappa * u;             // kernels.py:1066
   out[lt] = f2bf(y);
   ((bf16_t*)st.Ubuf)[(sh_ * L + h) * VD + lt] = f2bf(u);
-  if (hv % G == 0) {
-    const float kc = bf2f(mrow[H * KD + hk * KD + lt]) * ink;
-    ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + lt] = f2bf(kc);
-  }
+  if (hv % G == 0) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + lt] = sh.bkq[0][lt];   // bf16(kn)
   if (lt == 0) {
     st.Wbuf[sh_ * L + h] = 1.0f;
     st.hcnt[sh_] = h + 1;
+  }
+  if (wi == 0) {                // gate state (kernels.py:895-896)
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = lane + 64 * e;
+      st.Pbuf[sh_ * KD + c] = gnv[e];
+      ((f16_t*)st.Gbuf)[(sh_ * L + h) * KD + c] = f2h(env[e]);
+    }
   }
 }
 
