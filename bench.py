@@ -47,6 +47,171 @@ def dense_bytes(N, HV, H, K, V, elem=2):
     return N * (HV * (2 * elem * V * K + 4 * V + 4) + H * 4 * K)
 
 
+def kda_step_bytes(N, HV, K, V, R, h):
+    """Algorithmic bytes of one KDA step launch (HV = H) with h valid window entries per head: per (row, head) codes,
+    Sk/Sv, U^T|Q^T, v in / o out / u append, the per-channel gate (a in, dt_bias in, P read + write, e_h append),
+    q/k in, k append, scalars, and per window entry u_j, k_j, e_j, w_j."""
+    return N * HV * (V * K + 4 * (K + V) + 2 * R * (K + V) + 4 * V + 4 * K + (2 * V + 4 * K + 4) + 2 * K + 2 + 8 * K + 8
+                     + (2 * V + 4 * K + 4) * h)
+
+
+def quantize_bytes(n_heads, K, V):
+    """One standalone quantize: the fp32 state in, the checkpoint (codes, scales, factors) out."""
+    return n_heads * (4 * V * K + V * K + 4 * (K + V) + 2 * 4 * (K + V))
+
+
+def event_ms(torch, stream, fn, reps):
+    """Average duration of fn() (work on `stream`), from HIP events on that stream."""
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kda_bench(torch, dev, stream, capture):
+    """KDA decode (per-channel gate, Kimi form), B = 128, HV = H = 32, d = 128, W = 64, R = 4, int8
+    state; 4 rotated slot sets (> 1 GB).  Returns the amortised decode call (step + flush), the step alone (mean over
+    h = 0..63) and the flush with every head due."""
+    from leapquant_amd.state import LeapQuantState
+    B, HV, H, K, V, L, R = 128, 32, 32, 128, 128, 64, 4
+    NSET = 4
+    NS = B * NSET + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1002)
+    ssm = torch.empty(NS, HV, V, K, device=dev)
+    ssm.normal_(0.0, 0.02, generator=g)
+    lq = LeapQuantState(ssm, H, kda=True, L=L, R=R)
+    lq.quantize(ssm, torch.arange(1, NS, device=dev, dtype=torch.int32))
+    sets = [torch.arange(1 + B * k, 1 + B * (k + 1), device=dev, dtype=torch.int32) for k in range(NSET)]
+    pool = []
+    for _ in range(8):
+        q = torch.randn(B, H, K, device=dev, generator=g)
+        k = torch.randn(B, H, K, device=dev, generator=g)
+        q = q / q.norm(dim=-1, keepdim=True)
+        k = k / k.norm(dim=-1, keepdim=True)
+        v = torch.randn(B, HV, V, device=dev, generator=g)
+        mixed = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], 1).to(torch.bfloat16).contiguous()
+        gl = (-0.1 * torch.rand(B, HV * K, device=dev, generator=g)).clamp(max=-1e-4)
+        a = torch.log(torch.expm1(-gl)).to(torch.bfloat16)       # -softplus(a) = g (A_log = 0, dt_bias = 0)
+        b = torch.randn(B, HV, device=dev, generator=g).to(torch.bfloat16)
+        pool.append((mixed, a, b))
+    A_log = torch.zeros(HV, device=dev)
+    dt_bias = torch.zeros(HV * K, device=dev)
+    out = torch.empty(B, HV, V, device=dev, dtype=torch.bfloat16)
+    vw = lq.views(ssm)
+
+    def decode(i):
+        mixed, a, b = pool[i % 8]
+        lq.decode(ssm, mixed, a, b, A_log, dt_bias, sets[i % NSET], out)
+
+    def step_only(i):
+        mixed, a, b = pool[i % 8]
+        lq.kstep(vw["q32"], vw["Sk"], vw["Sv"], vw["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gbuf, lq.hcnt, mixed,
+                 a.reshape(B, HV, K), b, A_log, dt_bias, vw["uq"], sets[i % NSET], out)
+
+    def flush_only(kk):
+        lq.kflush(vw["q32"], vw["Sk"], vw["Sv"], vw["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gbuf, lq.hcnt,
+                  vw["sq16"], vw["uq"], lq.Q0, sets[kk])
+
+    CH = 64
+    gdec = capture(decode, CH)
+    for _ in range(2):
+        gdec.replay()
+    torch.cuda.synchronize()
+    decode_us = event_ms(torch, stream, gdec.replay, 8) * 1e3 / CH
+    # step alone: a graph of 64 steps gives each set 16; four replays take every window from h = 0 to h = 64, after
+    # which every head is due and the flush graphs reset them
+    lq.quantize(ssm, torch.arange(1, NS, device=dev, dtype=torch.int32))
+    gst = capture(step_only, CH)
+    gfl = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
+    torch.cuda.synchronize()
+    st_ms, fl_ms = [], []
+    for r in range(3):
+        st_ms.append(event_ms(torch, stream, gst.replay, 64 // (CH // NSET)))
+        for kk in range(NSET):
+            fl_ms.append(event_ms(torch, stream, gfl[kk].replay, 1))
+    step_us = sum(st_ms[1:]) / len(st_ms[1:]) * 1e3 / CH
+    flush_us = sum(fl_ms[NSET:]) / len(fl_ms[NSET:]) * 1e3
+    bytes_step = sum(kda_step_bytes(B, HV, K, V, R, h) for h in range(L)) / L
+    res = {"workload": "KDA decode, BASELINE config 2: B=128, HV=H=32, d=128, W=64, R=4, int8 state, %d rotated slot "
+                       "sets" % NSET,
+           "decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
+           "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1), "step_bytes_per_launch": int(bytes_step),
+           "flush_due_us": round(flush_us, 2)}
+    del gdec, gst, gfl, lq, ssm
+    torch.cuda.empty_cache()
+    return res
+
+
+def flush_quantize_bench(torch, dev, stream):
+    """standalone flush and quantize of 256 x 32 heads of 128 x 128 fp32 states with Student-t
+    (nu = 3, scale 0.02) entries; the flush with a full window (64 buffered entries) on every head; INT8 and 6-bit."""
+    from leapquant_amd import kernels as KN
+    from leapquant_amd.state import LeapQuantState
+    NSL, HV, H, K, V, L, R = 256, 32, 16, 128, 128, 64, 4
+    NS = NSL + 1
+    g = torch.Generator(device=dev)
+    g.manual_seed(1003)
+    S0 = torch.empty(NS, HV, V, K, device=dev)
+    for s0 in range(0, NS, 32):                      # Student-t(3) = z / sqrt(chi2_3 / 3), in chunks
+        sl = slice(s0, min(NS, s0 + 32))
+        z = torch.randn(S0[sl].shape, device=dev, generator=g)
+        c2 = sum(torch.randn(S0[sl].shape, device=dev, generator=g) ** 2 for _ in range(3))
+        S0[sl] = 0.02 * z / torch.sqrt(c2 / 3.0)
+    del z, c2
+    ssm = S0.clone()
+    slots = torch.arange(1, NS, device=dev, dtype=torch.int32)
+    nheads = NSL * HV
+    res = {"workload": "BASELINE config 3: 256 x 32 heads of 128 x 128 fp32 states, Student-t(3) x 0.02; flush with "
+                       "64 buffered entries on every head"}
+    for qmax, tag in ((127.0, "int8"), (31.0, "6bit")):
+        lq = LeapQuantState(ssm, H, L=L, R=R, qmax=qmax)
+        vw = lq.views(ssm)
+        quant = KN.make_quantize(NS, HV, K, V, L, ssm.stride(0), R=R, qmax=qmax)
+
+        def qrun():
+            quant(ssm, vw["Sq"], vw["Sk"], vw["Sv"], vw["uq"], lq.Wbuf, lq.Pbuf, lq.hcnt, lq.Q0, slots)
+
+        ts = []
+        for r in range(3):
+            ssm.copy_(S0)                            # the quantize overwrites its input with the checkpoint
+            torch.cuda.synchronize()
+            ts.append(event_ms(torch, stream, qrun, 1))
+        q_us = sum(ts[1:]) / 2 * 1e3
+        # a full window on every head: unit keys, values, gate products of U(-0.1, 0) log-gates
+        lq.Kbuf.copy_(torch.nn.functional.normalize(torch.randn(lq.Kbuf.shape, device=dev, generator=g), dim=-1))
+        lq.Ubuf.normal_(0.0, 0.02, generator=g)
+        lg = -0.1 * torch.rand(NS, HV, L, device=dev, generator=g)
+        w0 = torch.exp(torch.flip(torch.cumsum(torch.flip(lg, [2]), 2), [2]) - lg)   # prod of the later entries' gates
+        p0 = torch.exp(lg.sum(-1, keepdim=True))
+
+        def frun():
+            lq.kflush(vw["q32"], vw["Sk"], vw["Sv"], vw["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gd, lq.hcnt,
+                      vw["sq16"], vw["uq"], lq.Q0, slots)
+
+        tf = []
+        for r in range(3):
+            lq.Wbuf.copy_(w0)
+            lq.Pbuf.copy_(p0)
+            lq.hcnt.fill_(L)
+            torch.cuda.synchronize()
+            tf.append(event_ms(torch, stream, frun, 1))
+        f_us = sum(tf[1:]) / 2 * 1e3
+        fb = flush_bytes(NSL, HV, H, K, V, R, L)
+        res["quantize_%s_us" % tag] = round(q_us, 1)
+        res["quantize_%s_gbps" % tag] = round(quantize_bytes(nheads, K, V) / (q_us * 1e-6) / 1e9, 1)
+        res["flush_%s_us" % tag] = round(f_us, 1)
+        res["flush_%s_gbps" % tag] = round(fb / (f_us * 1e-6) / 1e9, 1)
+        del lq, vw
+    del S0, ssm
+    torch.cuda.empty_cache()
+    return res
+
+
 def traffic_bytes():
     """HBM bytes per step launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each scaled
     by what the counter reads for the 64 MiB copies above (None when the summary is absent)."""
@@ -255,6 +420,9 @@ def main():
     torch.cuda.synchronize()
     del src, dst
 
+    kda = kda_bench(torch, dev, stream, capture)
+    fq = flush_quantize_bench(torch, dev, stream)
+
     res = {
         "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
         "warmup": nw * CH, "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
@@ -270,6 +438,8 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(),
                      "kernel": "gdn_step_kernel<2>", "bytes_per_launch": int(bytes_step)},
     }
+    res["kda_config2"] = kda
+    res["flush_quantize_config3"] = fq
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))
