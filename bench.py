@@ -360,7 +360,7 @@ def main():
     lq.quantize(ssm, all_slots)                                   # every window back to h = 0
     gsteps = capture(lambda i: step_only(i, i % NSET), CH)
     gflush = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
-    gidle = capture(lambda i: flush_only(0), CH)                  # 64 flush launches with no head due
+    gidle = capture(lambda i: lq.flush(ssm, sets[0]), CH)         # 64 flush launches with no head due, as decode runs them
     torch.cuda.synchronize()
     rounds = 3
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(NSET + 2)] for _ in range(rounds)]

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 1
+#define LQ_ABI_VERSION 2
 
 enum lq_status {
   LQ_OK = 0,
@@ -45,6 +45,10 @@ typedef struct lq_state {
   void* Gbuf;             /* fp16 [NS][HV][L][K] (KDA) or NULL (GDN) */
   int* hcnt;              /* [NS][HV] */
   int NS, HV, H, K, V, L, R;
+  int* ctl;               /* optional (NULL: unused): int[2] = {heads made due since the last flush, flush workgroups
+                             done}, zero-initialised by the owner and kept by the kernels.  With it, the steps count the
+                             heads whose window they fill, and a flush that reads 0 returns at once instead of scanning
+                             hcnt; the last flush workgroup resets it.  Without it, the flush scans hcnt (the contract). */
 } lq_state;
 
 /* Decode inputs of one call: N rows, one token each. */

@@ -387,6 +387,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
+    if (st.ctl && h + 1 == L) atomicAdd(st.ctl, 1);   // this head is due: the flush that follows will not skip
   }
   if (wi == 0) {
 #pragma unroll
@@ -700,6 +701,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   if (lt == 0) {
     st.Wbuf[sh_ * L + h] = 1.0f;
     st.hcnt[sh_] = h + 1;
+    if (st.ctl && h + 1 == L) atomicAdd(st.ctl, 1);   // this head is due: the flush that follows will not skip
   }
   if (wi == 0) {                // gate state (kernels.py:895-896)
 #pragma unroll

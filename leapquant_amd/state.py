@@ -78,6 +78,9 @@ class LeapQuantState:
                      else torch.zeros(NS, HV, L, 1, device=dev))
         self.Gd = torch.zeros(1, 1, 1, 1, dtype=torch.bfloat16, device=dev)
         self.hcnt = torch.zeros(NS, HV, dtype=torch.int32, device=dev)
+        # heads made due by decode steps since the last flush / flush workgroups done: lets an idle flush return at
+        # once (kept by the kernels; zero between calls)
+        self.ctl = torch.zeros(2, dtype=torch.int32, device=dev)
         self.Q0 = torch.randn(V, R, generator=torch.Generator().manual_seed(0)).to(dev)
 
         if kda:
@@ -114,7 +117,7 @@ class LeapQuantState:
                 raise ValueError("the fp32 state cache must be 16-byte aligned with a slot stride divisible by 4")
             self._st = KN.state_struct(ssm, self.SS, self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf,
                                        self.Gbuf if self.kda else None, self.hcnt, self.NS, self.HV, self.H, self.K,
-                                       self.V, self.L, self.R)
+                                       self.V, self.L, self.R, ctl=self.ctl)
             self._skey = k
         return self._st
 
@@ -149,6 +152,16 @@ class LeapQuantState:
             _lib.check(L.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), stream), "lq_gdn_step")
         _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx),
                               N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
+
+    def flush(self, ssm, idx):
+        """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due counter lets a
+        flush with nothing due return at once)."""
+        idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        idx = idx.contiguous()
+        st = self._struct(ssm)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(idx.device).cuda_stream)
+        _lib.check(self._lib.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), idx.shape[0], 1 if self.kda else 0,
+                                      ctypes.c_float(self.qmax), stream), "lq_flush")
 
     @property
     def kstep_scale(self):
