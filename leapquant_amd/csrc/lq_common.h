@@ -17,12 +17,20 @@ typedef uint16_t f16_t;    // IEEE half bits
 // ---- scalar conversions ----------------------------------------------------------------------------------------
 __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-// fp32 -> bf16, round to nearest even (NaN kept quiet)
-__device__ __forceinline__ bf16_t f2bf(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t r = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  return (bf16_t)(((u & 0x7fffffffu) > 0x7f800000u) ? ((u >> 16) | 0x40u) : r);   // branch-free
+// fp32 -> bf16 / fp16, round to nearest even: the gfx950 conversions v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32
+typedef __bf16 lq_bf16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 lq_f16x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
+// two values in one word: lo in bits 0-15, hi in bits 16-31
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, lq_bf16x2{(__bf16)lo, (__bf16)hi});
 }
+__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, lq_f16x2{(_Float16)lo, (_Float16)hi});
+}
+// bf16 halves of a word as fp32
+__device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }
 
 __device__ __forceinline__ float h2f(f16_t h) { return (float)__builtin_bit_cast(_Float16, h); }

@@ -9,9 +9,11 @@
 // lane l holds
 //     acc[nt][i] = M[c][v],   c = 16 w + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
 // The window rebuild (a rank-L GEMM, ~29 flop/byte at L = 64) runs on MFMA with bf16 hi/lo operands exactly where the
-// reference splits; the rank-R subspace products, CholeskyQR2, residual, smoothing and requantisation are VALU work on
-// that layout with DPP / LDS reductions.  Due heads are found on the device (hcnt == L), so the fixed grid is
-// graph-capture safe.
+// reference splits.  The flush's rebuilt matrix B is fp16-exact, so every 128-long contraction of the subspace step
+// (P = B^T Q, Q = B P, the R x R Gram corrections, the rank-R residual updates) is an fp16 MFMA with fp32 accumulation
+// over operands held in registers: the packed tile itself is the B operand of v_mfma_f32_16x16x16_f16 (k = c), and one
+// MFMA against the identity gives the transposed packing (k = v).  Due heads are found on the device (hcnt == L), so
+// the fixed grid is graph-capture safe.
 #include "lq_common.h"
 
 namespace {
@@ -24,6 +26,21 @@ constexpr int NW = FT / 64;          // waves
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// D = A B + C over 16 x 16 blocks.  16x16x16: lane l holds A[l & 15][4 (l >> 4) + i] and B[4 (l >> 4) + i][l & 15];
+// 16x16x32: the same with 8 (l >> 4) + i; D (both): lane l holds D[4 (l >> 4) + i][l & 15], i < 4.
+__device__ __forceinline__ f32x4 mma16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x4 to_h4(f32x4 x) {
+  return f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+}
+__device__ __forceinline__ f32x4 from_h4(f16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
 
 struct Tile {
   f32x4 a[8];
@@ -33,17 +50,21 @@ struct FlushShared {
   union {
     bf16_t op[3][KD][OPS];     // rebuild operands [c or v][j]
     struct {                   // after the rebuild
-      f32x4 qpart[NW][VD];     // per-wave partials of the row reductions
-      float rowmax[NW][VD];
+      f32x4 qpart[NW][VD];     // per-wave partial Q rows
+      float rmx[4 * NW][VD];   // per-(wave, lane group) row maxima of the scaled residual
+      float rq[VD];            // qmax / row scale
+      f16_t ppT[4][KD];        // P16^T
     } r;
   };
   float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
   float svr[VD];               // row factor of the dequant (Sv pn / qmax, KDA: Sv / qmax)
   float w[LPMAX];
-  float uo[4][KD];             // old U^T (KDA: fp16(U^T pc)), rows >= R zero
-  float qo[4][VD];             // old Q^T, rows >= R zero
-  f32x4 qv[VD];                // current Q operand [v][r] (fp16-rounded Q0, then Q16); fp32 Q before CholeskyQR
-  f32x4 pp[KD];                // P16, then U16 [c][r]
+  f32x4 uoc[KD];               // old U rows [c][a] (KDA: fp16(U pc)), a >= R zero
+  f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
+  f16_t uoT[4][KD];            // the same, fp16 transposed (MFMA operands)
+  f16_t qoT[4][VD];
+  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
   unsigned long long due;      // persistent flush: due mask of the current candidate chunk
 };
 
@@ -121,18 +142,6 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
   }
 }
 
-// R x R product sum_x A[a][x] B[x][r] over 128 x (A row-major [4][128], B [128] of f32x4), every wave
-__device__ __forceinline__ void small_gram(const float (*A)[128], const f32x4* B, float M[4][4]) {
-  const int l = lane_id();
-  const f32x4 b0 = B[l], b1 = B[l + 64];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) {
-    const float a0 = A[a][l], a1 = A[a][l + 64];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) M[a][r] = sum64u(fmaf(a1, b1[r], a0 * b0[r]));
-  }
-}
-
 // CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835) on the 2 rows a lane of wave 0 holds
 __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
   float gg[10];
@@ -142,16 +151,16 @@ __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
 #pragma unroll
     for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
   float ll[10];
-  ll[0] = rsqrt_rn(fmaxf(gg[0], 1e-30f));
+  ll[0] = rsqrtf_rn(fmaxf(gg[0], 1e-30f));
   ll[1] = gg[1] * ll[0];
-  ll[2] = rsqrt_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
+  ll[2] = rsqrtf_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
   ll[3] = gg[3] * ll[0];
   ll[4] = (gg[4] - ll[3] * ll[1]) * ll[2];
-  ll[5] = rsqrt_rn(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
+  ll[5] = rsqrtf_rn(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
   ll[6] = gg[6] * ll[0];
   ll[7] = (gg[7] - ll[6] * ll[1]) * ll[2];
   ll[8] = (gg[8] - ll[6] * ll[3] - ll[7] * ll[4]) * ll[5];
-  ll[9] = rsqrt_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
+  ll[9] = rsqrtf_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     f32x4& p = s ? p1 : p0;
@@ -213,85 +222,91 @@ __device__ __forceinline__ void rebuild_mfma(Tile& t, const bf16_t (*A)[OPS], co
 }
 
 // Window rows of one head, loaded up front (unconditional, clamped addresses; rows >= h and the padding to LP carry
-// zero weight): item it = (row j = it % LP, 8-column chunk (it / LP)).  Two items per thread cover LP <= 64.
-constexpr int WIN_ITEMS = LPMAX * 16 / FT;
+// zero weight).  Thread t takes the row pair (2 jp, 2 jp + 1), jp = t % (LP / 2), in the 8-column chunk t / (LP / 2)
+// (16 chunks; LP = 64 keeps every thread busy), so that each LDS write below holds two entries.  KDA also takes the
+// window's per-channel decays (Gbuf, same [j][c] layout as the keys).
 struct WinRegs {
-  uint4 k[WIN_ITEMS], u[WIN_ITEMS];
+  uint4 k[2], u[2], g[2];
 };
+__device__ __forceinline__ int win_pair(int LP) { return opaque_tid() % (LP / 2); }
+__device__ __forceinline__ int win_chunk(int LP) { return opaque_tid() / (LP / 2); }
+template <bool KDA>
 __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int slot, int hv, int h, int LP) {
-  const int tid = opaque_tid();
   const int G = st.HV / st.H, hk = hv / G, L = st.L;
   const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD;
   const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * VD;
-  const int nit = LP * 16;
+  const f16_t* Gb = KDA ? (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD : nullptr;
+  const int jp = win_pair(LP), c8 = min(win_chunk(LP), 15) * 8;
 #pragma unroll
-  for (int k = 0; k < WIN_ITEMS; ++k) {
-    const int it = min(tid + FT * k, nit - 1);
-    const int j = it % LP, c8 = (it / LP) * 8;
-    const int jr = j < h ? j : 0;
+  for (int k = 0; k < 2; ++k) {
+    const int j = 2 * jp + k, jr = j < h ? j : 0;
     r.k[k] = *(const uint4*)(Kb + (long long)jr * KD + c8);
     r.u[k] = *(const uint4*)(Ub + (long long)jr * VD + c8);
+    if (KDA) r.g[k] = *(const uint4*)(Gb + (long long)jr * KD + c8);
   }
 }
-// GDN operands: op0[c][j] = K_j[c], op1 / op2 [v][j] = hi / lo of w_j u_j[v] (kernels.py:1501-1511); KDA: op2[v][j] = u_j[v]
-// (the KDA key operands are written by stage_kda_keys)
-__device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP, bool kda) {
-  const int tid = opaque_tid();
-  const int nit = LP * 16;
+// Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write.  GDN: op0 =
+// K_j[c], op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 = raw K_j[c] / e_j[c] (turned
+// into the decayed key operands by kda_key_scan), op2 = u_j[v].
+template <bool KDA>
+__device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP) {
+  const int ch = win_chunk(LP);
+  if (ch >= 16) return;
+  const int j0 = 2 * win_pair(LP), c8 = ch * 8;
+  const bool v0 = j0 < h, v1 = j0 + 1 < h;
+  const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
+  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+  const uint32_t ga[4] = {r.g[0].x, r.g[0].y, r.g[0].z, r.g[0].w}, gb[4] = {r.g[1].x, r.g[1].y, r.g[1].z, r.g[1].w};
+  const uint32_t keep = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
 #pragma unroll
-  for (int k = 0; k < WIN_ITEMS; ++k) {
-    const int it = min(tid + FT * k, nit - 1);
-    const int j = it % LP, c8 = (it / LP) * 8;
-    const float wj = j < h ? sh.w[j] : 0.f;
-    const uint32_t ku[4] = {r.k[k].x, r.k[k].y, r.k[k].z, r.k[k].w};
-    const uint32_t uu[4] = {r.u[k].x, r.u[k].y, r.u[k].z, r.u[k].w};
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bf16_t kb = (bf16_t)(ku[e >> 1] >> (16 * (e & 1)));
-      const bf16_t ub = (bf16_t)(uu[e >> 1] >> (16 * (e & 1)));
-      if (!kda) {
-        sh.op[0][c8 + e][j] = kb;
-        const float wu = wj * bf2f(ub);
-        const bf16_t hi = f2bf(wu);
-        sh.op[1][c8 + e][j] = hi;
-        sh.op[2][c8 + e][j] = f2bf(wu - bf2f(hi));
-      } else {
-        sh.op[2][c8 + e][j] = j < h ? ub : (bf16_t)0;
-      }
+  for (int e = 0; e < 8; ++e) {
+    const int x = e >> 1;
+    const bool odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
+    uint32_t* o0 = (uint32_t*)&sh.op[0][c8 + e][j0];
+    uint32_t* o1 = (uint32_t*)&sh.op[1][c8 + e][j0];
+    uint32_t* o2 = (uint32_t*)&sh.op[2][c8 + e][j0];
+    *o0 = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    if (!KDA) {
+      const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
+      const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+      const uint32_t hi = pk_bf16(wu0, wu1);
+      *o1 = hi;
+      *o2 = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+    } else {
+      *o1 = __builtin_amdgcn_perm(gb[x], ga[x], sel);
+      *o2 = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
     }
   }
 }
-// KDA key operands: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < L} e_i[c] (kernels.py:1453-1463).
-// Thread per channel c; the column's keys and decays come in batches of 16 entries (loads first, then the scan).
-__device__ __forceinline__ void stage_kda_keys(FlushShared& sh, const lq_state& st, int slot, int hv, int h, int LP) {
+// KDA key operands, in place: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c]
+// (kernels.py:1453-1463; the running product is taken backwards from the last entry, as there).  Thread per channel c,
+// 8 entries per LDS access.
+__device__ __forceinline__ void kda_key_scan(FlushShared& sh, int h, int LP) {
   const int c = opaque_tid();
   if (c >= KD) return;
-  const int G = st.HV / st.H, hk = hv / G, L = st.L;
-  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD + c;
-  const f16_t* Gb = (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD + c;
   float dcur = 1.0f;
-  for (int j0 = LP - 16; j0 >= 0; j0 -= 16) {
-    bf16_t kr[16];
-    f16_t er[16];
+  for (int j0 = LP - 8; j0 >= 0; j0 -= 8) {
+    const uint4 kr = *(const uint4*)&sh.op[0][c][j0];
+    const uint4 er = *(const uint4*)&sh.op[1][c][j0];
+    const uint32_t ku[4] = {kr.x, kr.y, kr.z, kr.w};
+    const uint32_t eu[4] = {er.x, er.y, er.z, er.w};
+    uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const int j = j0 + e, jr = j < h ? j : 0;
-      kr[e] = Kb[(long long)jr * KD];
-      er[e] = Gb[(long long)jr * KD];
-    }
-#pragma unroll
-    for (int e = 15; e >= 0; --e) {
+    for (int e = 7; e >= 0; --e) {
       const int j = j0 + e;
-      bf16_t hi = 0, lo = 0;
-      const float kd = bf2f(kr[e]) * (sh.w[j] * dcur);
       if (j < h) {
-        hi = f2bf(kd);
-        lo = f2bf(kd - bf2f(hi));
-        dcur = dcur * h2f(er[e]);
+        const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j] * dcur);
+        const bf16_t hi = f2bf(kd);
+        const bf16_t lo = f2bf(kd - bf2f(hi));
+        hw[e >> 1] |= (uint32_t)hi << (16 * (e & 1));
+        lw[e >> 1] |= (uint32_t)lo << (16 * (e & 1));
+        dcur = dcur * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
       }
-      sh.op[0][c][j] = hi;
-      sh.op[1][c][j] = lo;
     }
+    *(uint4*)&sh.op[0][c][j0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+    *(uint4*)&sh.op[1][c][j0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
   }
 }
 
@@ -312,12 +327,50 @@ __device__ __forceinline__ float max_parts(const float (*part)[VD], int v) {
 // ------------------------------------------------------------------------------------------------------------------
 // flush (kernels.py:1077-2033): one due (slot, head)
 // ------------------------------------------------------------------------------------------------------------------
+// P = B^T Q + pn U_old (Q_old^T Q) for this wave's 16 key channels, fp16-rounded (kernels.py:1580-1700).  Q^T comes
+// from sh.qT; bt[nt] is the transposed packing of B (lane l: B[16 w + (l & 15)][16 nt + 4 (l >> 4) + i]).  Lanes
+// l < 16 return P[16 w + l][0..3] (zero for r >= R); the other lanes return zeros.
+__device__ __forceinline__ f32x4 p_step(const FlushShared& sh, const f16x4 bt[8], float pn, int R) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x8 z8 = {};
+  const f16x4 z4 = {};
+  // M[a][r] = sum_v Q_old[v][a] Q[v][r]: lanes l < 4 hold column r = l
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 ao = rl4 ? *(const f16x8*)&sh.qoT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
+    macc = mma32(ao, bq, macc);
+  }
+  // P^T[r][c] = sum_v Q^T[r][v] B[c][v]  (k = v from the transposed packing)
+  f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+    pacc = mma16(aq, bt[nt], pacc);
+  }
+  float M[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+  const f32x4 uo = sh.uoc[16 * w + l16];
+  f32x4 p;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
+    p[r] = (q == 0 && r < R) ? hround(pacc[r] + pn * corr) : 0.f;
+  }
+  return p;
+}
+
 template <bool KDA>
 __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                            float qmax) {
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
-  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
   char* base = block_base(st, slot, hv);
   int8_t* Sq = (int8_t*)base;
   float* Sk = (float*)(base + VD * KD);
@@ -343,83 +396,106 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window(win, st, slot, hv, L, LP);
+  load_window<KDA>(win, st, slot, hv, L, LP);
   uint32_t wds[8];
   load_code_words(wds, Sq);
 
   if (tid < KD) {
     const int c = cv;
     float pcv = 1.f;
-    if (KDA) pcv = (float)exp((double)pbc);                                          // kernels.py:1451
+    if (KDA) pcv = expf(pbc);                                                          // kernels.py:1451
     sh.skl[c] = KDA ? scv * pcv : scv;                                                // kernels.py:1519
+    f32x4 u;
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      float u = a < R ? uqv[a] : 0.f;
-      if (KDA) u = hround(u * pcv);                                                   // kernels.py:1464-1465
-      sh.uo[a][c] = u;
+      u[a] = a < R ? uqv[a] : 0.f;
+      if (KDA) u[a] = hround(u[a] * pcv);                                             // kernels.py:1464-1465
+      sh.uoT[a][c] = f2h(u[a]);
     }
+    sh.uoc[c] = u;
   } else if (tid < KD + VD) {
     const int v = cv;
     sh.svr[v] = KDA ? scv * (1.0f / qmax) : scv * (pn / qmax);                       // kernels.py:1468, 1483
+    f32x4 o;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) sh.qo[a][v] = a < R ? uqv[a] : 0.f;
-    f32x4 q0;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) q0[r] = r < R ? hround(q0v[r]) : 0.f;             // kernels.py:1573-1577
-    sh.qv[v] = q0;
+    for (int a = 0; a < 4; ++a) {
+      o[a] = a < R ? uqv[a] : 0.f;
+      sh.qoT[a][v] = f2h(o[a]);
+      sh.qT[a][v] = f2h(a < R ? hround(q0v[a]) : 0.f);                                // kernels.py:1573-1577
+    }
+    sh.qov[v] = o;
   }
   if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
   __syncthreads();
-  store_window(sh, win, L, LP, KDA);
-  if (KDA) stage_kda_keys(sh, st, slot, hv, L, LP);
+  store_window<KDA>(sh, win, L, LP);
   __syncthreads();
+  if (KDA) {
+    kda_key_scan(sh, L, LP);
+    __syncthreads();
+  }
 
   // ---- stage 2: B = deq(S0) (+ decay) + window, fp16 (kernels.py:1483-1571) ----
-  Tile t;
-  tile_from_words(t, wds, sh.svr, sh.skl);
-  if (!KDA) {
-    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
-    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
-  } else {
-    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
-    rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
+  f16x4 bh[8], bt[8];                                 // B packed: k = c (tile layout) and k = v (transposed)
+  {
+    Tile t;
+    tile_from_words(t, wds, sh.svr, sh.skl);
+    if (!KDA) {
+      rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+    } else {
+      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+      rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
+    }
+    f16x4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      bh[nt] = to_h4(t.a[nt]);                        // the fp16 rounding of B
+      bt[nt] = to_h4(mma16(bh[nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));   // exact: B^T block through the identity
+    }
   }
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(t.a[nt][i]);
 
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
-  // P = B^T Q + pn U_old (Q_old^T Q), fp16
-  auto p_step = [&]() {
-    float M[4][4];
-    small_gram(sh.qo, sh.qv, M);                      // Q_old^T Q (every wave)
-    colred(t, sh.qv, [&](int i, f32x4 s) {
-      const int c = 16 * w + 4 * q + i;
-      if ((l & 15) == 0) {
-        f32x4 p;
+  const f32x4 p16 = p_step(sh, bt, pn, R);            // P16 rows of this wave (lanes < 16)
+  __syncthreads();                                    // every wave is past the rebuild: the op region is free
+  // Q = B P16 + pn Q_old (U_old^T P16): per-wave partials of B P16 over the wave's 16 channels, summed below
+  if (q == 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const float corr = sh.uo[0][c] * M[0][r] + sh.uo[1][c] * M[1][r] + sh.uo[2][c] * M[2][r] + sh.uo[3][c] * M[3][r];
-          p[r] = r < R ? hround(s[r] + pn * corr) : 0.f;
-        }
-        sh.pp[c] = p;
-      }
-    });
-  };
-  p_step();
-  __syncthreads();                                    // P16 complete; every wave is past the rebuild (op region free)
-  // Q = B P16 + pn Q_old (U_old^T P16)
-  rowred(t, sh.pp, sh.r.qpart);
-  float M2[4][4];
-  small_gram(sh.uo, sh.pp, M2);
+    for (int r = 0; r < 4; ++r) sh.r.ppT[r][16 * w + l16] = f2h(p16[r]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  {
+    const f16x4 z4 = {};
+    const f16x4 ap = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][16 * w + 4 * q] : z4;   // A[r][c] = P16^T
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f32x4 d = mma16(ap, bh[nt], f32x4{0.f, 0.f, 0.f, 0.f});                 // Q^T[r][16 nt + l]
+      if (q == 0) sh.r.qpart[w][16 * nt + l16] = d;
+    }
+  }
   __syncthreads();
-  if (tid < VD) {
+  if (tid < VD) {                                     // waves 0 and 1: one row v per thread
+    // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels (every column of P16 is in ppT now)
+    const f16x8 z8 = {};
+    f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.uoT[l16][32 * ks + 8 * q] : z8;
+      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
+      macc = mma32(ao, bp, macc);
+    }
+    float M2[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
     const int v = tid;
     f32x4 s = sum_parts(sh.r.qpart, v);
+    const f32x4 qo = sh.qov[v];
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      s[r] += pn * (sh.qo[0][v] * M2[0][r] + sh.qo[1][v] * M2[1][r] + sh.qo[2][v] * M2[2][r] + sh.qo[3][v] * M2[3][r]);
+    for (int r = 0; r < 4; ++r) s[r] += pn * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
     sh.qv[v] = s;
   }
   __syncthreads();
@@ -431,49 +507,60 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
     cholqr_pass(p0, p1);
     cholqr_pass(p0, p1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { p0[r] = r < R ? hround(p0[r]) : 0.f; p1[r] = r < R ? hround(p1[r]) : 0.f; }
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = r < R ? hround(p0[r]) : 0.f;
+      p1[r] = r < R ? hround(p1[r]) : 0.f;
+      sh.qT[r][l] = f2h(p0[r]);
+      sh.qT[r][l + 64] = f2h(p1[r]);
+    }
     sh.qv[l] = p0;
     sh.qv[l + 64] = p1;
   }
   __syncthreads();
-  p_step();                                           // U16 = P step with Q16
-  __syncthreads();
+  const f32x4 u16 = p_step(sh, bt, pn, R);            // U16 = P step with Q16 (lanes < 16: rows 16 w + l)
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
+  Tile t;
+  {
+    const f16x4 z4 = {};
+    const f16x4 auo = q == 0 ? to_h4(sh.uoc[16 * w + l16]) : z4;                     // A[c][a] = U_old
+    const f16x4 aun = q == 0 ? to_h4(-u16) : z4;                                     // A[c][r] = -U16
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const int v = 16 * nt + (l & 15);
-    const f32x4 qnv = sh.qv[v];
-    const f32x4 qov = f32x4{sh.qo[0][v], sh.qo[1][v], sh.qo[2][v], sh.qo[3][v]};
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                               // B[a][v] = Q_old^T
+      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                                // B[r][v] = Q16^T
+      f32x4 e = from_h4(bh[nt]);
+      if (!KDA) e *= rpn;
+      e = mma16(auo, bqo, e);
+      if (!KDA) e *= pn;
+      e = mma16(aun, bqn, e);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = 16 * w + 4 * q + i;
-      const f32x4 unc = sh.pp[c];
-      float e = KDA ? t.a[nt][i] : t.a[nt][i] * rpn;
-      e = fmaf(qov[0], sh.uo[0][c], e);
-      e = fmaf(qov[1], sh.uo[1][c], e);
-      e = fmaf(qov[2], sh.uo[2][c], e);
-      e = fmaf(qov[3], sh.uo[3][c], e);
-      if (!KDA) e = e * pn;
-      e = fmaf(-qnv[0], unc[0], e);
-      e = fmaf(-qnv[1], unc[1], e);
-      e = fmaf(-qnv[2], unc[2], e);
-      e = fmaf(-qnv[3], unc[3], e);
-      t.a[nt][i] = hround(e);
+      for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(e[i]);
     }
   }
 
   // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
   float rsk[4];
+  {
+    float cs[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    float s = 0.f;
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.f;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) s += fabsf(t.a[nt][i]);
-    s = sum16(s);
-    const float msum = s * (1.0f / VD);
-    rsk[i] = fminf(rsqrtf_rn(msum), 1.0f / LQ_EPS);
-    if ((l & 15) == 0) Sk[16 * w + 4 * q + i] = fmaxf(sqrtf(msum), LQ_EPS);
+      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[nt][i]);
+      cs[i] = sum16(x);
+    }
+    // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
+    const int ic = l & 3;
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / VD);
+    const float sq = sqrtf(msum);
+    const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
+    if (l16 < 4) Sk[16 * w + 4 * q + l16] = fmaxf(sq, LQ_EPS);
+    rsk[0] = dpp<0x00>(rs);                           // quad_perm [i, i, i, i]: column i of the lane's quad
+    rsk[1] = dpp<0x55>(rs);
+    rsk[2] = dpp<0xaa>(rs);
+    rsk[3] = dpp<0xff>(rs);
   }
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
@@ -484,37 +571,39 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
       t.a[nt][i] *= rsk[i];
       m = fmaxf(m, fabsf(t.a[nt][i]));
     }
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    if (q == 0) sh.r.rowmax[w][16 * nt + (l & 15)] = m;
+    sh.r.rmx[4 * w + q][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  if (tid < VD) {
+    float m = sh.r.rmx[0][tid];
+#pragma unroll
+    for (int k = 1; k < 4 * NW; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
+    const float rmax = fmaxf(m, LQ_EPS);
+    Sv[tid] = rmax;
+    sh.r.rq[tid] = qmax * (1.0f / rmax);
   }
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    const int v = 16 * nt + (l & 15);
-    const float rmax = fmaxf(max_parts(sh.r.rowmax, v), LQ_EPS);
-    const float rq = qmax * (1.0f / rmax);
-    if (w == 0 && q == 0) Sv[v] = rmax;
-    uint32_t word = 0;
+    const int v = 16 * nt + l16;
+    const float rq = sh.r.rq[v];
+    uint32_t b[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const uint32_t bits = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
-      word |= (bits & 0xffu) << (8 * i);
-    }
-    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = word;
+    for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
-  if (tid < KD) {
-    const int c = tid;
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + c] = f2h(sh.pp[c][r]);
-    if (KDA) {
-      st.Pbuf[sh_ * KD + c] = 0.f;
-      f16_t* Gb = (f16_t*)st.Gbuf + sh_ * L * KD + c;
-      for (int j = 0; j < L; ++j) Gb[(long long)j * KD] = 0x3c00;   // fp16 1.0
-    }
-  } else if (tid < KD + VD) {
-    const int v = tid - KD;
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
+  if (q == 0) {
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + 16 * w + l16] = f2h(u16[r]);
+  }
+  if (tid < VD) {
+    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + tid] = f2h(sh.qv[tid][r]);
+  }
+  if (KDA) {
+    if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
+    uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
+    for (int i = tid; i < L * KD / 8; i += FT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {
@@ -734,19 +823,22 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window(win, st, slot, hv, h, LP);
+  load_window<false>(win, st, slot, hv, h, LP);
   uint32_t wds[8];
   load_code_words(wds, Sq);
+  f32x4 fac;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
   if (tid < KD) {
     sh.skl[cv] = scv;
-    for (int a = 0; a < 4; ++a) sh.uo[a][cv] = a < R ? uqv[a] : 0.f;
+    sh.uoc[cv] = fac;
   } else if (tid < KD + VD) {
     sh.svr[cv] = scv;
-    for (int a = 0; a < 4; ++a) sh.qo[a][cv] = a < R ? uqv[a] : 0.f;
+    sh.qov[cv] = fac;
   }
   if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
   __syncthreads();
-  store_window(sh, win, h, LP, false);
+  store_window<false>(sh, win, h, LP);
   Tile t;
   {
     const float inv = 1.0f / qmax;
@@ -755,12 +847,14 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + (l & 15);
       const float rv = sh.svr[v];
+      const f32x4 qo = sh.qov[v];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int c = c0 + i;
+        const f32x4 uo = sh.uoc[c];
         float x = (((float)(int)(int8_t)(wds[nt] >> (8 * i)) * inv) * sh.skl[c]) * rv;   // kernels.py:2107
 #pragma unroll
-        for (int a = 0; a < 4; ++a) x = fmaf(sh.qo[a][v], sh.uo[a][c], x);            // kernels.py:2109-2111
+        for (int a = 0; a < 4; ++a) x = fmaf(qo[a], uo[a], x);                         // kernels.py:2109-2111
         t.a[nt][i] = x * P;                                                             // kernels.py:2113
       }
     }
