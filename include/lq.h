@@ -45,10 +45,11 @@ typedef struct lq_state {
   void* Gbuf;             /* fp16 [NS][HV][L][K] (KDA) or NULL (GDN) */
   int* hcnt;              /* [NS][HV] */
   int NS, HV, H, K, V, L, R;
-  int* ctl;               /* optional (NULL: unused): int[2] = {heads made due since the last flush, flush workgroups
-                             done}, zero-initialised by the owner and kept by the kernels.  With it, the steps count the
-                             heads whose window they fill, and a flush that reads 0 returns at once instead of scanning
-                             hcnt; the last flush workgroup resets it.  Without it, the flush scans hcnt (the contract). */
+  int* ctl;               /* optional (NULL: unused): int[2] = {due flag: nonzero when a step has filled some head's
+                             window since the last flush, flush workgroups done}, zero-initialised by the owner and
+                             kept by the kernels.  With it, a flush that reads a clear flag returns at once instead of
+                             scanning hcnt; the last flush workgroup clears both.  Without it, the flush scans hcnt
+                             (the contract). */
 } lq_state;
 
 /* Decode inputs of one call: N rows, one token each. */

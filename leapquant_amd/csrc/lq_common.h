@@ -125,6 +125,14 @@ __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds_wave_base
 #pragma clang diagnostic pop
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---- due flag (lq_state.ctl[0]): set by a step that fills a head's window, cleared by the flush ----------------------
+// All heads made due in one call write the same word; a load first keeps the writes to the few that find it clear (the
+// writes of every head at once serialise at the memory side and stall the whole launch).
+__device__ __forceinline__ void mark_due(int* ctl) {
+  if (ctl && __hip_atomic_load(ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0)
+    __hip_atomic_fetch_or(ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 // ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------
 struct Block {
   const int8_t* Sq;   // [V][K]

@@ -615,8 +615,8 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 
 // Persistent flush: workgroup b checks the candidates p = b + gridDim.x k (row n = p / HV, head p % HV) 64 at a time
 // (wave 0, one per lane), and processes the due ones (slot > 0, hcnt == L; kernels.py:1200) one after another.
-// With the due counter st.ctl (kept by the steps), a call in which no step made a head due reads one counter and
-// returns; otherwise the last workgroup to finish resets the counter for the next call.
+// With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
+// otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
 template <bool KDA>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax) {
@@ -624,7 +624,7 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
   const int HV = st.HV, L = st.L;
   const int total = N * HV;
   const int stride = gridDim.x;
-  if (st.ctl && __atomic_load_n(st.ctl, __ATOMIC_RELAXED) == 0) return;   // uniform: nothing was made due
+  if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
   for (int base = blockIdx.x; base < total; base += 64 * stride) {
     if (threadIdx.x < 64) {
       const int p = base + stride * (int)threadIdx.x;
@@ -648,7 +648,7 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
       flush_head<KDA>(sh, st, Q0, idx[n], hv, qmax);
     }
   }
-  if (st.ctl) {                 // every workgroup has read the counter; the last one to finish clears it
+  if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
     __syncthreads();
     if (threadIdx.x == 0 && atomicAdd(st.ctl + 1, 1) == (int)gridDim.x - 1) {
       __atomic_store_n(st.ctl, 0, __ATOMIC_RELAXED);

@@ -138,10 +138,6 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   const f16_t* UQp = (const f16_t*)(Svp + VD);
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   const long long sh_ = (long long)slot * HV + hv;
-  // Window fills of the G value heads: a vector load (lane l reads head hk G + min(l, G - 1)), issued first.  Vector
-  // loads complete in order, so waiting for it waits for nothing issued later; a scalar load here would make the
-  // compiler wait for every scalar load in flight before the first use of any.
-  const int hlane = st.hcnt[(long long)slot * HV + hk * G + min(lane, G - 1)];
   float* Wp = st.Wbuf + sh_ * L;
   bf16_t kxr[2], qxr[2];
   float skx[2], wx[2];
@@ -171,53 +167,15 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   const float P = st.Pbuf[sh_];
-  __builtin_amdgcn_sched_barrier(0);   // the small loads above are issued before the wait for the window fills
-  const int h = __builtin_amdgcn_readlane(hlane, g);
-  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
-  int hmax = h;
+  // Window fills of the G value heads: uniform loads, served by the scalar data cache.  A vector load here would queue
+  // behind the bulk loads the CU's other workgroups have issued, and every later load of this workgroup waits for it.
+  int hg[G];
 #pragma unroll
-  for (int g2 = 0; g2 < G; ++g2) hmax = max(hmax, __builtin_amdgcn_readlane(hlane, g2));
-  hmax = min(hmax, L);
-  // The big loads, in the order the work after them needs them: the window (values u_j into LDS, then the buffered
-  // keys), and the int8 tile last.  Everything built on the window -- key dots, A4 / A5 -- runs while the tile still
-  // streams; after the tile's last bytes only the GEMV, the delta rule and the stores remain.
-  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction (the loop holds no compiler-visible
-  // load, so it adds no wait)
-  {
-    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
-    const int nch = live ? (h + 3) >> 2 : 0;
-    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
-  }
+  for (int g2 = 0; g2 < G; ++g2) hg[g2] = st.hcnt[(long long)slot * HV + hk * G + g2];
   __builtin_amdgcn_sched_barrier(0);
-  // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
-  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
-  bf16x8 kfr[KT][4];
-  {
-    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
-#pragma unroll
-    for (int t = 0; t < KT; ++t) {
-      const int j = 16 * (wv + 2 * G * t) + n16;
-      const int jr = j < hmax ? j : 0;
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
-    }
-  }
-  i32x4 afr[4][2];              // the int8 tile: A fragments, row 64 wi + 16 rt + n16
-  {
-    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
-#pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
-  }
-  // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
-  // stores at the end, so this count is exact)
-  constexpr int AFTER_WINDOW = 4 * KT + 8;
-  __builtin_amdgcn_sched_barrier(0);
-
-  // ---- per value head scalar work, one wave (wi = 0): gate, beta, norms, digits, key-dot operands.  Its global
-  //      writes (key append, gated weights) wait until the end, so that nothing joins the window / tile loads in the
-  //      vector memory counter before the window's wait ----
+  // ---- per value head scalar work, one wave (wi = 0), before the window fills arrive: gate, beta, norms, digits,
+  //      key-dot operands.  Its global writes (key append, gated weights) wait until the end, so that nothing joins
+  //      the window / tile loads in the vector memory counter before the window's wait ----
   bf16_t kapp[2] = {0, 0};
   float wjv[2] = {0.f, 0.f};
   if (wi == 0) {
@@ -273,12 +231,63 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
       }
       const float wj = wx[e] * alpha;
       wjv[e] = wj;              // w_j = Wbuf[j] alpha (kernels.py:270-274), written back at the end
-      if (live && c < h) sh.w[g][c] = wj;
     }
     if (lane == 0) {
       sh.sc[g][0] = alpha; sh.sc[g][1] = beta; sh.sc[g][2] = kappa; sh.sc[g][3] = kmax; sh.sc[g][4] = qmax;
     }
   }
+
+  int h = hg[0], hmax = hg[0];
+#pragma unroll
+  for (int g2 = 1; g2 < G; ++g2) {
+    h = g == g2 ? hg[g2] : h;
+    hmax = max(hmax, hg[g2]);
+  }
+  const bool live = h < L;      // a full window is never stepped (the flush follows every step)
+  hmax = min(hmax, L);
+  if (wi == 0 && live) {
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      const int c = lane + 64 * e;
+      if (c < h) sh.w[g][c] = wjv[e];
+    }
+  }
+  // The big loads, in the order the work after them needs them: the window (values u_j into LDS, then the buffered
+  // keys), and the int8 tile last.  Everything built on the window -- key dots, A4 / A5 -- runs while the tile still
+  // streams; after the tile's last bytes only the GEMV, the delta rule and the stores remain.
+  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction (the loop holds no compiler-visible
+  // load, so it adds no wait)
+  {
+    const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
+    const int nch = live ? (h + 3) >> 2 : 0;
+    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
+  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
+  bf16x8 kfr[KT][4];
+  {
+    const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
+#pragma unroll
+    for (int t = 0; t < KT; ++t) {
+      const int j = 16 * (wv + 2 * G * t) + n16;
+      const int jr = j < hmax ? j : 0;
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
+    }
+  }
+  i32x4 afr[4][2];              // the int8 tile: A fragments, row 64 wi + 16 rt + n16
+  {
+    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
+#pragma unroll
+    for (int rt = 0; rt < 4; ++rt)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+  }
+  // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
+  // stores at the end, so this count is exact)
+  constexpr int AFTER_WINDOW = 4 * KT + 8;
+  __builtin_amdgcn_sched_barrier(0);
 
   __syncthreads();              // digits, dot operands, scalars and w_j are in LDS (the barrier waits for no global load)
 
@@ -338,7 +347,22 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
   const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
   float a4 = 0.f, a5 = 0.f;
-  for (int j = 0; j < h; ++j) {
+  int j = 0;
+  for (; j + 4 <= h; j += 4) {  // four entries' LDS reads in flight at once; the sums keep the order of j
+    float ub[4];
+    float2 c[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ub[e] = bf2f(sh.ub[g][j + e][lt]);
+      c[e] = sh.cwq[g][j + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a4 = fmaf(ub[e], c[e].x, a4);
+      a5 = fmaf(ub[e], c[e].y, a5);
+    }
+  }
+  for (; j < h; ++j) {
     const float ub = bf2f(sh.ub[g][j][lt]);
     const float2 c = sh.cwq[g][j];
     a4 = fmaf(ub, c.x, a4);
@@ -387,7 +411,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
-    if (st.ctl && h + 1 == L) atomicAdd(st.ctl, 1);   // this head is due: the flush that follows will not skip
+    if (h + 1 == L) mark_due(st.ctl);   // this head is due: the flush that follows will not skip
   }
   if (wi == 0) {
 #pragma unroll
@@ -701,7 +725,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   if (lt == 0) {
     st.Wbuf[sh_ * L + h] = 1.0f;
     st.hcnt[sh_] = h + 1;
-    if (st.ctl && h + 1 == L) atomicAdd(st.ctl, 1);   // this head is due: the flush that follows will not skip
+    if (h + 1 == L) mark_due(st.ctl);   // this head is due: the flush that follows will not skip
   }
   if (wi == 0) {                // gate state (kernels.py:895-896)
 #pragma unroll

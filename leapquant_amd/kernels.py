@@ -62,7 +62,7 @@ def _check_dims(K, V, L, R):
 
 def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, ctl=None):
     """lq_state of a layer: `Sq` is any view whose data pointer is the checkpoint of (slot 0, head 0), i.e. the fp32
-    cache's data pointer.  `ctl`: optional int32 [2] due counter kept by the kernels (None: the flush scans hcnt)."""
+    cache's data pointer.  `ctl`: optional int32 [2] due flag + flush counter kept by the kernels (None: the flush scans hcnt)."""
     if ctl is not None and (ctl.dtype != torch.int32 or ctl.numel() < 2):
         raise ValueError("ctl: int32 [2] expected")
     return _lib.LqState(_dev(Sq), SS, _dev(Kbuf), _dev(Ubuf), _dev(Wbuf), _dev(Pbuf),

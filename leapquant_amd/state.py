@@ -154,7 +154,7 @@ class LeapQuantState:
                               N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
 
     def flush(self, ssm, idx):
-        """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due counter lets a
+        """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due flag lets a
         flush with nothing due return at once)."""
         idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
         idx = idx.contiguous()
