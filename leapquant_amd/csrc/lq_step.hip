@@ -478,9 +478,10 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   const float* Svp = Skp + KD;
   const f16_t* UQp = (const f16_t*)(Svp + VD);
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
-  // Window fill: a vector load (lane l reads head (hv + l) mod HV of the same slot; lane 0 the head itself), issued
-  // first so that waiting for it waits for nothing issued later.
-  const int hlane = st.hcnt[(long long)slot * HV + (hv + lane) % HV];
+  // Window fill: a uniform load, served by the scalar data cache (a vector load here would queue behind the bulk loads
+  // the CU's other workgroups have issued, and every later load of this workgroup would wait for it).
+  const int hfill = st.hcnt[sh_];
+  __builtin_amdgcn_sched_barrier(0);
   // per-channel operands of channels c = lane, lane + 64 (scalar wave) and of row lt (all lanes)
   bf16_t kxr[2], qxr[2], axr[2];
   float skx[2], dtx[2], pbx[2], wx[2];
@@ -509,7 +510,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 #pragma unroll
   for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   __builtin_amdgcn_sched_barrier(0);
-  const int h = __builtin_amdgcn_readlane(hlane, 0);
+  const int h = hfill;
   if (h >= L) { out[lt] = 0; return; }    // a full window is never stepped (the flush follows every step)
   // window rows j < h straight to LDS, 1 KiB (4 rows) per wave instruction; then the int8 tile
   {
@@ -678,7 +679,22 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 
   // ---- row v = lt: buffered entries, rank-R part, then the GEMV (the tile arrives last) and the delta rule ----
   float a4 = 0.f, a5 = 0.f;
-  for (int j = 0; j < h; ++j) {
+  int j = 0;
+  for (; j + 4 <= h; j += 4) {  // four entries' LDS reads in flight at once; the sums keep the order of j
+    float ubv[4];
+    float2 cc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      ubv[e] = bf2f(sh.ub[j + e][lt]);
+      cc[e] = sh.post.cwq[j + e];
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      a4 = fmaf(ubv[e], cc[e].x, a4);
+      a5 = fmaf(ubv[e], cc[e].y, a5);
+    }
+  }
+  for (; j < h; ++j) {
     const float ubv = bf2f(sh.ub[j][lt]);
     const float2 cc = sh.post.cwq[j];
     a4 = fmaf(ubv, cc.x, a4);
