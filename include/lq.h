@@ -98,6 +98,19 @@ int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, floa
  * UQ, idx) (kernels.py:2041-2123, state.py:152-154).  Requires K = V = 128, 1 <= L <= 64, 1 <= R <= 4. */
 int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream);
 
+/* Prefill dequant (KDA): fp32 S = (deq(Sq) + Q U^T) diag(exp(P)) + sum_{j<h} w_j u_j (K_j * D_j)^T, D_j the product of
+ * the decays of the entries after j, written over the ssm blocks of the slots idx[n] > 0; the window is kept (the
+ * checkpoint after the prefill resets it).  Replaces the torch rebuild LeapQuantState._kda_rebuild + dequantize
+ * (state.py:118-128, 147-150).  Requires K = V = 128, 1 <= L <= 64, 1 <= R <= 4, Gbuf set. */
+int lq_kda_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream);
+
+/* Prefill checkpoint (KDA) of the fp32 states of the slots idx[n] > 0: rank-R factors by three rounds of
+ * P = MGS(S^T Q), Q = MGS(S P) from Q0, U = S^T Q, both fp16; residual codes clamp(rint(E / (Sk Sv) qmax)) with
+ * Sk = sqrt(mean_v |E|), Sv = max_c |E / Sk|; window reset (Wbuf = 0, Pbuf = 0, Gbuf = 1, hcnt = 0).  Replaces the
+ * torch checkpoint LeapQuantState._kda_checkpoint with lowrank_factor (state.py:130-142, kernels.py:2318-2331).
+ * Requires K = V = 128, 1 <= R <= 4, Gbuf set. */
+int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream);
+
 /* Rank-R subspace iteration on n fp32 matrices x [n][K][V]: `iters` rounds of P = MGS(x Q), Q = MGS(x^T P) from
  * Q0 [V][R]; U = x Q.  Outputs U [n][K][R], Q [n][V][R] (fp32).
  * Replaces make_lowrank / lowrank_factor (kernels.py:2246-2331).  Requires K = V = 128, 1 <= R <= 4. */

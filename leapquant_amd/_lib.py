@@ -30,6 +30,8 @@ SIGNATURES = {
     "lq_flush": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "lq_quantize": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "lq_dequant": (c_int, [ctypes.POINTER(LqState), c_void_p, c_int, c_float, c_void_p]),
+    "lq_kda_dequant": (c_int, [ctypes.POINTER(LqState), c_void_p, c_int, c_float, c_void_p]),
+    "lq_kda_checkpoint": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "lq_lowrank": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
     "lq_dense_step": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(LqStepIO),
                               c_void_p]),

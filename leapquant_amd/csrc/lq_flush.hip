@@ -658,7 +658,10 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// standalone quantize of an fp32 state (kernels.py:2126-2242)
+// standalone quantize of an fp32 state (kernels.py:2126-2242), and the KDA prefill checkpoint (state.py:130-142): the
+// same subspace steps (P = MGS(S^T Q), Q = MGS(S P); U = fp16(S^T Q)), one round for GDN, three for KDA (the
+// low-rank factoriser's iters = 3, kernels.py:2318-2326), then the residual codes.  KDA resets its window as
+// state.py:138-142 does (Pbuf = 0 per channel, Gbuf = 1).
 // ------------------------------------------------------------------------------------------------------------------
 struct QuantShared {
   f32x4 qv[VD];
@@ -668,8 +671,9 @@ struct QuantShared {
   float sk[KD];
 };
 
+template <bool KDA>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
-void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax) {
+void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax, int iters) {
   __shared__ QuantShared sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
@@ -691,25 +695,27 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     sh.qv[tid] = q0v;
   }
   __syncthreads();
-  // P = S^T Q, MGS; Q = S P, MGS (ITERS = 1)
-  colred(t, sh.qv, [&](int i, f32x4 s) { if ((l & 15) == 0) sh.pp[16 * w + 4 * q + i] = s; });
-  __syncthreads();
-  if (w == 0) {
-    f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
-    mgs(p0, p1, R);
-    sh.pp[l] = p0;
-    sh.pp[l + 64] = p1;
+  // P = S^T Q, MGS; Q = S P, MGS (`iters` rounds)
+  for (int it = 0; it < iters; ++it) {
+    colred(t, sh.qv, [&](int i, f32x4 s) { if ((l & 15) == 0) sh.pp[16 * w + 4 * q + i] = s; });
+    __syncthreads();
+    if (w == 0) {
+      f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
+      mgs(p0, p1, R);
+      sh.pp[l] = p0;
+      sh.pp[l + 64] = p1;
+    }
+    __syncthreads();
+    rowred(t, sh.pp, sh.qpart);
+    __syncthreads();
+    if (w == 0) {
+      f32x4 p0 = sum_parts(sh.qpart, l), p1 = sum_parts(sh.qpart, l + 64);
+      mgs(p0, p1, R);
+      sh.qv[l] = p0;
+      sh.qv[l + 64] = p1;
+    }
+    __syncthreads();
   }
-  __syncthreads();
-  rowred(t, sh.pp, sh.qpart);
-  __syncthreads();
-  if (w == 0) {
-    f32x4 p0 = sum_parts(sh.qpart, l), p1 = sum_parts(sh.qpart, l + 64);
-    mgs(p0, p1, R);
-    sh.qv[l] = p0;
-    sh.qv[l + 64] = p1;
-  }
-  __syncthreads();
   // U = fp16(S^T Q), Q16 = fp16(Q)
   f32x4 ucol[4];
   colred(t, sh.qv, [&](int i, f32x4 s) { ucol[i] = s; });
@@ -789,9 +795,154 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (KDA) {
+    if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
+    uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
+    for (int i = tid; i < L * KD / 8; i += FT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  }
   if (tid == 0) {
-    st.Pbuf[sh_] = 1.f;
+    if (!KDA) st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// prefill dequant, KDA (state.py:118-128): S = diag(exp(P)) applied to S0 = Q U^T + deq(Sq) over the key channels,
+// plus sum_{j<h} w_j u_j (K_j * D_j)^T with D_j = prod_{j<i<h} e_i, written in place as fp32.  The window is left as
+// it is (the checkpoint after the engine's prefill resets it).  w_j K_j D_j goes into the rank-h MFMA as three bf16
+// terms (hi, mid, lo: 24 significant bits), so the window part keeps fp32 accuracy.
+// ------------------------------------------------------------------------------------------------------------------
+struct KdaDeqShared {
+  bf16_t op[4][KD][OPS];       // [0..2] hi / mid / lo of w_j K_j[c] D_j[c] ([c][j]), [3] u_j[v] ([v][j])
+  float skl[KD];               // Sk / qmax
+  float svr[VD];               // Sv
+  float pcs[KD];               // exp(P)
+  float w[LPMAX];
+  f32x4 uoc[KD];               // U rows [c][r]
+  f32x4 qov[VD];               // Q rows [v][r]
+};
+
+__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(2)))
+void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
+  __shared__ KdaDeqShared sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  const int slot = idx[n];
+  if (slot <= 0 || slot >= st.NS) return;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
+  char* base = block_base(st, slot, hv);
+  const int8_t* Sq = (const int8_t*)base;
+  const float* Sk = (const float*)(base + VD * KD);
+  const float* Sv = Sk + KD;
+  const f16_t* UQ = (const f16_t*)(Sv + VD);
+  const int h = min(st.hcnt[sh_], L);
+  const int LP = h > 0 ? ((h + 31) & ~31) : 32;
+  const int cv = tid & 127;
+  const bool colt = tid < KD;
+  const float scv = colt ? Sk[cv] : Sv[cv];
+  float uqv[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
+  const float pbc = st.Pbuf[sh_ * KD + cv];
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinRegs win;
+  load_window<true>(win, st, slot, hv, h, LP);
+  uint32_t wds[8];
+  load_code_words(wds, Sq);
+  f32x4 fac;
+#pragma unroll
+  for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
+  if (tid < KD) {
+    sh.skl[cv] = scv / qmax;
+    sh.pcs[cv] = expf(pbc);                                                           // state.py:128
+    sh.uoc[cv] = fac;
+  } else if (tid < KD + VD) {
+    sh.svr[cv] = scv;
+    sh.qov[cv] = fac;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
+  __syncthreads();
+  // window: raw keys / decays into op0 / op1, values into op3 (rows >= h: zero values)
+  {
+    const int ch = win_chunk(LP);
+    if (ch < 16) {
+      const int j0 = 2 * win_pair(LP), c8 = ch * 8;
+      const uint32_t keep = (j0 < h ? 0x0000ffffu : 0u) | (j0 + 1 < h ? 0xffff0000u : 0u);
+      const uint32_t ka[4] = {win.k[0].x, win.k[0].y, win.k[0].z, win.k[0].w}, kb[4] = {win.k[1].x, win.k[1].y, win.k[1].z, win.k[1].w};
+      const uint32_t ua[4] = {win.u[0].x, win.u[0].y, win.u[0].z, win.u[0].w}, ub[4] = {win.u[1].x, win.u[1].y, win.u[1].z, win.u[1].w};
+      const uint32_t ga[4] = {win.g[0].x, win.g[0].y, win.g[0].z, win.g[0].w}, gb[4] = {win.g[1].x, win.g[1].y, win.g[1].z, win.g[1].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int x = e >> 1;
+        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
+        *(uint32_t*)&sh.op[0][c8 + e][j0] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+        *(uint32_t*)&sh.op[1][c8 + e][j0] = __builtin_amdgcn_perm(gb[x], ga[x], sel);
+        *(uint32_t*)&sh.op[3][c8 + e][j0] = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
+      }
+    }
+  }
+  __syncthreads();
+  // decayed keys, thread per channel, backward from the last live entry (state.py:124-127); 8 entries per access
+  if (tid < KD) {
+    const int c = tid;
+    float dcur = 1.0f;
+    for (int j0 = LP - 8; j0 >= 0; j0 -= 8) {
+      const uint4 kr = *(const uint4*)&sh.op[0][c][j0];
+      const uint4 er = *(const uint4*)&sh.op[1][c][j0];
+      const uint32_t ku[4] = {kr.x, kr.y, kr.z, kr.w};
+      const uint32_t eu[4] = {er.x, er.y, er.z, er.w};
+      uint32_t hw[4] = {0u, 0u, 0u, 0u}, mw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 7; e >= 0; --e) {
+        const int j = j0 + e;
+        if (j < h) {
+          const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j] * dcur);
+          const bf16_t hi = f2bf(kd);
+          const float r1 = kd - bf2f(hi);
+          const bf16_t mid = f2bf(r1);
+          const bf16_t lo = f2bf(r1 - bf2f(mid));
+          hw[e >> 1] |= (uint32_t)hi << (16 * (e & 1));
+          mw[e >> 1] |= (uint32_t)mid << (16 * (e & 1));
+          lw[e >> 1] |= (uint32_t)lo << (16 * (e & 1));
+          dcur = dcur * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
+        }
+      }
+      *(uint4*)&sh.op[0][c][j0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
+      *(uint4*)&sh.op[1][c][j0] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
+      *(uint4*)&sh.op[2][c][j0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+    }
+  }
+  // S0 pc in the tile layout: (code Sk / qmax) Sv + sum_r Q[v][r] U[c][r], times exp(P[c]) (state.py:121-122, 128)
+  Tile t;
+  {
+    const int c0 = 16 * w + 4 * q;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const float rv = sh.svr[v];
+      const f32x4 qo = sh.qov[v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + i;
+        const f32x4 uo = sh.uoc[c];
+        float x = ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * sh.skl[c]) * rv;
+#pragma unroll
+        for (int a = 0; a < 4; ++a) x = fmaf(qo[a], uo[a], x);
+        t.a[nt][i] = sh.pcs[c] * x;
+      }
+    }
+  }
+  __syncthreads();                                    // decayed keys staged
+  rebuild_mfma(t, sh.op[0], sh.op[3], LP / 32);
+  rebuild_mfma(t, sh.op[1], sh.op[3], LP / 32);
+  rebuild_mfma(t, sh.op[2], sh.op[3], LP / 32);
+  __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
+  float* S = (float*)base;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    *(float4*)(S + v * KD + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
   }
 }
 
@@ -971,7 +1122,25 @@ extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, 
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  quantize_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax);
+  quantize_kernel<false><<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax, 1);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
+  int rc = check_block_state(st, false);
+  if (rc) return rc;
+  if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  quantize_kernel<true><<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax, 3);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
+  int rc = check_block_state(st, true);
+  if (rc) return rc;
+  if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  kda_dequant_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, idx, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

@@ -88,7 +88,7 @@ class LeapQuantState:
         else:
             self.kstep = KN.make_gdn_step(NS, HV, H, K, V, L, SS, R=R)
         self.kflush = KN.make_flush(NS, HV, K, V, L, SS, R=R, ITERS=1, KDA=kda, NMAX=nmax, qmax=qmax)
-        if not kda:                          # KDA prefill round trip runs in torch + the HIP low-rank factoriser
+        if not kda:                          # the KDA prefill round trip has its own entry points
             self.kdeq = _make_dequant(NS, HV, K, V, L, SS, buf_dtype=KN.BF16, R=R, qmax=qmax)
             self.kquant = _make_quantize(NS, HV, K, V, L, SS, R=R, ITERS=1, qmax=qmax)
         self._lib = _lib.lib()
@@ -167,51 +167,20 @@ class LeapQuantState:
     def kstep_scale(self):
         return 128 ** -0.5 if self.kda else self.K ** -0.5
 
-    def _kda_rebuild(self, ssm, sl):
-        """KDA: S = exp(P) (Q U^T + deq(res)) + sum_{j<h} w_j u_j (x) (k_j * D_j), D_j the product of the decays of the
-        entries after j (entries j >= h count as 1).  Torch on the GPU, as in state.py:118-128 of the reference."""
-        v = self.views(ssm)
-        K = self.K
-        uq = v["uq"][sl].float()
-        S0 = torch.matmul(uq[..., K:].transpose(-1, -2), uq[..., :K]) \
-            + v["Sq"][sl].float() * (v["Sk"][sl][..., None, :] / self.qmax) * v["Sv"][sl][..., :, None]
-        h = self.hcnt[sl]
-        live = torch.arange(self.L, device=ssm.device)[None, None, :, None] < h[..., None, None]
-        E = torch.where(live, self.Gbuf[sl].float(), torch.ones((), device=ssm.device))
-        # D_j = prod_{i > j} E_i: exclusive reverse cumulative product
-        D = torch.cat([torch.flip(torch.cumprod(torch.flip(E[:, :, 1:], [2]), 2), [2]), torch.ones_like(E[:, :, :1])], 2)
-        G = self.HV // self.H
-        kdec = self.Kbuf[sl].float().repeat_interleave(G, dim=1) * D
-        wu = self.Wbuf[sl][..., None] * self.Ubuf[sl].float()                     # [n, HV, L, V]
-        return torch.exp(self.Pbuf[sl])[..., None, :] * S0 + torch.matmul(wu.transpose(-1, -2), kdec)
-
-    def _kda_checkpoint(self, ssm, sl):
-        """KDA: 8-bit checkpoint of the fp32 states in the slots sl (state.py:130-142): rank-R factors from the HIP
-        low-rank factoriser (3 subspace iterations), fp16; smoothed residual quantised with clamp(round(.))."""
-        v = self.views(ssm)
-        S = ssm[sl].float()                                        # [n, HV, V, K]
-        U, Q = KN.lowrank_factor(S.transpose(-1, -2), self.R)     # rank-R fit in the [K, V] orientation
-        Uh, Qh = U.half(), Q.half()
-        res = S - torch.matmul(Qh.float(), Uh.float().transpose(-1, -2))
-        sk = res.abs().mean(-2).sqrt().clamp_min(KN.EPS)
-        sv = (res.abs() / sk[..., None, :]).amax(-1).clamp_min(KN.EPS)
-        codes = torch.round(res / (sk[..., None, :] * sv[..., :, None]) * self.qmax).clamp(-self.qmax, self.qmax)
-        v["Sq"][sl] = codes.to(torch.int8)
-        v["Sk"][sl] = sk
-        v["Sv"][sl] = sv
-        v["uq"][sl] = torch.cat([Uh.transpose(-1, -2), Qh.transpose(-1, -2)], -1)
-        self.Wbuf[sl] = 0.0
-        self.Pbuf[sl] = 0.0
-        self.Gbuf[sl] = 1.0
-        self.hcnt[sl] = 0
+    def _kda_round_trip(self, ssm, idx, fn, *extra):
+        idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        idx = idx.contiguous()
+        st = self._struct(ssm)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(idx.device).cuda_stream)
+        _lib.check(getattr(self._lib, fn)(ctypes.byref(st), *extra, KN._p(idx), idx.shape[0],
+                                          ctypes.c_float(self.qmax), stream), fn)
 
     def dequantize(self, ssm, idx):
         """Materialise the fp32 state of the slots idx in place (before the engine's own prefill kernel runs)."""
         if idx.numel() == 0:
             return
-        if self.kda:
-            sl = idx.to(torch.int64)
-            ssm[sl] = self._kda_rebuild(ssm, sl)
+        if self.kda:                 # S = (Q U^T + deq) diag(exp(P)) + decayed window (state.py:118-128), HIP
+            self._kda_round_trip(ssm, idx, "lq_kda_dequant")
             return
         v = self.views(ssm)
         self.kdeq(ssm, v["Sq"], v["Sk"], v["Sv"], self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf, self.Gbuf, self.hcnt,
@@ -221,8 +190,8 @@ class LeapQuantState:
         """Write the 8-bit checkpoint of the fp32 states in the slots idx and reset their windows (after a prefill)."""
         if idx.numel() == 0:
             return
-        if self.kda:
-            self._kda_checkpoint(ssm, idx.to(torch.int64))
+        if self.kda:                 # rank-R fit (3 rounds) + residual codes, window reset (state.py:130-142), HIP
+            self._kda_round_trip(ssm, idx, "lq_kda_checkpoint", KN._p(self.Q0))
             return
         v = self.views(ssm)
         self.kquant(ssm, v["Sq"], v["Sk"], v["Sv"], v["uq"], self.Wbuf, self.Pbuf, self.hcnt, self.Q0,

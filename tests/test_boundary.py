@@ -75,9 +75,12 @@ def test_entry_points_reject_bad_state(lib, bad):
     assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == -1
     assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 0, ctypes.c_float(127.0), z) == -1
     assert lib.lq_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_kda_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == -1
     if "Kbuf" not in bad and "Ubuf" not in bad:
         assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, ctypes.c_float(127.0),
                                z) == -1
+        assert lib.lq_kda_checkpoint(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
+                                     ctypes.c_float(127.0), z) == -1
 
 
 def test_entry_points_accept_empty_calls(lib):
@@ -89,6 +92,9 @@ def test_entry_points_accept_empty_calls(lib):
     assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1, ctypes.c_float(31.0), z) == 0
     assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == 0
     assert lib.lq_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_kda_dequant(ctypes.byref(st), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_kda_checkpoint(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, ctypes.c_float(31.0),
+                                 z) == 0
     assert lib.lq_lowrank(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 128, 128,
                           4, 3, z) == 0
 
@@ -104,12 +110,18 @@ def test_other_argument_errors(lib):
     assert lib.lq_kda_step(ctypes.byref(_state(Gbuf=None)), ctypes.byref(_io()), ctypes.c_float(0.0), z) == -1
     assert lib.lq_flush(ctypes.byref(_state(Gbuf=None)), ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 1,
                         ctypes.c_float(127.0), z) == -1
+    assert lib.lq_kda_dequant(ctypes.byref(_state(Gbuf=None)), ctypes.c_void_p(16), 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_kda_checkpoint(ctypes.byref(_state(Gbuf=None)), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
+                                 ctypes.c_float(127.0), z) == -1
     # GDN step: HV / H must be 1, 2 or 4
     assert lib.lq_gdn_step(ctypes.byref(_state(HV=24, H=3)), ctypes.byref(_io(N=1)), z) == -1
     # code range
     for q in (0.5, 128.0, float("nan")):
         assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 0, ctypes.c_float(q), z) == -1
         assert lib.lq_quantize(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 1, ctypes.c_float(q), z) == -1
+        assert lib.lq_kda_checkpoint(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 1, ctypes.c_float(q),
+                                     z) == -1
+        assert lib.lq_kda_dequant(ctypes.byref(st), ctypes.c_void_p(16), 1, ctypes.c_float(q), z) == -1
     assert lib.lq_flush(ctypes.byref(st), None, ctypes.c_void_p(16), 1, 0, ctypes.c_float(127.0), z) == -1
     assert lib.lq_flush(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), -1, 0, ctypes.c_float(127.0), z) == -1
     # lowrank limits

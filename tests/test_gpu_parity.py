@@ -241,11 +241,14 @@ def test_lowrank_matches_oracle():
     assert np.linalg.norm(Q - Q_ref) <= 1e-3 * np.linalg.norm(Q_ref)
 
 
-def test_kda_round_trip_matches_oracle():
-    rng = np.random.default_rng(900)
+@pytest.mark.parametrize("L,steps", [(16, 12), (64, 40)])
+def test_kda_round_trip_matches_oracle(L, steps):
+    """KDA prefill round trip (HIP lq_kda_dequant / lq_kda_checkpoint) against the oracle's rebuild and checkpoint, slots
+    at their own window fills (up to a full window at L = 16; several LDS passes of the decay scan at L = 64)."""
+    rng = np.random.default_rng(900 + L)
     NS, HV, H = 5, 4, 4
-    st, S, Q0 = make_state(rng, NS, HV, H, L=16, kda=True)
-    _prestep(rng, st, Q0, True, steps=12, NS=NS, HV=HV, H=H)
+    st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=True)
+    _prestep(rng, st, Q0, True, steps=steps, NS=NS, HV=HV, H=H)
     slots = np.array([1, 4], np.int64)
     ssm, lq = G.to_gpu(st)
     reb = O.kda_rebuild(st, slots)
