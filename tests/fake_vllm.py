@@ -33,15 +33,19 @@ def _act(y, activation):
     return F.silu(y) if activation in ("silu", "swish", True) else y
 
 
+ON_DEVICE = [False]   # True: the conv update runs where its tensors live (model loops, graph capture)
+
+
 def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None, conv_state_indices=None,
                          validate_data=False):
     """x [n, C]; conv_state [NS, C, W - 1] (channel-first view); weight [C, W].  Returns [n, C] and shifts the states.
-    Computed on the host whatever the device, so an expectation built on the CPU matches it bit for bit."""
-    idx = conv_state_indices.long()
-    win = torch.cat([conv_state[idx].float().cpu(), x.float().cpu()[:, :, None]], -1)        # [n, C, W]
-    y = (win * weight.detach().float().cpu()[None]).sum(-1)
+    Computed on the host (unless ON_DEVICE), so an expectation built on the CPU matches it bit for bit."""
+    dev = x.device if ON_DEVICE[0] else torch.device("cpu")
+    idx = conv_state_indices.long().to(conv_state.device)
+    win = torch.cat([conv_state[idx].float().to(dev), x.float().to(dev)[:, :, None]], -1)     # [n, C, W]
+    y = (win * weight.detach().float().to(dev)[None]).sum(-1)
     if bias is not None:
-        y = y + bias.detach().float().cpu()
+        y = y + bias.detach().float().to(dev)
     conv_state[idx] = win[..., 1:].to(conv_state.dtype).to(conv_state.device)
     return _act(y, activation).to(x.dtype).to(x.device)
 
