@@ -462,6 +462,52 @@ def main():
     bf16_gbps = dense_bytes(B, HV, H, K, V) / (bf16_us * 1e-6) / 1e9
     del gd, Sd
 
+    # ---- conv1d update fused into the step (lq_gdn_step_conv) against the conv update kernel + step, same rotated
+    # sets and raw projections (the pool's mixed rows stand for the raw in_proj output); windows from h = 0 ----
+    import ctypes
+    from leapquant_amd import _lib
+    C = 2 * H * K + HV * V
+    conv = torch.empty(NS, C, 3, device=dev).normal_(0.0, 1.0, generator=g).to(torch.bfloat16)
+    cw = (torch.empty(C, 4, device=dev).normal_(0.0, 0.5, generator=g)).to(torch.bfloat16).contiguous()
+    cv = KN.conv_struct(conv, cw, None, True)
+    xconv = torch.empty(B, C, device=dev, dtype=torch.bfloat16)
+    sts = lq._struct(ssm)
+    ios = {}
+
+    def io_of(x, a, b, kset):
+        key = (x.data_ptr(), a.data_ptr(), kset)
+        if key not in ios:
+            ios[key] = KN._step_io(x, a, b, A_log, dt_bias, sets[kset], out, K ** -0.5)
+        return ios[key]
+
+    def fused(i):
+        x, a, b = pool[i % P]
+        _lib.check(_lib.lib().lq_gdn_step_conv(ctypes.byref(sts), ctypes.byref(io_of(x, a, b, i % NSET)),
+                                                ctypes.byref(cv), ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)),
+                   "lq_gdn_step_conv")
+
+    def unfused(i):
+        x, a, b = pool[i % P]
+        KN.conv_update(x, conv, cw, None, sets[i % NSET], xconv, True)
+        _lib.check(_lib.lib().lq_gdn_step(ctypes.byref(sts), ctypes.byref(io_of(xconv, a, b, i % NSET)),
+                                           ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "lq_gdn_step")
+
+    conv_us = {}
+    for name, fn in (("fused", fused), ("unfused", unfused)):
+        gr = capture(fn, CH)
+        lq.quantize(ssm, all_slots)                               # every window back to h = 0
+        torch.cuda.synchronize()
+        c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            c0.record(stream)
+            for _ in range(NSET):                                 # every set steps h = 0 .. 63
+                gr.replay()
+            c1.record(stream)
+        torch.cuda.synchronize()
+        conv_us[name] = c0.elapsed_time(c1) * 1e3 / (NSET * CH)
+        del gr
+    del conv, xconv
+
     # ---- 8 copies of 64 MiB: the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters when this
     # same command runs under rocprofv3 --pmc (bytes per launch of the step: profiles/gdn_step_B64_traffic.json) ----
     src = torch.empty(64 * 2 ** 20 // 4, device=dev)
@@ -489,6 +535,11 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(),
                      "kernel": "gdn_step_kernel<2>", "bytes_per_launch": int(bytes_step)},
     }
+    res["conv_fused_config1"] = {
+        "workload": "config 1 step with vLLM's causal_conv1d_update (width 4, SiLU, bf16 state [NS, C, 3]) fused in, "
+                    "against the conv update kernel + step; rotated sets, h = 0..63",
+        "fused_step_us": round(conv_us["fused"], 3), "conv_then_step_us": round(conv_us["unfused"], 3),
+        "plain_step_us": round(step_us, 3)}
     res["kda_config2"] = kda
     res["flush_quantize_config3"] = fq
     if not args.no_cpu:

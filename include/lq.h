@@ -65,6 +65,20 @@ typedef struct lq_step_io {
   float scale;            /* query scale (K^-1/2 by default) */
 } lq_step_io;
 
+/* Depthwise causal conv1d update (vLLM's causal_conv1d_update) fused into the GDN step: the step reads the raw
+ * projection x (io.mixed, pre-conv, bf16 [N][C], C = 2*H*K + HV*V) and computes, for the channels it consumes,
+ * mixed[c] = bf16(act(sum_{t<W-1} w[c][t] s[t] + w[c][W-1] x[c] + bias[c])), s the slot's conv state, then shifts the
+ * state by one (s[t] = s[t+1], s[W-2] = x[c]).  Padding rows leave their state untouched. */
+typedef struct lq_conv {
+  void* state;            /* bf16 conv state; element (slot, channel c, tap t), t < W - 1, at
+                             state[slot * slot_stride + c * ch_stride + t * tap_stride] */
+  const void* weight;     /* bf16 [C][W] depthwise weights */
+  const void* bias;       /* bf16 [C] or NULL */
+  long long slot_stride, ch_stride, tap_stride;   /* in elements */
+  int W;                  /* taps: 4 */
+  int silu;               /* 1: SiLU after the bias; 0: none */
+} lq_conv;
+
 int lq_abi_version(void);
 
 /* GDN decode step: one token per row; appends (k, u, w = 1) to the window and updates the gate products.
@@ -73,6 +87,10 @@ int lq_abi_version(void);
  * 1 <= R <= 4, HV % H == 0 and HV / H in {1, 2, 4}.  A head whose window is already full (hcnt >= L) is left
  * untouched and its output row is zero (the flush after every step keeps hcnt < L on entry). */
 int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream);
+
+/* lq_gdn_step with the conv1d update fused in (see lq_conv): io->mixed holds the raw projection.  No counterpart in the
+ * reference as one call: replaces vLLM's causal_conv1d_update (leapquant/vllm/gdn.py:32) followed by the step. */
+int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream);
 
 /* KDA decode step (per-key-channel gate).  glb != 0: GLM's bounded gate glb * sigmoid(exp(A_log) (a + dt_bias));
  * glb == 0: Kimi's -exp(A_log) softplus(a + dt_bias).
@@ -116,6 +134,11 @@ int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N
  * Replaces make_lowrank / lowrank_factor (kernels.py:2246-2331).  Requires K = V = 128, 1 <= R <= 4. */
 int lq_lowrank(const float* x, const float* Q0, float* U, float* Q, int n, int K, int V, int R, int iters,
                void* stream);
+
+/* Baseline (no reference counterpart): the standalone conv1d update that lq_gdn_step_conv fuses into the step, same
+ * arithmetic (it stands for vLLM's causal_conv1d_update, leapquant/vllm/gdn.py:32): out [N][C] bf16 from the raw
+ * projection x [N][C], the conv states of the slots idx[n] > 0 (< NS) shifted in place. */
+int lq_conv_update(const lq_conv* cv, const void* x, void* out, const int* idx, int N, int C, int NS, void* stream);
 
 /* Baseline for the measurements (no reference counterpart): the same GDN decode step on a dense state S
  * [NS][HV][V][K] stored as bf16 (state_dtype 0) or fp32 (state_dtype 1), updated in place:

@@ -22,10 +22,16 @@ class LqStepIO(ctypes.Structure):
                 ("idx", c_void_p), ("out", c_void_p), ("N", c_int), ("scale", c_float)]
 
 
+class LqConv(ctypes.Structure):
+    _fields_ = [("state", c_void_p), ("weight", c_void_p), ("bias", c_void_p), ("slot_stride", c_ll),
+                ("ch_stride", c_ll), ("tap_stride", c_ll), ("W", c_int), ("silu", c_int)]
+
+
 # exported symbol -> (restype, argtypes); must match include/lq.h
 SIGNATURES = {
     "lq_abi_version": (c_int, []),
     "lq_gdn_step": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_void_p]),
+    "lq_gdn_step_conv": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv), c_void_p]),
     "lq_kda_step": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_float, c_void_p]),
     "lq_flush": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "lq_quantize": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_float, c_void_p]),
@@ -33,6 +39,7 @@ SIGNATURES = {
     "lq_kda_dequant": (c_int, [ctypes.POINTER(LqState), c_void_p, c_int, c_float, c_void_p]),
     "lq_kda_checkpoint": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "lq_lowrank": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_int, c_void_p]),
+    "lq_conv_update": (c_int, [ctypes.POINTER(LqConv), c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "lq_dense_step": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(LqStepIO),
                               c_void_p]),
 }

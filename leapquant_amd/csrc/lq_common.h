@@ -125,6 +125,41 @@ __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds_wave_base
 #pragma clang diagnostic pop
 __device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// ---- depthwise causal conv1d update (lq_conv, W = 4) ----------------------------------------------------------
+// Conv taps of one channel (lq_conv, W = 4): the raw projection x, the slot's three state taps and the four weights.
+struct ConvTaps {
+  bf16_t x, s[3];
+  uint2 w;                  // four bf16 weights
+  bf16_t b;
+};
+__device__ __forceinline__ ConvTaps conv_taps(const lq_conv& cv, const bf16_t* xrow, long long sbase, int ch) {
+  ConvTaps t;
+  const bf16_t* S = (const bf16_t*)cv.state + sbase + (long long)ch * cv.ch_stride;
+  t.x = xrow[ch];
+#pragma unroll
+  for (int i = 0; i < 3; ++i) t.s[i] = S[i * cv.tap_stride];
+  t.w = ((const uint2*)cv.weight)[ch];
+  t.b = cv.bias ? ((const bf16_t*)cv.bias)[ch] : (bf16_t)0;
+  return t;
+}
+// mixed[c] = bf16(act(w0 s0 + w1 s1 + w2 s2 + w3 x + bias)): products and sums rounded one at a time, left to right
+__device__ __forceinline__ float conv_out(const ConvTaps& t, bool silu) {
+  const float w[4] = {bf_lo(t.w.x), bf_hi(t.w.x), bf_lo(t.w.y), bf_hi(t.w.y)};
+  float y = __fmul_rn(w[0], bf2f(t.s[0]));
+  y = __fadd_rn(y, __fmul_rn(w[1], bf2f(t.s[1])));
+  y = __fadd_rn(y, __fmul_rn(w[2], bf2f(t.s[2])));
+  y = __fadd_rn(y, __fmul_rn(w[3], bf2f(t.x)));
+  y = __fadd_rn(y, bf2f(t.b));
+  if (silu) y = y / (1.0f + expf(-y));
+  return bfround(y);
+}
+__device__ __forceinline__ void conv_shift(const lq_conv& cv, long long sbase, int ch, const ConvTaps& t) {
+  bf16_t* S = (bf16_t*)cv.state + sbase + (long long)ch * cv.ch_stride;
+  S[0] = t.s[1];
+  S[cv.tap_stride] = t.s[2];
+  S[2 * cv.tap_stride] = t.x;
+}
+
 // ---- due flag (lq_state.ctl[0]): set by a step that fills a head's window, cleared by the flush ----------------------
 // All heads made due in one call write the same word; a load first keeps the writes to the few that find it clear (the
 // writes of every head at once serialise at the memory side and stall the whole launch).

@@ -107,6 +107,21 @@ __global__ __launch_bounds__(128 * G) void dense_step_kernel(void* S, int NS, in
 
 }  // namespace
 
+// Baseline (no reference counterpart): the standalone conv1d update that lq_gdn_step_conv fuses into the step, with
+// the same arithmetic -- vLLM's causal_conv1d_update stands here (vLLM is not installed).  Thread per (row, channel):
+// out[n][c] = bf16(act(conv)), the slot's conv state shifted; padding rows (slot <= 0) are skipped.
+__global__ __launch_bounds__(256) void conv_update_kernel(lq_conv cv, const bf16_t* __restrict__ x, bf16_t* out,
+                                                          const int* __restrict__ idx, int C, int NS) {
+  const int n = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int slot = idx[n];
+  if (c >= C || slot <= 0 || slot >= NS) return;
+  const long long sb = (long long)slot * cv.slot_stride;
+  const ConvTaps t = conv_taps(cv, x + (long long)n * C, sb, c);
+  out[(long long)n * C + c] = f2bf(conv_out(t, cv.silu));
+  conv_shift(cv, sb, c, t);
+}
+
 extern "C" int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, int K, int V, const lq_step_io* io,
                              void* stream) {
   if (!S || !io || K != KD || V != VD || H <= 0 || HV <= 0 || HV % H != 0 || NS <= 0 || io->N < 0) return LQ_ERR_ARG;
@@ -124,5 +139,19 @@ extern "C" int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, in
     else return LQ_ERR_ARG;
   }
 #undef LQ_DENSE
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_conv_update(const lq_conv* cv, const void* x, void* out, const int* idx, int N, int C, int NS,
+                              void* stream) {
+  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || N < 0 || C <= 0 || NS <= 0)
+    return LQ_ERR_ARG;
+  if (cv->ch_stride <= 0 || cv->tap_stride <= 0 || (C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride)
+    return LQ_ERR_ARG;
+  if (((uintptr_t)cv->weight & 7) != 0) return LQ_ERR_ARG;
+  if (N == 0) return LQ_OK;
+  if (!x || !out || !idx) return LQ_ERR_ARG;
+  dim3 grid((unsigned)((C + 255) / 256), (unsigned)N);
+  conv_update_kernel<<<grid, 256, 0, (hipStream_t)stream>>>(*cv, (const bf16_t*)x, (bf16_t*)out, idx, C, NS);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }

@@ -105,9 +105,9 @@ struct StepShared {
 // LDS by direct global -> LDS loads.  <= 128 VGPRs and < 40 KiB LDS: four workgroups per CU, the whole B = 64 x H = 16
 // grid resident at once.
 // ------------------------------------------------------------------------------------------------------------------
-template <int G>
+template <int G, bool CONV>
 __global__ __launch_bounds__(128 * G) __attribute__((amdgpu_waves_per_eu(4)))
-void gdn_step_kernel(lq_state st, lq_step_io io) {
+void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   __shared__ StepShared<G> sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
@@ -141,11 +141,18 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   float* Wp = st.Wbuf + sh_ * L;
   bf16_t kxr[2], qxr[2];
   float skx[2], wx[2];
+  ConvTaps ktap[2], qtap[2], vtap;    // CONV: taps of the key / query channels c and of the value channel lt
+  const long long cvb = CONV ? (long long)slot * cv.slot_stride : 0;
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int c = lane + 64 * e;
-    kxr[e] = mrow[H * KD + hk * KD + c];
-    qxr[e] = mrow[hk * KD + c];
+    if (CONV) {
+      ktap[e] = conv_taps(cv, mrow, cvb, H * KD + hk * KD + c);
+      qtap[e] = conv_taps(cv, mrow, cvb, hk * KD + c);
+    } else {
+      kxr[e] = mrow[H * KD + hk * KD + c];
+      qxr[e] = mrow[hk * KD + c];
+    }
     skx[e] = Skp[c];
     wx[e] = Wp[min(c, L - 1)];
   }
@@ -161,7 +168,9 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
   }
-  const float vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
+  float vin = 0.f;
+  if (CONV) vtap = conv_taps(cv, mrow, cvb, 2 * H * KD + hv * VD + lt);
+  else vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
   float qt[4];                  // Q^T[r][lt]
 #pragma unroll
@@ -178,9 +187,21 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   //      the window / tile loads in the vector memory counter before the window's wait ----
   bf16_t kapp[2] = {0, 0};
   float wjv[2] = {0.f, 0.f};
+  uint32_t kpk[4] = {0u, 0u, 0u, 0u}, qpk[4] = {0u, 0u, 0u, 0u};   // CONV: key / query state after the shift
   if (wi == 0) {
     const float alpha = gdn_alpha_f(bf2f(araw), dtb, alog);
     const float beta = beta_f(bf2f(braw));
+    if (CONV) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        kxr[e] = f2bf(conv_out(ktap[e], cv.silu));
+        qxr[e] = f2bf(conv_out(qtap[e], cv.silu));
+        kpk[e] = ktap[e].s[1] | ((uint32_t)ktap[e].s[2] << 16);   // the shifted taps (s1, s2 | x)
+        kpk[2 + e] = ktap[e].x;
+        qpk[e] = qtap[e].s[1] | ((uint32_t)qtap[e].s[2] << 16);
+        qpk[2 + e] = qtap[e].x;
+      }
+    }
     const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
     float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
     nq = fmaf(qx[1], qx[1], nq); nk = fmaf(kx[1], kx[1], nk); nkq = fmaf(kx[1], qx[1], nkq);
@@ -237,6 +258,10 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
     }
   }
 
+  if (CONV) {                   // the value channel lt of this head: conv output and state shift
+    vin = conv_out(vtap, cv.silu);
+    conv_shift(cv, cvb, 2 * H * KD + hv * VD + lt, vtap);
+  }
   int h = hg[0], hmax = hg[0];
 #pragma unroll
   for (int g2 = 1; g2 < G; ++g2) {
@@ -290,6 +315,19 @@ void gdn_step_kernel(lq_state st, lq_step_io io) {
   __builtin_amdgcn_sched_barrier(0);
 
   __syncthreads();              // digits, dot operands, scalars and w_j are in LDS (the barrier waits for no global load)
+  if (CONV && wv == 0) {        // the key head's conv state shift, once per workgroup, after every wave read its taps
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      bf16_t* Sk_ = (bf16_t*)cv.state + cvb + (long long)(H * KD + hk * KD + lane + 64 * e) * cv.ch_stride;
+      bf16_t* Sq_ = (bf16_t*)cv.state + cvb + (long long)(hk * KD + lane + 64 * e) * cv.ch_stride;
+      Sk_[0] = (bf16_t)kpk[e];
+      Sk_[cv.tap_stride] = (bf16_t)(kpk[e] >> 16);
+      Sk_[2 * cv.tap_stride] = (bf16_t)kpk[2 + e];
+      Sq_[0] = (bf16_t)qpk[e];
+      Sq_[cv.tap_stride] = (bf16_t)(qpk[e] >> 16);
+      Sq_[2 * cv.tap_stride] = (bf16_t)qpk[2 + e];
+    }
+  }
 
   // ---- buffered-key dots: this wave's K tiles against bf16 (hi, mid, lo) of kn (columns 0-2) and qn (4-6) ----
   {
@@ -775,10 +813,33 @@ extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* strea
   if (io->N == 0) return LQ_OK;
   dim3 grid((unsigned)(io->N * st->H));
   hipStream_t s = (hipStream_t)stream;
+  const lq_conv none = {};
   switch (G) {
-    case 1: gdn_step_kernel<1><<<grid, 128, 0, s>>>(*st, *io); break;
-    case 2: gdn_step_kernel<2><<<grid, 256, 0, s>>>(*st, *io); break;
-    case 4: gdn_step_kernel<4><<<grid, 512, 0, s>>>(*st, *io); break;
+    case 1: gdn_step_kernel<1, false><<<grid, 128, 0, s>>>(*st, *io, none); break;
+    case 2: gdn_step_kernel<2, false><<<grid, 256, 0, s>>>(*st, *io, none); break;
+    case 4: gdn_step_kernel<4, false><<<grid, 512, 0, s>>>(*st, *io, none); break;
+    default: return LQ_ERR_ARG;
+  }
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
+  int rc = check_step(st, io);
+  if (rc) return rc;
+  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1)) return LQ_ERR_ARG;
+  const long long C = 2ll * st->H * st->K + (long long)st->HV * st->V;
+  if (cv->ch_stride <= 0 || cv->tap_stride <= 0 || cv->slot_stride <= 0) return LQ_ERR_ARG;
+  // the state taps of a slot must stay inside its slot_stride elements
+  if ((C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride) return LQ_ERR_ARG;
+  if (((uintptr_t)cv->weight & 7) != 0) return LQ_ERR_ARG;
+  const int G = st->HV / st->H;
+  if (io->N == 0) return LQ_OK;
+  dim3 grid((unsigned)(io->N * st->H));
+  hipStream_t s = (hipStream_t)stream;
+  switch (G) {
+    case 1: gdn_step_kernel<1, true><<<grid, 128, 0, s>>>(*st, *io, *cv); break;
+    case 2: gdn_step_kernel<2, true><<<grid, 256, 0, s>>>(*st, *io, *cv); break;
+    case 4: gdn_step_kernel<4, true><<<grid, 512, 0, s>>>(*st, *io, *cv); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;

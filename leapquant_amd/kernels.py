@@ -258,6 +258,32 @@ def lowrank_factor(x, r, iters=3):
     return U.reshape(*lead, K, r), Q.reshape(*lead, V, r)
 
 
+def conv_struct(conv_state, weight, bias=None, silu=True):
+    """lq_conv of a conv state [NS, C, W - 1] view (any strides), bf16 weights [C, 4] and optional bf16 bias [C]."""
+    C = weight.shape[0]
+    w = weight.reshape(C, -1)
+    if conv_state.dtype != torch.bfloat16 or conv_state.dim() != 3 or conv_state.shape[1:] != (C, 3):
+        raise ValueError("conv_state: bf16 [NS, C, 3] expected")
+    if w.dtype != torch.bfloat16 or w.shape[1] != 4 or not w.is_contiguous():
+        raise ValueError("conv weight: contiguous bf16 [C, 4] expected")
+    if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != C or not bias.is_contiguous()):
+        raise ValueError("conv bias: bf16 [C] expected")
+    return _lib.LqConv(_dev(conv_state), _dev(w), _dev(bias) if bias is not None else 0, conv_state.stride(0),
+                       conv_state.stride(1), conv_state.stride(2), 4, 1 if silu else 0)
+
+
+def conv_update(x, conv_state, weight, bias, idx, out, silu=True):
+    """Baseline (stands for vLLM's causal_conv1d_update): out [N, C] bf16 from the raw projection x [N, C], the conv
+    states of the slots idx[n] > 0 shifted in place (the arithmetic lq_gdn_step_conv fuses into the step)."""
+    N, C = x.shape
+    cv = conv_struct(conv_state, weight, bias, silu)
+    _need(x, torch.bfloat16, (N, C), "x")
+    _need(out, torch.bfloat16, (N, C), "out")
+    _need(idx, torch.int32, (N,), "idx")
+    _lib.check(_lib.lib().lq_conv_update(ctypes.byref(cv), _p(x), _p(out), _p(idx), N, C, conv_state.shape[0],
+                                         _stream(x)), "lq_conv_update")
+
+
 def dense_step(S, mixed, a, b, A_log, dt_bias, idx, o, H, scale=None):
     """Baseline (no reference counterpart): the same GDN decode step on a dense bf16 / fp32 state S [NS, HV, V, K]
     updated in place."""

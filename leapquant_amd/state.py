@@ -153,6 +153,46 @@ class LeapQuantState:
         _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx),
                               N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
 
+    def decode_conv(self, ssm, x, conv_state, conv_weight, conv_bias, silu, a, b, A_log, dt_bias, idx, out):
+        """GDN decode with the conv1d update fused into the step (lq_gdn_step_conv): x is the raw projection
+        [N, 2HK + HV V] (bf16, before vLLM's causal_conv1d_update); conv_state [NS, C, W-1] (any strides) and
+        conv_weight [C, W] bf16 with W = 4; the conv state of every row's slot is shifted in place.  Then the flush."""
+        if self.kda:
+            raise ValueError("decode_conv: GDN only")
+        C = 2 * self.H * self.K + self.HV * self.V
+        if conv_state.dtype != torch.bfloat16 or conv_state.dim() != 3 or conv_state.shape[1:] != (C, 3) \
+                or conv_state.shape[0] < self.NS:
+            raise ValueError("conv_state: bf16 [NS, C, 3] expected")
+        w = conv_weight.reshape(C, -1)
+        if w.dtype != torch.bfloat16 or w.shape[1] != 4 or not w.is_contiguous() or w.data_ptr() % 8:
+            raise ValueError("conv_weight: contiguous bf16 [C, 4] expected")
+        if conv_bias is not None and (conv_bias.dtype != torch.bfloat16 or conv_bias.numel() != C
+                                      or not conv_bias.is_contiguous()):
+            raise ValueError("conv_bias: bf16 [C] expected")
+        A_log = A_log if A_log.dtype == torch.float32 else self._p32(A_log)
+        dt_bias = dt_bias if dt_bias.dtype == torch.float32 else self._p32(dt_bias)
+        N = idx.shape[0]
+        a = a.reshape(N, self.HV).contiguous()
+        dt_bias = dt_bias.reshape(self.HV).contiguous()
+        A_log = A_log.reshape(self.HV).contiguous()
+        idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
+        idx = idx.contiguous()
+        if x.dtype != torch.bfloat16 or not x.is_contiguous() or x.shape != (N, C):
+            raise ValueError("x: contiguous bf16 [N, 2HK + HV V] expected")
+        if out.dtype != torch.bfloat16 or out.numel() != N * self.HV * self.V or not out.is_contiguous():
+            raise ValueError("out: contiguous bf16 [N, HV, V] expected")
+        if b.dtype != torch.bfloat16 or b.numel() != N * self.HV:
+            raise ValueError("b: bf16 [N, HV] expected")
+        b = b.contiguous()
+        st = self._struct(ssm)
+        io = KN._step_io(x, a, b, A_log, dt_bias, idx, out, self.kstep_scale)
+        cv = KN.conv_struct(conv_state, w, conv_bias, silu)
+        stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
+        L = self._lib
+        _lib.check(L.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), stream), "lq_gdn_step_conv")
+        _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 0, ctypes.c_float(self.qmax), stream),
+                   "lq_flush")
+
     def flush(self, ssm, idx):
         """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due flag lets a
         flush with nothing due return at once)."""

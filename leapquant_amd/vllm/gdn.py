@@ -1,7 +1,7 @@
 """LeapQuant on vLLM's Gated DeltaNet layers (QwenGatedDeltaNetAttention), reference: leapquant/vllm/gdn.py:11-81.
 
 * A step with only decode tokens: vLLM's conv1d update, then the HIP step + flush on the 8-bit state, writing straight
-  into the layer's output buffer.
+  into the layer's output buffer; with a bf16 conv of width 4 the conv update runs inside the step (lq_gdn_step_conv).
 * A step with prefill tokens: the prefill slots are dequantised to fp32, vLLM's own forward runs (its chunked prefill
   sees ordinary fp32 states), and the slots are re-quantised afterwards.  The decode tokens of such a step reach vLLM's
   fused recurrent decode function, which is intercepted and sent through the HIP step instead, so a decode slot is
@@ -40,9 +40,19 @@ def install(nmax):
         if not is_conv_state_dim_first():
             conv_state = conv_state.transpose(-1, -2)
         w = layer.conv1d.weight
-        mixed = causal_conv1d_update(mixed_qkv[:n], conv_state, w.view(w.size(0), w.size(2)), layer.conv1d.bias,
-                                     layer.activation, conv_state_indices=idx, validate_data=False)
+        w2 = w.view(w.size(0), w.size(2))
         st = _state_of(layer, nmax)
+        bias = layer.conv1d.bias
+        if (conv_state.dtype == torch.bfloat16 and w2.dtype == torch.bfloat16 and w2.shape[1] == 4
+                and (bias is None or bias.dtype == torch.bfloat16) and layer.activation in ("silu", "swish", None)):
+            # bf16 conv of width 4: the conv update runs inside the HIP step (one launch, no round trip of the conv
+            # output through memory)
+            st.decode_conv(layer.kv_cache[1], mixed_qkv[:n].contiguous(), conv_state, w2.contiguous(), bias,
+                           layer.activation is not None, a[:n].contiguous(), b[:n].contiguous(), layer.A_log,
+                           layer.dt_bias, idx, core_attn_out[:n].view(n, st.HV, st.V))
+            return
+        mixed = causal_conv1d_update(mixed_qkv[:n], conv_state, w2, bias, layer.activation, conv_state_indices=idx,
+                                     validate_data=False)
         st.decode(layer.kv_cache[1], mixed.contiguous(), a[:n].contiguous(), b[:n].contiguous(), layer.A_log,
                   layer.dt_bias, idx, core_attn_out[:n].view(n, st.HV, st.V))
 

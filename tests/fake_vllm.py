@@ -43,7 +43,10 @@ def causal_conv1d_update(x, conv_state, weight, bias=None, activation=None, conv
     dev = x.device if ON_DEVICE[0] else torch.device("cpu")
     idx = conv_state_indices.long().to(conv_state.device)
     win = torch.cat([conv_state[idx].float().to(dev), x.float().to(dev)[:, :, None]], -1)     # [n, C, W]
-    y = (win * weight.detach().float().to(dev)[None]).sum(-1)
+    wf = weight.detach().float().to(dev)
+    y = win[..., 0] * wf[None, :, 0]                   # taps accumulated left to right, one rounding per operation
+    for t in range(1, wf.shape[1]):
+        y = y + win[..., t] * wf[None, :, t]
     if bias is not None:
         y = y + bias.detach().float().to(dev)
     conv_state[idx] = win[..., 1:].to(conv_state.dtype).to(conv_state.device)

@@ -137,6 +137,32 @@ def test_other_argument_errors(lib):
     assert lib.lq_dense_step(p, 0, 8, 4, 2, 128, 128, ctypes.byref(io), z) == 0
 
 
+def _conv(**kw):
+    from leapquant_amd import _lib
+    C = 2 * 2 * 128 + 4 * 128
+    d = dict(state=16, weight=32, bias=None, slot_stride=3 * C, ch_stride=3, tap_stride=1, W=4, silu=1)
+    d.update(kw)
+    return _lib.LqConv(**d)
+
+
+def test_fused_conv_entry_points_check_their_arguments(lib):
+    """lq_gdn_step_conv / lq_conv_update: width 4 only, state taps inside a slot, 8-byte aligned weights, null pointers."""
+    z = ctypes.c_void_p(0)
+    st, io = _state(), _io()
+    assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(_conv()), z) == 0      # N = 0
+    for bad in (dict(W=3), dict(silu=2), dict(state=None), dict(weight=None), dict(weight=36), dict(slot_stride=100),
+                dict(ch_stride=0), dict(tap_stride=0)):
+        assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(_conv(**bad)), z) == -1, bad
+        assert lib.lq_conv_update(ctypes.byref(_conv(**bad)), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                                  ctypes.c_void_p(16), 1, 1024, 8, z) == -1, bad
+    assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), None, z) == -1
+    assert lib.lq_gdn_step_conv(ctypes.byref(_state(K=64)), ctypes.byref(io), ctypes.byref(_conv()), z) == -1
+    assert lib.lq_conv_update(ctypes.byref(_conv()), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              0, 1024, 8, z) == 0
+    assert lib.lq_conv_update(ctypes.byref(_conv()), None, ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 1024, 8,
+                              z) == -1
+
+
 def test_python_wrapper_raises_on_status():
     from leapquant_amd import _lib
     _lib.check(0, "x")

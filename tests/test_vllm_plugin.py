@@ -25,6 +25,12 @@ class Recorder:
                                           dt_bias=dt_bias, idx=idx.clone(), out=out)))
         out.fill_(7.0)
 
+    def decode_conv(self, ssm, x, conv_state, conv_weight, conv_bias, silu, a, b, A_log, dt_bias, idx, out):
+        self.calls.append(("decode_conv", dict(ssm=ssm, x=x.clone(), conv_state=conv_state, weight=conv_weight,
+                                               bias=conv_bias, silu=silu, a=a.clone(), b=b.clone(), idx=idx.clone(),
+                                               out=out)))
+        out.fill_(5.0)
+
     def dequantize(self, ssm, idx):
         self.calls.append(("dequantize", idx.clone()))
 
@@ -107,6 +113,29 @@ def test_gdn_decode_only_step_goes_to_leapquant(plugin):
     assert c["out"].shape == (n, HV, K) and c["out"].data_ptr() == out.data_ptr()
     assert bool((out[:n] == 7).all()) and bool((out[n:] == 0).all())
     assert torch.equal(layer.kv_cache[0], conv0)                        # the conv state was advanced for those rows
+
+
+def test_gdn_decode_only_bf16_conv_is_fused(plugin):
+    """A bf16 conv of width 4 goes into the step: decode_conv gets the raw projection and the conv state itself (the
+    conv update is the kernel's), and vLLM's conv update does not run."""
+    layer = gdn_layer()
+    with torch.no_grad():
+        layer.conv1d.weight.data = layer.conv1d.weight.data.to(torch.bfloat16)
+    layer.kv_cache = (layer.kv_cache[0].to(torch.bfloat16), layer.kv_cache[1])
+    conv0 = layer.kv_cache[0].clone()
+    n = 3
+    idx = torch.tensor([2, 0, 5, -1], dtype=torch.int32)
+    FV.CONTEXT.attn_metadata = {layer.prefix: FV.gdn_metadata(n, idx)}
+    mixed_qkv, b, a, out = inputs(4)
+    layer._forward_core(mixed_qkv, b, a, out)
+    st = plugin.rec[id(layer)]
+    (name, c), = st.calls
+    assert name == "decode_conv" and "vllm_core" not in FV.CALLS
+    assert torch.equal(c["x"], mixed_qkv[:n]) and c["conv_state"].data_ptr() == layer.kv_cache[0].data_ptr()
+    assert c["weight"].shape == (2 * H * K + HV * K, 4) and c["silu"] and c["bias"] is None
+    assert torch.equal(c["idx"], idx[:n]) and torch.equal(c["a"], a[:n]) and torch.equal(c["b"], b[:n])
+    assert bool((out[:n] == 5).all()) and bool((out[n:] == 0).all())
+    assert torch.equal(layer.kv_cache[0], conv0)                        # the plugin itself did not touch the state
 
 
 def test_gdn_profiling_run_uses_vllm(plugin):
