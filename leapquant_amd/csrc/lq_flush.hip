@@ -280,33 +280,55 @@ __device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, 
     }
   }
 }
-// KDA key operands, in place: op0 / op1 [c][j] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c]
-// (kernels.py:1453-1463; the running product is taken backwards from the last entry, as there).  Thread per channel c,
-// 8 entries per LDS access.
-__device__ __forceinline__ void kda_key_scan(FlushShared& sh, int h, int LP) {
-  const int c = opaque_tid();
-  if (c >= KD) return;
-  float dcur = 1.0f;
-  for (int j0 = LP - 8; j0 >= 0; j0 -= 8) {
-    const uint4 kr = *(const uint4*)&sh.op[0][c][j0];
-    const uint4 er = *(const uint4*)&sh.op[1][c][j0];
-    const uint32_t ku[4] = {kr.x, kr.y, kr.z, kr.w};
-    const uint32_t eu[4] = {er.x, er.y, er.z, er.w};
-    uint32_t hw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
+// KDA key operands, in place over the raw keys op[0] and decays op[1] ([c][j]): op[0..NT-1] = the NT-term bf16 split
+// (hi, [mid,] lo) of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, state.py:124-127).
+// Four lanes per channel: lane s of a quad takes the s-th quarter of the window (LP / 4 = 8 or 16 entries, held in
+// registers), forms its decay product, takes the product of the later quarters from its neighbours by DPP and walks
+// its quarter backwards from there, as the reference's running product does.  FT = 4 KD threads, all of them take part.
+template <int NT>
+__device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float* wj, int h, int LP) {
+  static_assert(FT == 4 * KD, "one quad of lanes per channel");
+  const int tid = opaque_tid(), c = tid >> 2, s = tid & 3, seg = LP >> 2, jb = s * seg;
+  uint32_t ku[2][4], eu[2][4];
+  float p = 1.0f;
 #pragma unroll
-    for (int e = 7; e >= 0; --e) {
-      const int j = j0 + e;
-      if (j < h) {
-        const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j] * dcur);
-        const bf16_t hi = f2bf(kd);
-        const bf16_t lo = f2bf(kd - bf2f(hi));
-        hw[e >> 1] |= (uint32_t)hi << (16 * (e & 1));
-        lw[e >> 1] |= (uint32_t)lo << (16 * (e & 1));
-        dcur = dcur * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
-      }
+  for (int x = 1; x >= 0; --x) {
+    if (8 * x < seg) {
+      const uint4 kr = *(const uint4*)&op[0][c][jb + 8 * x];
+      const uint4 er = *(const uint4*)&op[1][c][jb + 8 * x];
+      ku[x][0] = kr.x; ku[x][1] = kr.y; ku[x][2] = kr.z; ku[x][3] = kr.w;
+      eu[x][0] = er.x; eu[x][1] = er.y; eu[x][2] = er.z; eu[x][3] = er.w;
+#pragma unroll
+      for (int e = 7; e >= 0; --e)
+        if (jb + 8 * x + e < h) p = p * h2f((f16_t)(eu[x][e >> 1] >> (16 * (e & 1))));
     }
-    *(uint4*)&sh.op[0][c][j0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-    *(uint4*)&sh.op[1][c][j0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
+  }
+  const float p1 = dpp<0x55>(p), p2 = dpp<0xaa>(p), p3 = dpp<0xff>(p);   // quarter products of lanes 1..3
+  float dcur = s < 3 ? p3 : 1.0f;
+  if (s < 2) dcur = dcur * p2;
+  if (s < 1) dcur = dcur * p1;
+#pragma unroll
+  for (int x = 1; x >= 0; --x) {
+    if (8 * x < seg) {
+      const int j0 = jb + 8 * x;
+      uint32_t tw[NT][4] = {};
+#pragma unroll
+      for (int e = 7; e >= 0; --e) {
+        const int j = j0 + e;
+        if (j < h) {
+          float r = bf2f((bf16_t)(ku[x][e >> 1] >> (16 * (e & 1)))) * (wj[j] * dcur);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const bf16_t b = f2bf(r);
+            tw[t][e >> 1] |= (uint32_t)b << (16 * (e & 1));
+            r = r - bf2f(b);
+          }
+          dcur = dcur * h2f((f16_t)(eu[x][e >> 1] >> (16 * (e & 1))));
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *(uint4*)&op[t][c][j0] = make_uint4(tw[t][0], tw[t][1], tw[t][2], tw[t][3]);
+    }
   }
 }
 
@@ -430,7 +452,7 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   store_window<KDA>(sh, win, L, LP);
   __syncthreads();
   if (KDA) {
-    kda_key_scan(sh, L, LP);
+    kda_key_scan<2>(sh.op, sh.w, L, LP);
     __syncthreads();
   }
 
@@ -883,36 +905,7 @@ void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     }
   }
   __syncthreads();
-  // decayed keys, thread per channel, backward from the last live entry (state.py:124-127); 8 entries per access
-  if (tid < KD) {
-    const int c = tid;
-    float dcur = 1.0f;
-    for (int j0 = LP - 8; j0 >= 0; j0 -= 8) {
-      const uint4 kr = *(const uint4*)&sh.op[0][c][j0];
-      const uint4 er = *(const uint4*)&sh.op[1][c][j0];
-      const uint32_t ku[4] = {kr.x, kr.y, kr.z, kr.w};
-      const uint32_t eu[4] = {er.x, er.y, er.z, er.w};
-      uint32_t hw[4] = {0u, 0u, 0u, 0u}, mw[4] = {0u, 0u, 0u, 0u}, lw[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 7; e >= 0; --e) {
-        const int j = j0 + e;
-        if (j < h) {
-          const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j] * dcur);
-          const bf16_t hi = f2bf(kd);
-          const float r1 = kd - bf2f(hi);
-          const bf16_t mid = f2bf(r1);
-          const bf16_t lo = f2bf(r1 - bf2f(mid));
-          hw[e >> 1] |= (uint32_t)hi << (16 * (e & 1));
-          mw[e >> 1] |= (uint32_t)mid << (16 * (e & 1));
-          lw[e >> 1] |= (uint32_t)lo << (16 * (e & 1));
-          dcur = dcur * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
-        }
-      }
-      *(uint4*)&sh.op[0][c][j0] = make_uint4(hw[0], hw[1], hw[2], hw[3]);
-      *(uint4*)&sh.op[1][c][j0] = make_uint4(mw[0], mw[1], mw[2], mw[3]);
-      *(uint4*)&sh.op[2][c][j0] = make_uint4(lw[0], lw[1], lw[2], lw[3]);
-    }
-  }
+  kda_key_scan<3>(sh.op, sh.w, h, LP);                // decayed keys, hi / mid / lo (state.py:124-127)
   // S0 pc in the tile layout: (code Sk / qmax) Sv + sum_r Q[v][r] U[c][r], times exp(P[c]) (state.py:121-122, 128)
   Tile t;
   {
