@@ -281,11 +281,14 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   // keys), and the int8 tile last.  Everything built on the window -- key dots, A4 / A5 -- runs while the tile still
   // streams; after the tile's last bytes only the GEMV, the delta rule and the stores remain.
   // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction (the loop holds no compiler-visible
-  // load, so it adds no wait)
+  // load, so it adds no wait); rows past the buffer's last (L not a multiple of 4) re-read it
   {
     const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
     const int nch = live ? (h + 3) >> 2 : 0;
-    for (int c = wi; c < nch; c += 2) lds_load16(ubg + c * 1024 + 16 * lane, (char*)&sh.ub[g][0][0] + c * 1024);
+    for (int c = wi; c < nch; c += 2) {
+      const int row = min(4 * c + (lane >> 4), L - 1);
+      lds_load16(ubg + row * (VD * 2) + 16 * (lane & 15), (char*)&sh.ub[g][0][0] + c * 1024);
+    }
   }
   __builtin_amdgcn_sched_barrier(0);
   // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
@@ -477,23 +480,49 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
 //   * u = beta (v - (m + A6 + A4)), y = y_q + A7 + A5 + kappa u (kernels.py:1065-1066).
 // ------------------------------------------------------------------------------------------------------------------
 struct KdaShared {
-  bf16_t ub[LMAX][VD];      // window values u_j
-  union {
-    bf16_t kb[LMAX][KD];    // window keys K_j (of the key head), read by the decay scan only
-    struct {
-      float2 mq[VD];        // GEMV rows (k, q) in digit units
-      float2 cwq[LMAX];     // (w_j dk_j, w_j dq_j)
-    } post;                 // written after the scan
-  };
   f16_t gk[LMAX][KD];       // window step decays e_j; the scan overwrites entry j with the decayed key K~_j (bf16)
+  float2 part[2][VD];       // per wave: (A4, A5) sums of row v over the wave's window entries
+  float2 mq[VD];            // GEMV rows (k, q) in digit units
+  float2 cwq[LMAX];         // (w_j dk_j, w_j dq_j)
+  float2 dhand[KD / 2];     // running decay product after wave 1's entries, channel pairs (2 p, 2 p + 1)
   int8_t dig[6][KD];        // int8 GEMV B operand: k digits 0-2, q digits 0-2
   bf16_t bkq[6][KD];        // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
   f16_t hkq[4][KD];         // factor-dot B operand: fp16 hi / lo of 64 pc kn, then of 64 pc qn
   float2 duq[4];            // (dU_r, dQ_r)
   float w[LMAX];            // entry weights w_j = Wbuf[j]
-  float en[KD];             // exp(g) per channel: the scan's first factor
   float sc[8];              // beta, kappa, kmax, qmax
+  f16_t uq[4][KD + VD];     // the checkpoint's factor rows (U_r | Q_r), fp16
 };
+
+// per-channel gate g (kernels.py:704-712, 802): glb sigmoid(e^A_log (a + dt_bias)) (glb != 0), else -e^A_log softplus
+__device__ __forceinline__ float kda_gate(float a, float dt, float ea, float glb) {
+  const float xg = a + dt;
+  return glb != 0.f ? glb / (1.0f + expf(-ea * xg)) : -ea * softplus20f(xg);
+}
+
+// Decayed keys K~_j = bf16(K_j dcur), dcur *= e_j, backwards over rows jb + cnt - 1 .. jb of the window (kernels.py:
+// 966-979), for the lane's channel pair (2 lane, 2 lane + 1): raw keys from registers, decays read from LDS and
+// overwritten in place by K~.  8 rows per pass, the pass's LDS reads first.
+__device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr)[32], int jb, int cnt, int lane,
+                                              float& d0, float& d1) {
+#pragma unroll
+  for (int g8 = 3; g8 >= 0; --g8) {
+    if (8 * g8 < cnt) {
+      uint32_t ev[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) ev[i] = *(const uint32_t*)&sh.gk[jb + 8 * g8 + i][2 * lane];
+#pragma unroll
+      for (int i = 7; i >= 0; --i) {
+        const int r = 8 * g8 + i;
+        if (r < cnt) {
+          *(uint32_t*)&sh.gk[jb + r][2 * lane] = pk_bf16(bf_lo(kr[r]) * d0, bf_hi(kr[r]) * d1);
+          d0 = d0 * h2f((f16_t)(ev[i] & 0xffffu));
+          d1 = d1 * h2f((f16_t)(ev[i] >> 16));
+        }
+      }
+    }
+  }
+}
 
 __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io io, float glb) {
   __shared__ KdaShared sh;
@@ -520,47 +549,57 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   // the CU's other workgroups have issued, and every later load of this workgroup would wait for it).
   const int hfill = st.hcnt[sh_];
   __builtin_amdgcn_sched_barrier(0);
-  // per-channel operands of channels c = lane, lane + 64 (scalar wave) and of row lt (all lanes)
+  // per-channel operands: wave 0 (scalar work) channels c = lane, lane + 64; wave 1 (its own gate) c = 2 lane + e
   bf16_t kxr[2], qxr[2], axr[2];
   float skx[2], dtx[2], pbx[2], wx[2];
 #pragma unroll
   for (int e = 0; e < 2; ++e) {
     const int c = lane + 64 * e;
+    const int cg = wi ? 2 * lane + e : c;
     kxr[e] = mrow[H * KD + hk * KD + c];
     qxr[e] = mrow[hk * KD + c];
-    axr[e] = ((const bf16_t*)io.a)[((long long)n * HV + hv) * KD + c];
+    axr[e] = ((const bf16_t*)io.a)[((long long)n * HV + hv) * KD + cg];
     skx[e] = Skp[c];
-    dtx[e] = io.dt_bias[hv * KD + c];
+    dtx[e] = io.dt_bias[hv * KD + cg];
     pbx[e] = st.Pbuf[sh_ * KD + c];
     wx[e] = st.Wbuf[sh_ * L + min(c, L - 1)];
   }
   const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
   const float alog = io.A_log[hv];
-  f16x8 ufr[4];                 // factor rows U^T_r (fp16): A fragment row m = r of the factor-dot MFMA
-  {
-    const int r = n16 < R ? n16 : 0;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) ufr[ks] = *(const f16x8*)(UQp + r * (KD + VD) + 32 * ks + 8 * q4);
-  }
   const float vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
-  float qt[4];
-#pragma unroll
-  for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   __builtin_amdgcn_sched_barrier(0);
   const int h = hfill;
   if (h >= L) { out[lt] = 0; return; }    // a full window is never stepped (the flush follows every step)
-  // window rows j < h straight to LDS, 1 KiB (4 rows) per wave instruction; then the int8 tile
+  // the four factor rows (2 KiB, inside the checkpoint block whatever R) to LDS, one KiB per wave
+  lds_load16((const char*)UQp + 1024 * wi + 16 * lane, (char*)&sh.uq[2 * wi][0]);
+  // The window's live entries j < h split between the waves: wave 0 takes [0, h0), wave 1 [h0, h), h0 a multiple of 4
+  // (or h), each at most 32 entries.  Each wave's decays go straight to its own LDS rows (1 KiB = 4 rows per wave
+  // instruction, rows past the buffer's last re-reading it); its values u_j and keys K_j go to registers, a channel
+  // pair (2 lane, 2 lane + 1) per lane and row.  Then the int8 tile.
+  const int h0 = min(h, 4 * ((h + 7) >> 3));
+  const int jb = wi ? h0 : 0, cnt = wi ? h - h0 : h0;
+  uint32_t ur[32], kr[32];
   {
-    const int nch = (h + 3) >> 2;
-    const char* ug = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
-    const char* kg = (const char*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD);
     const char* gg = (const char*)((const f16_t*)st.Gbuf + sh_ * L * KD);
-    for (int c = wi; c < nch; c += 2) {
-      lds_load16(ug + c * 1024 + 16 * lane, (char*)&sh.ub[0][0] + c * 1024);
-      lds_load16(kg + c * 1024 + 16 * lane, (char*)&sh.kb[0][0] + c * 1024);
-      lds_load16(gg + c * 1024 + 16 * lane, (char*)&sh.gk[0][0] + c * 1024);
+    for (int r = 0; r < cnt; r += 4) {
+      const int row = min(jb + r + q4, L - 1);
+      lds_load16(gg + row * (KD * 2) + 16 * n16, (char*)&sh.gk[jb + r][0]);
     }
+    const uint32_t* ug = (const uint32_t*)((const bf16_t*)st.Ubuf + sh_ * L * VD) + lane;
+    const uint32_t* kg = (const uint32_t*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD) + lane;
+#pragma unroll
+    for (int g4 = 0; g4 < 8; ++g4)
+      if (4 * g4 < cnt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ur[4 * g4 + i] = ug[(jb + min(4 * g4 + i, cnt - 1)) * (VD / 2)];
+      }
+#pragma unroll
+    for (int g4 = 0; g4 < 8; ++g4)
+      if (4 * g4 < cnt) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) kr[4 * g4 + i] = kg[(jb + min(4 * g4 + i, cnt - 1)) * (KD / 2)];
+      }
   }
   __builtin_amdgcn_sched_barrier(0);
   i32x4 afr[4][2];
@@ -571,23 +610,21 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
   }
-  constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the window's LDS loads: the tile
+  constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the window's loads: the tile
   __builtin_amdgcn_sched_barrier(0);
+  const float ea = expf(alog);
 
-  // ---- scalar wave: per-channel gate, norms, digits, dot operands ----
+  // ---- wave 0: per-channel gate, norms, digits, dot operands.  wave 1: its own entries' decayed keys ----
   float gnv[2] = {0.f, 0.f}, env[2] = {0.f, 0.f};
   if (wi == 0) {
-    const float ea = expf(alog);
     const float beta = beta_f(bf2f(braw));
     float pcv[2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) {
-      const float xg = bf2f(axr[e]) + dtx[e];
-      const float g = glb != 0.f ? glb / (1.0f + expf(-ea * xg)) : -ea * softplus20f(xg);
+      const float g = kda_gate(bf2f(axr[e]), dtx[e], ea, glb);
       gnv[e] = pbx[e] + g;
       pcv[e] = expf(gnv[e]);
       env[e] = expf(g);
-      sh.en[lane + 64 * e] = env[e];
     }
     const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
     float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
@@ -636,72 +673,31 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       if (c < L) sh.w[c] = wx[e];
     }
     if (lane == 0) { sh.sc[0] = beta; sh.sc[1] = kappa; sh.sc[2] = kmax; sh.sc[3] = qmax; }
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");   // own window rows landed
+  } else {
+    // the scan starts at exp(g) of the channel (the same gate as wave 0's, so the same bits) and runs over wave 1's
+    // entries first; the product it reaches is where wave 0's entries continue
+    float d0 = expf(kda_gate(bf2f(axr[0]), dtx[0], ea, glb));
+    float d1 = expf(kda_gate(bf2f(axr[1]), dtx[1], ea, glb));
+    asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");   // own decay rows in LDS, keys in registers
+    kda_scan_rows(sh, kr, jb, cnt, lane, d0, d1);
+    sh.dhand[lane] = make_float2(d0, d1);
   }
-  // this wave's window rows have landed in LDS (they precede only the tile in the counter) ...
-  asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
-  __syncthreads();              // ... and the other wave's, with the gate, digits and dot operands
+  __syncthreads();              // gate, digits, dot operands, w_j, factor rows; wave 1's decayed keys and hand-over
 
-  // ---- decay scan, channel c = lt, backward over the live entries, 8 entries per pass (reads first) ----
-  {
-    const int c = lt;
-    float dcur = sh.en[c];
-    int j1 = h;                 // entries j1 - 8 .. j1 - 1 in this pass
-    for (; j1 >= 8; j1 -= 8) {
-      float kbv[8], ev[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        kbv[i] = bf2f(sh.kb[j1 - 1 - i][c]);
-        ev[i] = h2f(sh.gk[j1 - 1 - i][c]);
-      }
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        ((bf16_t*)&sh.gk[j1 - 1 - i][0])[c] = f2bf(kbv[i] * dcur);
-        dcur = dcur * ev[i];
-      }
-    }
-    for (int j = j1 - 1; j >= 0; --j) {
-      const float kbv = bf2f(sh.kb[j][c]);
-      const float ev = h2f(sh.gk[j][c]);
-      ((bf16_t*)&sh.gk[j][0])[c] = f2bf(kbv * dcur);
-      dcur = dcur * ev;
-    }
-  }
-  __syncthreads();              // decayed keys of every channel are in LDS
-
-  // ---- decayed-key dots: 16-row tiles t = wi, wi + 2, ... of K~ against bf16 (hi, mid, lo) of kn (0-2), qn (4-6) ----
-  {
-    bf16x8 bk[4];
-    const bool bcol = (n16 & 3) < 3 && n16 < 8;
-    const int brow = bcol ? (n16 >> 2) * 3 + (n16 & 3) : 0;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 b = *(const bf16x8*)&sh.bkq[brow][32 * ks + 8 * q4];
-      bk[ks] = bcol ? b : bf16x8{};
-    }
-    for (int t = wi; 16 * t < h; t += 2) {
-      const int j0 = 16 * t;
-      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 a = *(const bf16x8*)((const bf16_t*)&sh.gk[j0 + n16][0] + 32 * ks + 8 * q4);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bk[ks], acc, 0, 0, 0);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
-        const int j = j0 + 4 * q4 + i;
-        if ((n16 == 0 || n16 == 4) && j < h) ((float*)&sh.post.cwq[j])[n16 >> 2] = sh.w[j] * s;
-      }
-    }
-  }
-  // ---- factor dots (wave 1): U^T rows against fp16 (hi, lo) of 64 pc kn (columns 0, 1) and 64 pc qn (2, 3) ----
-  if (wi == 1) {
-    f16x8 bh[4];
+  if (wi == 0) {
+    float2 d = sh.dhand[lane];
+    kda_scan_rows(sh, kr, jb, cnt, lane, d.x, d.y);
+  } else {
+    // ---- factor dots: U^T rows against fp16 (hi, lo) of 64 pc kn (columns 0, 1) and 64 pc qn (2, 3) ----
+    f16x8 bh[4], ufr[4];        // ufr: A fragment row m = r (U^T_r, fp16)
     const bool bcol = n16 < 4;
+    const int r = n16 < R ? n16 : 0;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       const f16x8 b = *(const f16x8*)&sh.hkq[bcol ? n16 : 0][32 * ks + 8 * q4];
       bh[ks] = bcol ? b : f16x8{};
+      ufr[ks] = *(const f16x8*)&sh.uq[r][32 * ks + 8 * q4];
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -713,36 +709,53 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       if ((n16 == 0 || n16 == 2) && r < R) ((float*)&sh.duq[r])[n16 >> 1] = s;
     }
   }
-  __syncthreads();              // key dots and factor dots are in LDS
-
-  // ---- row v = lt: buffered entries, rank-R part, then the GEMV (the tile arrives last) and the delta rule ----
-  float a4 = 0.f, a5 = 0.f;
-  int j = 0;
-  for (; j + 4 <= h; j += 4) {  // four entries' LDS reads in flight at once; the sums keep the order of j
-    float ubv[4];
-    float2 cc[4];
+  // ---- decayed-key dots of this wave's entries, 16-row tiles from jb (rows past the wave's own are not kept) ----
+  bf16x8 bk[4];                 // B operand: columns 0-2 hi / mid / lo of kn, 4-6 of qn
+  {
+    const bool bcol = (n16 & 3) < 3 && n16 < 8;
+    const int brow = bcol ? (n16 >> 2) * 3 + (n16 & 3) : 0;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      ubv[e] = bf2f(sh.ub[j + e][lt]);
-      cc[e] = sh.post.cwq[j + e];
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      a4 = fmaf(ubv[e], cc[e].x, a4);
-      a5 = fmaf(ubv[e], cc[e].y, a5);
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 b = *(const bf16x8*)&sh.bkq[brow][32 * ks + 8 * q4];
+      bk[ks] = bcol ? b : bf16x8{};
     }
   }
-  for (; j < h; ++j) {
-    const float ubv = bf2f(sh.ub[j][lt]);
-    const float2 cc = sh.post.cwq[j];
-    a4 = fmaf(ubv, cc.x, a4);
-    a5 = fmaf(ubv, cc.y, a5);
+  for (int j0 = jb; j0 < jb + cnt; j0 += 16) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const bf16x8 a = *(const bf16x8*)((const bf16_t*)&sh.gk[j0 + n16][0] + 32 * ks + 8 * q4);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bk[ks], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
+      const int j = j0 + 4 * q4 + i;
+      if ((n16 == 0 || n16 == 4) && j < jb + cnt) ((float*)&sh.cwq[j])[n16 >> 2] = sh.w[j] * s;
+    }
   }
-  float a6 = 0.f, a7 = 0.f;
-  for (int r = 0; r < R; ++r) {
-    const float2 d = sh.duq[r];
-    a6 = fmaf(qt[r], d.x, a6);
-    a7 = fmaf(qt[r], d.y, a7);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's own cwq rows: LDS round trip within the wave
+  // ---- A4 / A5 over this wave's entries for rows v = 2 lane, 2 lane + 1, in the order of j ----
+  {
+    float a40 = 0.f, a50 = 0.f, a41 = 0.f, a51 = 0.f;
+#pragma unroll
+    for (int g8 = 0; g8 < 4; ++g8) {
+      if (8 * g8 < cnt) {
+        float2 cc[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) cc[i] = sh.cwq[min(jb + 8 * g8 + i, LMAX - 1)];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          const int r = 8 * g8 + i;
+          if (r < cnt) {
+            const float u0 = bf_lo(ur[r]), u1 = bf_hi(ur[r]);
+            a40 = fmaf(u0, cc[i].x, a40); a50 = fmaf(u0, cc[i].y, a50);
+            a41 = fmaf(u1, cc[i].x, a41); a51 = fmaf(u1, cc[i].y, a51);
+          }
+        }
+      }
+    }
+    *(float4*)&sh.part[wi][2 * lane] = make_float4(a40, a50, a41, a51);
   }
   {
     i32x4 bfr[2];
@@ -762,13 +775,24 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       for (int i = 0; i < 4; ++i) {
         const float c0 = (float)acc[i];
         const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
-        if (n16 == 8 || n16 == 9) ((float*)&sh.post.mq[64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
+        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
       }
     }
   }
-  // rows 64 wi .. 64 wi + 63 of the GEMV are this wave's own rows: LDS round trip within the wave, no barrier
+  __syncthreads();              // both waves' A4 / A5 sums and the factor dots are in LDS
+
+  // ---- row v = lt: buffered entries, rank-R part, the GEMV and the delta rule ----
+  const float2 p0 = sh.part[0][lt], p1 = sh.part[1][lt];
+  const float a4 = p0.x + p1.x, a5 = p0.y + p1.y;
+  float a6 = 0.f, a7 = 0.f;
+  for (int r = 0; r < R; ++r) {
+    const float2 d = sh.duq[r];
+    const float qt = h2f(sh.uq[r][KD + lt]);
+    a6 = fmaf(qt, d.x, a6);
+    a7 = fmaf(qt, d.y, a7);
+  }
   const float beta = sh.sc[0], kappa = sh.sc[1];
-  const float2 mqr = sh.post.mq[lt];
+  const float2 mqr = sh.mq[lt];
   const float mq = (mqr.x * (sh.sc[2] * (1.0f / DIGIT_SCALE))) * sv;
   const float yq = (mqr.y * (sh.sc[3] * (1.0f / DIGIT_SCALE))) * sv;
   const float u = beta * (vin - (mq + a6 + a4));        // kernels.py:1065

@@ -43,6 +43,36 @@ def _run_step(lq, ssm, mixed, a, b, A_log, dt_bias, idx):
     return out.float().cpu().numpy()
 
 
+@pytest.mark.parametrize("kda", [False, True])
+@pytest.mark.parametrize("L", [64, 13])
+def test_step_at_every_fill(kda, L):
+    """One step on slots at chosen window fills: empty, a single entry, the 4-row load boundaries, both sides of the
+    KDA step's split of the window between its two waves (multiples of 4 and 8), the last fill before the window is
+    full; L = 13 also has windows whose 4-row loads reach past the buffer's last row."""
+    fills = ([0, 1, 3, 4, 5, 8, 9, 15, 16, 17, 24, 31, 32, 33, 40, 47, 48, 62, 63] if L == 64
+             else [0, 1, 2, 3, 4, 5, 7, 8, 9, 11, 12])
+    rng = np.random.default_rng(300 + L + 7 * kda)
+    NS, HV = len(fills) + 1, 2
+    H = HV if kda else 1
+    st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda)
+    A_log, dt_bias = gate_params(HV, 128, kda)
+    target = np.array([0] + fills)
+    for t in range(max(fills)):            # slot s takes fills[s - 1] steps (none reaches L: no flush fires)
+        sl = np.nonzero(target > t)[0].astype(np.int64)
+        mixed, a, b = make_inputs(rng, len(sl), HV, H, kda=kda)
+        (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, sl)
+        O.flush(st, Q0, sl)
+    assert np.array_equal(st["hcnt"][1:, 0], fills)
+    idx = rng.permutation(np.arange(1, NS)).astype(np.int64)
+    mixed, a, b = make_inputs(rng, len(idx), HV, H, kda=kda)
+    ssm, lq = G.to_gpu(st)
+    o_ref = (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, idx)
+    o_gpu = _run_step(lq, ssm, *G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx))
+    np.testing.assert_allclose(o_gpu, o_ref, rtol=RT, atol=AT)
+    assert (G.bf16_ulps(o_gpu, o_ref) <= 2).mean() > 0.99
+    _assert_step_state(G.from_gpu(ssm, lq), st, idx)
+
+
 def _run_flush(lq, ssm, idx):
     v = lq.views(ssm)
     Gb = lq.Gbuf.view(torch.bfloat16) if lq.kda else lq.Gd
@@ -52,10 +82,12 @@ def _run_flush(lq, ssm, idx):
 
 
 def _assert_step_state(g, r, slots_touched):
-    """Window appends and scalars after one step: bf16 appends within 1 ulp, fp32 scalars to 1e-6."""
+    """Window appends and scalars after one step: bf16 appends within 1 ulp (or 1e-6 absolute: u = beta (v - pred) can
+    cancel to ~1e-8, where the fp32 rounding of O(1) terms is many bf16 ulps of the result), fp32 scalars to 1e-6."""
     assert np.array_equal(g["hcnt"], r["hcnt"])
-    assert G.bf16_ulps(g["Ubuf"], r["Ubuf"]).max() <= 1
-    assert G.bf16_ulps(g["Kbuf"], r["Kbuf"]).max() <= 1
+    for k in ("Ubuf", "Kbuf"):
+        bad = (G.bf16_ulps(g[k], r[k]) > 1) & (np.abs(g[k] - r[k]) > 1e-6)
+        assert not bad.any(), (k, np.argwhere(bad)[:4])
     np.testing.assert_allclose(g["Wbuf"], r["Wbuf"], rtol=1e-6, atol=0)
     np.testing.assert_allclose(g["Pbuf"], r["Pbuf"], rtol=1e-6, atol=0)
     if r["kda"]:
