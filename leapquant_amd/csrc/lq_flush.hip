@@ -187,11 +187,19 @@ __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
   }
 }
 
-// the 8 code words of the lane's tile entries (issued early; consumed by tile_from_words)
+// the 8 code words of the lane's tile entries (issued early; consumed by tile_from_words).  A head of K_ x V_ < 128 x
+// 128 sits zero-padded in the tile: entries past its rows / columns read as 0 (clamped addresses, no divergent load).
+template <int K_ = KD, int V_ = VD>
 __device__ __forceinline__ void load_code_words(uint32_t wds[8], const int8_t* Sq) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
+  const int c = 16 * w + 4 * q;
+  const bool cok = K_ == KD || c < K_;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) wds[nt] = *(const uint32_t*)(Sq + (16 * nt + (l & 15)) * KD + 16 * w + 4 * q);
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    const uint32_t x = *(const uint32_t*)(Sq + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
+    wds[nt] = (cok && (V_ == VD || v < V_)) ? x : 0u;
+  }
 }
 // Tile init with the dequantised checkpoint codes  x svr[v] x skl[c]
 __device__ __forceinline__ void tile_from_words(Tile& t, const uint32_t wds[8], const float* svr, const float* skl) {
@@ -230,18 +238,21 @@ struct WinRegs {
 };
 __device__ __forceinline__ int win_pair(int LP) { return opaque_tid() % (LP / 2); }
 __device__ __forceinline__ int win_chunk(int LP) { return opaque_tid() / (LP / 2); }
-template <bool KDA>
+template <bool KDA, int K_ = KD, int V_ = VD>
 __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int slot, int hv, int h, int LP) {
   const int G = st.HV / st.H, hk = hv / G, L = st.L;
-  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * KD;
-  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * VD;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
   const f16_t* Gb = KDA ? (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD : nullptr;
   const int jp = win_pair(LP), c8 = min(win_chunk(LP), 15) * 8;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);       // columns past a K_ / V_ < 128 head: zero operands
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int j = 2 * jp + k, jr = j < h ? j : 0;
-    r.k[k] = *(const uint4*)(Kb + (long long)jr * KD + c8);
-    r.u[k] = *(const uint4*)(Ub + (long long)jr * VD + c8);
+    const uint4 kx = *(const uint4*)(Kb + (long long)jr * K_ + (K_ == KD ? c8 : min(c8, K_ - 8)));
+    const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
+    r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
+    r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
     if (KDA) r.g[k] = *(const uint4*)(Gb + (long long)jr * KD + c8);
   }
 }
@@ -387,17 +398,21 @@ __device__ __forceinline__ f32x4 p_step(const FlushShared& sh, const f16x4 bt[8]
   return p;
 }
 
-template <bool KDA>
+// A GDN head of K_ x V_ < 128 x 128 (kernels.py:1089: (64, 128), (64, 64)) runs zero-padded in the 128 x 128 tile:
+// its loads read zeros past its rows / columns, every product and Gram sum then only adds exact zeros, the column
+// means divide by V_, and the stores write its own rows / columns only.
+template <bool KDA, int K_ = KD, int V_ = VD>
 __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                            float qmax) {
+  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
   char* base = block_base(st, slot, hv);
   int8_t* Sq = (int8_t*)base;
-  float* Sk = (float*)(base + VD * KD);
-  float* Sv = Sk + KD;
-  f16_t* UQ = (f16_t*)(Sv + VD);
+  float* Sk = (float*)(base + V_ * K_);
+  float* Sv = Sk + K_;
+  f16_t* UQ = (f16_t*)(Sv + V_);
   const int LP = (L + 31) & ~31;
 
   // ---- stage 1: every load of the head up front (scalars, scales, factors, window rows, code words) ----
@@ -408,19 +423,25 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   }
   const int cv = tid & 127;                           // column (tid < 128) or row (128 <= tid < 256) of the stage-1 loads
   const bool colt = tid < KD;
-  const float scv = colt ? Sk[cv] : Sv[cv];
+  const int nc = colt ? K_ : V_;                      // this thread's column / row count
+  const bool cok = (K_ == KD && V_ == VD) || cv < nc;
+  const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
+  const int vq = V_ == VD ? cv : min(cv, V_ - 1);
+  const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
   float uqv[4], q0v[4];
 #pragma unroll
   for (int a = 0; a < 4; ++a) {
-    uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
-    q0v[a] = Q0[cv * R + min(a, R - 1)];
+    const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
+    uqv[a] = cok ? x : 0.f;
+    const float y = Q0[vq * R + min(a, R - 1)];
+    q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
   }
   const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window<KDA>(win, st, slot, hv, L, LP);
+  load_window<KDA, K_, V_>(win, st, slot, hv, L, LP);
   uint32_t wds[8];
-  load_code_words(wds, Sq);
+  load_code_words<K_, V_>(wds, Sq);
 
   if (tid < KD) {
     const int c = cv;
@@ -575,10 +596,10 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
     }
     // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
     const int ic = l & 3;
-    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / VD);
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
     const float sq = sqrtf(msum);
     const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
-    if (l16 < 4) Sk[16 * w + 4 * q + l16] = fmaxf(sq, LQ_EPS);
+    if (l16 < 4 && (K_ == KD || 16 * w + 4 * q + l16 < K_)) Sk[16 * w + 4 * q + l16] = fmaxf(sq, LQ_EPS);
     rsk[0] = dpp<0x00>(rs);                           // quad_perm [i, i, i, i]: column i of the lane's quad
     rsk[1] = dpp<0x55>(rs);
     rsk[2] = dpp<0xaa>(rs);
@@ -601,7 +622,7 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 #pragma unroll
     for (int k = 1; k < 4 * NW; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
     const float rmax = fmaxf(m, LQ_EPS);
-    Sv[tid] = rmax;
+    if (V_ == VD || tid < V_) Sv[tid] = rmax;
     sh.r.rq[tid] = qmax * (1.0f / rmax);
   }
   __syncthreads();
@@ -613,14 +634,15 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 #pragma unroll
     for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
     const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
-    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_))
+      *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
-  if (q == 0) {
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + 16 * w + l16] = f2h(u16[r]);
+  if (q == 0 && (K_ == KD || 16 * w + l16 < K_)) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + 16 * w + l16] = f2h(u16[r]);
   }
-  if (tid < VD) {
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + tid] = f2h(sh.qv[tid][r]);
+  if (tid < V_) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
   }
   if (KDA) {
     if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
@@ -639,7 +661,7 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 // (wave 0, one per lane), and processes the due ones (slot > 0, hcnt == L; kernels.py:1200) one after another.
 // With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
 // otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
-template <bool KDA>
+template <bool KDA, int K_ = KD, int V_ = VD>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax) {
   __shared__ FlushShared sh;
@@ -667,7 +689,7 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
       m &= m - 1;
       const int p = base + stride * b;
       const int n = p / HV, hv = p - n * HV;
-      flush_head<KDA>(sh, st, Q0, idx[n], hv, qmax);
+      flush_head<KDA, K_, V_>(sh, st, Q0, idx[n], hv, qmax);
     }
   }
   if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
@@ -693,9 +715,10 @@ struct QuantShared {
   float sk[KD];
 };
 
-template <bool KDA>
+template <bool KDA, int K_ = KD, int V_ = VD>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax, int iters) {
+  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
   __shared__ QuantShared sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
@@ -705,15 +728,20 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   char* base = block_base(st, slot, hv);
   const float* S = (const float*)base;
-  Tile t;
+  Tile t;                                             // a K_ x V_ < 128 x 128 head zero-padded (see flush_head)
+  {
+    const int c = 16 * w + 4 * q;
+    const bool cok = K_ == KD || c < K_;
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const float4 x = *(const float4*)(S + (16 * nt + (l & 15)) * KD + 16 * w + 4 * q);
-    t.a[nt] = f32x4{x.x, x.y, x.z, x.w};
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const float4 x = *(const float4*)(S + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
+      t.a[nt] = (cok && (V_ == VD || v < V_)) ? f32x4{x.x, x.y, x.z, x.w} : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
   }
   if (tid < VD) {
     f32x4 q0v;
-    for (int r = 0; r < 4; ++r) q0v[r] = r < R ? Q0[tid * R + r] : 0.f;
+    for (int r = 0; r < 4; ++r) q0v[r] = (r < R && tid < V_) ? Q0[tid * R + r] : 0.f;
     sh.qv[tid] = q0v;
   }
   __syncthreads();
@@ -773,7 +801,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
       s += fabsf(e);
     }
     s = sum16(s);
-    const float skc = fmaxf(sqrtf(s / (float)VD), LQ_EPS);      // kernels.py:2222
+    const float skc = fmaxf(sqrtf(s / (float)V_), LQ_EPS);      // kernels.py:2222
     if ((l & 15) == 0) sh.sk[16 * w + 4 * q + i] = skc;
   }
   __syncthreads();
@@ -792,9 +820,9 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   __syncthreads();
   // every read of the fp32 state is done: the checkpoint may now overwrite the block
   int8_t* Sq = (int8_t*)base;
-  float* Sk = (float*)(base + VD * KD);
-  float* Sv = Sk + KD;
-  f16_t* UQ = (f16_t*)(Sv + VD);
+  float* Sk = (float*)(base + V_ * K_);
+  float* Sv = Sk + K_;
+  f16_t* UQ = (f16_t*)(Sv + V_);
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
@@ -806,15 +834,20 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
       const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
       word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
     }
-    *(uint32_t*)(Sq + v * KD + 16 * w + 4 * q) = word;
-    if (w == 0 && q == 0) Sv[v] = svv;
+    if (V_ == VD || v < V_) {
+      if (K_ == KD || 16 * w + 4 * q < K_) *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = word;
+      if (w == 0 && q == 0) Sv[v] = svv;
+    }
   }
   if (tid < KD) {
-    Sk[tid] = sh.sk[tid];
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + tid] = f2h(sh.pp[tid][r]);
+    if (K_ == KD || tid < K_) {
+      Sk[tid] = sh.sk[tid];
+      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + tid] = f2h(sh.pp[tid][r]);
+    }
   } else if (tid < KD + VD) {
     const int v = tid - KD;
-    for (int r = 0; r < R; ++r) UQ[r * (KD + VD) + KD + v] = f2h(sh.qv[v][r]);
+    if (V_ == VD || v < V_)
+      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + v] = f2h(sh.qv[v][r]);
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (KDA) {
@@ -940,8 +973,10 @@ void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place
+// prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place.  A head
+// of K_ x V_ < 128 x 128 runs zero-padded in the tile (see flush_head) and writes its own rows / columns only.
 // ------------------------------------------------------------------------------------------------------------------
+template <int K_ = KD, int V_ = VD>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   __shared__ FlushShared sh;
@@ -953,23 +988,29 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   char* base = block_base(st, slot, hv);
   const int8_t* Sq = (const int8_t*)base;
-  const float* Sk = (const float*)(base + VD * KD);
-  const float* Sv = Sk + KD;
-  const f16_t* UQ = (const f16_t*)(Sv + VD);
+  const float* Sk = (const float*)(base + V_ * K_);
+  const float* Sv = Sk + K_;
+  const f16_t* UQ = (const f16_t*)(Sv + V_);
   const int h = min(st.hcnt[sh_], L);
   const float P = st.Pbuf[sh_];
   const int LP = h > 0 ? ((h + 31) & ~31) : 32;
   const int cv = tid & 127;
   const bool colt = tid < KD;
-  const float scv = colt ? Sk[cv] : Sv[cv];
+  const int nc = colt ? K_ : V_;
+  const bool cok = (K_ == KD && V_ == VD) || cv < nc;
+  const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
+  const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
   float uqv[4];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
+  for (int a = 0; a < 4; ++a) {
+    const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
+    uqv[a] = cok ? x : 0.f;
+  }
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window<false>(win, st, slot, hv, h, LP);
+  load_window<false, K_, V_>(win, st, slot, hv, h, LP);
   uint32_t wds[8];
-  load_code_words(wds, Sq);
+  load_code_words<K_, V_>(wds, Sq);
   f32x4 fac;
 #pragma unroll
   for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
@@ -1011,7 +1052,8 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
-    *(float4*)(S + v * KD + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
+    if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_))
+      *(float4*)(S + v * K_ + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {
@@ -1086,9 +1128,14 @@ int num_cus() {
   return cache[dev];
 }
 
-int check_block_state(const lq_state* st, bool need_buf) {
+// head dims (K, V): (128, 128) for GDN and KDA; GDN also (64, 128) and (64, 64) (kernels.py:1089-1092)
+bool head_dims(const lq_state* st, bool kda) {
+  return (st->K == KD && st->V == VD) || (!kda && st->K == 64 && (st->V == 128 || st->V == 64));
+}
+
+int check_block_state(const lq_state* st, bool need_buf, bool kda) {
   if (!st || !st->ssm || !st->hcnt || !st->Wbuf || !st->Pbuf) return LQ_ERR_ARG;
-  if (st->K != KD || st->V != VD || st->L < 1 || st->L > LPMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (!head_dims(st, kda) || st->L < 1 || st->L > LPMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
   if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0) return LQ_ERR_ARG;
   if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3)) return LQ_ERR_ARG;
   if (((uintptr_t)st->ssm & 15) != 0) return LQ_ERR_ARG;
@@ -1099,28 +1146,35 @@ int check_block_state(const lq_state* st, bool need_buf) {
 }  // namespace
 
 extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream) {
-  int rc = check_block_state(st, true);
+  int rc = check_block_state(st, true, kda != 0);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || (kda && !st->Gbuf)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
   const int total = N * st->HV;
-  const int g = total < 2 * num_cus() ? total : 2 * num_cus();   // persistent: two workgroups per CU at most
-  if (kda) flush_kernel<true><<<dim3((unsigned)g), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, N, qmax);
-  else flush_kernel<false><<<dim3((unsigned)g), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, N, qmax);
+  const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
+  hipStream_t s = (hipStream_t)stream;
+  if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
+  else if (st->K == KD) flush_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
+  else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
+  else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
 extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, false);
+  int rc = check_block_state(st, false, false);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  quantize_kernel<false><<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax, 1);
+  const dim3 g((unsigned)(N * st->HV));
+  hipStream_t s = (hipStream_t)stream;
+  if (st->K == KD) quantize_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else if (st->V == VD) quantize_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else quantize_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
 extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, false);
+  int rc = check_block_state(st, false, true);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
@@ -1129,7 +1183,7 @@ extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int*
 }
 
 extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, true);
+  int rc = check_block_state(st, true, true);
   if (rc) return rc;
   if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
@@ -1138,11 +1192,15 @@ extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float q
 }
 
 extern "C" int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, true);
+  int rc = check_block_state(st, true, false);
   if (rc) return rc;
   if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  dequant_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, idx, qmax);
+  const dim3 g((unsigned)(N * st->HV));
+  hipStream_t s = (hipStream_t)stream;
+  if (st->K == KD) dequant_kernel<><<<g, FT, 0, s>>>(*st, idx, qmax);
+  else if (st->V == VD) dequant_kernel<64, 128><<<g, FT, 0, s>>>(*st, idx, qmax);
+  else dequant_kernel<64, 64><<<g, FT, 0, s>>>(*st, idx, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

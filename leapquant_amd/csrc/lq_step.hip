@@ -6,10 +6,10 @@
 // Mapping (MI355X-first, not the reference's persistent TMA/mbarrier pipeline): one workgroup per (row n, key head hk),
 // the G = HV / H value heads sharing the key head's q, k and buffered keys in the same workgroup, so the buffered keys
 // are read once per key head and only the h valid window rows are read.
-//   * GDN: two waves per value head; every dot product on the matrix cores (int8 MFMA for the two GEMVs against the
-//     16 KiB int8 tile, bf16 / fp16 MFMA for the window-key and factor dots), fed by 16-byte loads issued up front.
-//   * KDA: 128 threads per value head on the VALU; each tile row is owned by 8 lanes (16 columns each) whose partial
-//     sums meet in DPP reductions, the per-channel gate folded into the key operand.
+//   * GDN: V / 64 waves per value head; every dot product on the matrix cores (int8 MFMA for the two GEMVs against
+//     the int8 tile, bf16 / fp16 MFMA for the window-key and factor dots), fed by 16-byte loads issued up front.
+//   * KDA (K = V = 128): two waves per value head, the same matrix-core dots, the per-channel gate folded into the
+//     key operands and the window's decayed keys formed by a backward scan split between the two waves.
 #include "lq_common.h"
 
 namespace {
@@ -78,13 +78,13 @@ __device__ __forceinline__ float quad_bcast(float x) {
 }
 constexpr float KSPLIT = 64.0f;   // kn / qn scaled by 2^6 before the fp16 hi / lo split (keeps the lo part normal)
 
-template <int G>
+template <int K_, int V_, int G>
 struct StepShared {
-  bf16_t ub[G][LMAX][VD];  // the window's u_j rows per value head (direct global -> LDS loads)
-  int8_t dig[G][6][KD];    // int8 GEMV B operand: k digits 0-2, q digits 0-2
-  bf16_t bkq[6][KD];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
-  f16_t hkq[4][KD];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
-  float2 mq[G][VD];        // GEMV rows (k, q) in digit units
+  bf16_t ub[G][LMAX][V_];  // the window's u_j rows per value head (direct global -> LDS loads)
+  int8_t dig[G][6][K_];    // int8 GEMV B operand: k digits 0-2, q digits 0-2
+  bf16_t bkq[6][K_];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
+  f16_t hkq[4][K_];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
+  float2 mq[G][V_];        // GEMV rows (k, q) in digit units
   float2 cwq[G][LMAX];     // (w_j dk_j, w_j dq_j) per value head: buffered entry j's coefficients in A4 / A5
   float2 duq[G][4];        // (dU_r, dQ_r) per value head, factor r
   float w[G][LMAX];        // gated entry weights w_j per value head
@@ -94,7 +94,9 @@ struct StepShared {
 // ------------------------------------------------------------------------------------------------------------------
 // GDN step  (kernels.py:129-144 gate / beta, 236-279 norms and weights, 380-585 stream, dots and appends)
 //
-// One workgroup per (row n, key head hk) with 2 waves per value head g; wave (g, wi) owns tile rows 64 wi .. 64 wi + 63.
+// One workgroup per (row n, key head hk) with V / 64 waves per value head g; wave (g, wi) owns tile rows 64 wi ..
+// 64 wi + 63.  Head dims (K, V) = (128, 128), (64, 128), (64, 64) (kernels.py:62): K sets the lanes' channel count in
+// the scalar work and the k-steps of every MFMA, V the waves per value head.
 // Every dot product runs on the matrix cores:
 //   * m = deq(Sq) kn, y = deq(Sq) qn: the int8 tile goes from HBM straight into the A operand of
 //     v_mfma_i32_16x16x64_i8; B holds kf = kn Sk / 127 and qf = qn Sk / 127 as three int8 digits each (24-bit fixed
@@ -105,18 +107,22 @@ struct StepShared {
 // LDS by direct global -> LDS loads.  <= 128 VGPRs and < 40 KiB LDS: four workgroups per CU, the whole B = 64 x H = 16
 // grid resident at once.
 // ------------------------------------------------------------------------------------------------------------------
-template <int G, bool CONV>
-__global__ __launch_bounds__(128 * G) __attribute__((amdgpu_waves_per_eu(4)))
+template <int K_, int V_, int G, bool CONV>
+__global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
 void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
-  __shared__ StepShared<G> sh;
+  constexpr int KD = K_, VD = V_;
+  constexpr int WPH = VD / 64;  // waves per value head
+  constexpr int NE = KD / 64;   // channels per lane in the scalar work
+  constexpr int KS32 = KD / 32, KS64 = KD / 64;   // k-steps of the 16x16x32 (bf16 / fp16) and 16x16x64 (int8) MFMAs
+  __shared__ StepShared<K_, V_, G> sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
   const int hk = blockIdx.x - n * H;
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave in the workgroup
-  const int g = wv >> 1;        // value head of this wave within the key head
-  const int wi = wv & 1;        // its tile half: rows 64 wi ..
-  const int lt = tid & 127;     // thread within the value head (the row it owns in the output phase)
+  const int g = wv / WPH;       // value head of this wave within the key head
+  const int wi = wv % WPH;      // its tile part: rows 64 wi ..
+  const int lt = tid & (VD - 1);   // thread within the value head (the row it owns in the output phase)
   const int lane = tid & 63;
   const int n16 = lane & 15, q4 = lane >> 4;                 // MFMA lane coordinates
   const int hv = hk * G + g;
@@ -139,12 +145,12 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   const long long sh_ = (long long)slot * HV + hv;
   float* Wp = st.Wbuf + sh_ * L;
-  bf16_t kxr[2], qxr[2];
-  float skx[2], wx[2];
-  ConvTaps ktap[2], qtap[2], vtap;    // CONV: taps of the key / query channels c and of the value channel lt
+  bf16_t kxr[NE], qxr[NE];
+  float skx[NE], wx[NE];
+  ConvTaps ktap[NE], qtap[NE], vtap;  // CONV: taps of the key / query channels c and of the value channel lt
   const long long cvb = CONV ? (long long)slot * cv.slot_stride : 0;
 #pragma unroll
-  for (int e = 0; e < 2; ++e) {
+  for (int e = 0; e < NE; ++e) {
     const int c = lane + 64 * e;
     if (CONV) {
       ktap[e] = conv_taps(cv, mrow, cvb, H * KD + hk * KD + c);
@@ -160,13 +166,13 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
   const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
   // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA (last wave)
-  f16x8 ufr[4];
-  const bool fwave = wv == 2 * G - 1;
+  f16x8 ufr[KS32];
+  const bool fwave = wv == WPH * G - 1;
   {
     const int m = n16 < G * R ? n16 : 0, g2 = m / R, r = m - g2 * R;
     const f16_t* U = (const f16_t*)(block_base(st, slot, hk * G + g2) + VD * KD + 4 * (KD + VD)) + r * (KD + VD);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
+    for (int ks = 0; ks < KS32; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
   }
   float vin = 0.f;
   if (CONV) vtap = conv_taps(cv, mrow, cvb, 2 * H * KD + hv * VD + lt);
@@ -185,35 +191,38 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   // ---- per value head scalar work, one wave (wi = 0), before the window fills arrive: gate, beta, norms, digits,
   //      key-dot operands.  Its global writes (key append, gated weights) wait until the end, so that nothing joins
   //      the window / tile loads in the vector memory counter before the window's wait ----
-  bf16_t kapp[2] = {0, 0};
-  float wjv[2] = {0.f, 0.f};
-  uint32_t kpk[4] = {0u, 0u, 0u, 0u}, qpk[4] = {0u, 0u, 0u, 0u};   // CONV: key / query state after the shift
+  bf16_t kapp[NE] = {};
+  float wjv[NE] = {};
+  uint32_t kpk[2 * NE] = {}, qpk[2 * NE] = {};   // CONV: key / query state after the shift
   if (wi == 0) {
     const float alpha = gdn_alpha_f(bf2f(araw), dtb, alog);
     const float beta = beta_f(bf2f(braw));
     if (CONV) {
 #pragma unroll
-      for (int e = 0; e < 2; ++e) {
+      for (int e = 0; e < NE; ++e) {
         kxr[e] = f2bf(conv_out(ktap[e], cv.silu));
         qxr[e] = f2bf(conv_out(qtap[e], cv.silu));
         kpk[e] = ktap[e].s[1] | ((uint32_t)ktap[e].s[2] << 16);   // the shifted taps (s1, s2 | x)
-        kpk[2 + e] = ktap[e].x;
+        kpk[NE + e] = ktap[e].x;
         qpk[e] = qtap[e].s[1] | ((uint32_t)qtap[e].s[2] << 16);
-        qpk[2 + e] = qtap[e].x;
+        qpk[NE + e] = qtap[e].x;
       }
     }
-    const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
+    float kx[NE], qx[NE];
+#pragma unroll
+    for (int e = 0; e < NE; ++e) { kx[e] = bf2f(kxr[e]); qx[e] = bf2f(qxr[e]); }
     float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
-    nq = fmaf(qx[1], qx[1], nq); nk = fmaf(kx[1], kx[1], nk); nkq = fmaf(kx[1], qx[1], nkq);
+#pragma unroll
+    for (int e = 1; e < NE; ++e) { nq = fmaf(qx[e], qx[e], nq); nk = fmaf(kx[e], kx[e], nk); nkq = fmaf(kx[e], qx[e], nkq); }
     nq = sum64(nq); nk = sum64(nk); nkq = sum64(nkq);
     const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
     const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
     const float kappa = nkq * inq * ink;
     const float inv = 1.0f / LQ_QMAX;
-    float kn[2], qn[2], kf[2], qf[2];
+    float kn[NE], qn[NE], kf[NE], qf[NE];
     float kmax = 0.f, qmax = 0.f;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NE; ++e) {
       kn[e] = kx[e] * ink;
       qn[e] = qx[e] * inq;
       kf[e] = (kn[e] * skx[e]) * inv;          // kernels.py:255-256
@@ -225,7 +234,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
     qmax = fmaxf(max64(qmax), 1e-30f);
     const float rk = 1.0f / kmax, rq = 1.0f / qmax;
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NE; ++e) {
       const int c = lane + 64 * e;
       int8_t d0, d1, d2;
       digits3(kf[e], rk, d0, d1, d2);
@@ -272,7 +281,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   hmax = min(hmax, L);
   if (wi == 0 && live) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NE; ++e) {
       const int c = lane + 64 * e;
       if (c < h) sh.w[g][c] = wjv[e];
     }
@@ -280,75 +289,78 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   // The big loads, in the order the work after them needs them: the window (values u_j into LDS, then the buffered
   // keys), and the int8 tile last.  Everything built on the window -- key dots, A4 / A5 -- runs while the tile still
   // streams; after the tile's last bytes only the GEMV, the delta rule and the stores remain.
-  // window values u_j (j < h) straight to LDS, 1 KiB (4 rows) per wave instruction (the loop holds no compiler-visible
-  // load, so it adds no wait); rows past the buffer's last (L not a multiple of 4) re-read it
+  // window values u_j (j < h) straight to LDS, 1 KiB (RPK = 4 rows at V = 128, 8 at V = 64) per wave instruction (the
+  // loop holds no compiler-visible load, so it adds no wait); rows past the buffer's last (L not a multiple of RPK)
+  // re-read it
   {
+    constexpr int RPK = 512 / VD, LPR = VD / 8;             // rows per KiB, lanes per row
     const char* ubg = (const char*)((const bf16_t*)st.Ubuf + sh_ * L * VD);
-    const int nch = live ? (h + 3) >> 2 : 0;
-    for (int c = wi; c < nch; c += 2) {
-      const int row = min(4 * c + (lane >> 4), L - 1);
-      lds_load16(ubg + row * (VD * 2) + 16 * (lane & 15), (char*)&sh.ub[g][0][0] + c * 1024);
+    const int nch = live ? (h + RPK - 1) / RPK : 0;
+    for (int c = wi; c < nch; c += WPH) {
+      const int row = min(RPK * c + lane / LPR, L - 1);
+      lds_load16(ubg + row * (VD * 2) + 16 * (lane % LPR), (char*)&sh.ub[g][0][0] + c * 1024);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
   // buffered keys: this wave's 16-row tiles of K, A fragments of the key-dot MFMA (rows >= hmax read row 0, unused)
-  constexpr int KT = (4 + 2 * G - 1) / (2 * G);             // 16-row key tiles per wave (64 rows over 2G waves)
-  bf16x8 kfr[KT][4];
+  constexpr int NWV = WPH * G;                              // waves in the workgroup
+  constexpr int KT = (4 + NWV - 1) / NWV;                   // 16-row key tiles per wave (64 rows over the waves)
+  bf16x8 kfr[KT][KS32];
   {
     const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD;
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const int j = 16 * (wv + 2 * G * t) + n16;
+      const int j = 16 * (wv + NWV * t) + n16;
       const int jr = j < hmax ? j : 0;
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
+      for (int ks = 0; ks < KS32; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
     }
   }
-  i32x4 afr[4][2];              // the int8 tile: A fragments, row 64 wi + 16 rt + n16
+  i32x4 afr[4][KS64];           // the int8 tile: A fragments, row 64 wi + 16 rt + n16
   {
     const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+      for (int ks = 0; ks < KS64; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
   }
   // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
   // stores at the end, so this count is exact)
-  constexpr int AFTER_WINDOW = 4 * KT + 8;
+  constexpr int AFTER_WINDOW = KS32 * KT + 4 * KS64;
   __builtin_amdgcn_sched_barrier(0);
 
   __syncthreads();              // digits, dot operands, scalars and w_j are in LDS (the barrier waits for no global load)
   if (CONV && wv == 0) {        // the key head's conv state shift, once per workgroup, after every wave read its taps
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NE; ++e) {
       bf16_t* Sk_ = (bf16_t*)cv.state + cvb + (long long)(H * KD + hk * KD + lane + 64 * e) * cv.ch_stride;
       bf16_t* Sq_ = (bf16_t*)cv.state + cvb + (long long)(hk * KD + lane + 64 * e) * cv.ch_stride;
       Sk_[0] = (bf16_t)kpk[e];
       Sk_[cv.tap_stride] = (bf16_t)(kpk[e] >> 16);
-      Sk_[2 * cv.tap_stride] = (bf16_t)kpk[2 + e];
+      Sk_[2 * cv.tap_stride] = (bf16_t)kpk[NE + e];
       Sq_[0] = (bf16_t)qpk[e];
       Sq_[cv.tap_stride] = (bf16_t)(qpk[e] >> 16);
-      Sq_[2 * cv.tap_stride] = (bf16_t)qpk[2 + e];
+      Sq_[2 * cv.tap_stride] = (bf16_t)qpk[NE + e];
     }
   }
 
   // ---- buffered-key dots: this wave's K tiles against bf16 (hi, mid, lo) of kn (columns 0-2) and qn (4-6) ----
   {
-    bf16x8 bk[4];
+    bf16x8 bk[KS32];
     const bool bcol = (n16 & 3) < 3 && n16 < 8;
     const int brow = bcol ? (n16 >> 2) * 3 + (n16 & 3) : 0;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < KS32; ++ks) {
       const bf16x8 b = *(const bf16x8*)&sh.bkq[brow][32 * ks + 8 * q4];
       bk[ks] = bcol ? b : bf16x8{};
     }
 #pragma unroll
     for (int t = 0; t < KT; ++t) {
-      const int j0 = 16 * (wv + 2 * G * t);
+      const int j0 = 16 * (wv + NWV * t);
       if (j0 < hmax) {
         f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[t][ks], bk[ks], acc, 0, 0, 0);
+        for (int ks = 0; ks < KS32; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kfr[t][ks], bk[ks], acc, 0, 0, 0);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
@@ -363,16 +375,16 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   }
   // ---- factor dots (last wave): U^T rows of the G heads against fp16 (hi, lo) of 64 kn (columns 0, 1), 64 qn (2, 3) ----
   if (fwave) {
-    f16x8 bh[4];
+    f16x8 bh[KS32];
     const bool bcol = n16 < 4;
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ks = 0; ks < KS32; ++ks) {
       const f16x8 b = *(const f16x8*)&sh.hkq[bcol ? n16 : 0][32 * ks + 8 * q4];
       bh[ks] = bcol ? b : f16x8{};
     }
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ufr[ks], bh[ks], acc, 0, 0, 0);
+    for (int ks = 0; ks < KS32; ++ks) acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(ufr[ks], bh[ks], acc, 0, 0, 0);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float s = (acc[i] + dpp<DPP_XOR1>(acc[i])) * (1.0f / KSPLIT);               // hi + lo (lanes 0 / 2)
@@ -417,19 +429,19 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   }
   // ---- int8 GEMV on the matrix cores (the tile is the last data to arrive).  B columns: 0 / 4 / 8 = k digits 0 / 1 / 2, 1 / 5 / 9 = q digits, others 0 ----
   {
-    i32x4 bfr[2];
+    i32x4 bfr[KS64];
     const int drow = (n16 & 3) * 3 + (n16 >> 2);              // table row of column n16 (valid for n16 < 10, n16 & 3 < 2)
     const bool bcol = (n16 & 3) < 2 && n16 < 10;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int ks = 0; ks < KS64; ++ks) {
       const i32x4 b = *(const i32x4*)&sh.dig[g][bcol ? drow : 0][64 * ks + 16 * q4];
       bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
     }
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt) {
       i32x4 acc = {0, 0, 0, 0};
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][0], bfr[0], acc, 0, 0, 0);
-      acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][1], bfr[1], acc, 0, 0, 0);
+#pragma unroll
+      for (int ks = 0; ks < KS64; ++ks) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][ks], bfr[ks], acc, 0, 0, 0);
       // lane (n16, q4) holds rows 64 wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -456,7 +468,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   }
   if (wi == 0) {
 #pragma unroll
-    for (int e = 0; e < 2; ++e) {
+    for (int e = 0; e < NE; ++e) {
       const int c = lane + 64 * e;
       if (g == 0) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + c] = kapp[e];   // key append
       if (c < h) Wp[c] = wjv[e];
@@ -817,9 +829,12 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 
 }  // namespace
 
+// head dims of the GDN step (kernels.py:62); the KDA step is K = V = 128 only (kernels.py:727)
+static bool gdn_dims(int K, int V) { return (K == 128 && V == 128) || (K == 64 && (V == 128 || V == 64)); }
+
 static int check_step(const lq_state* st, const lq_step_io* io) {
   if (!st || !io) return LQ_ERR_ARG;
-  if (st->K != KD || st->V != VD || st->L < 1 || st->L > LMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (!gdn_dims(st->K, st->V) || st->L < 1 || st->L > LMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
   if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0 || io->N < 0) return LQ_ERR_ARG;
   if (!st->ssm || !st->Kbuf || !st->Ubuf || !st->Wbuf || !st->Pbuf || !st->hcnt) return LQ_ERR_ARG;
   // 16-byte loads of the int8 rows and of the scale / factor block need a 16-byte aligned block start
@@ -830,21 +845,31 @@ static int check_step(const lq_state* st, const lq_step_io* io) {
   return LQ_OK;
 }
 
-extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream) {
-  int rc = check_step(st, io);
-  if (rc) return rc;
-  const int G = st->HV / st->H;
-  if (io->N == 0) return LQ_OK;
+template <int K_, int V_, bool CONV>
+static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, hipStream_t s) {
   dim3 grid((unsigned)(io->N * st->H));
-  hipStream_t s = (hipStream_t)stream;
-  const lq_conv none = {};
-  switch (G) {
-    case 1: gdn_step_kernel<1, false><<<grid, 128, 0, s>>>(*st, *io, none); break;
-    case 2: gdn_step_kernel<2, false><<<grid, 256, 0, s>>>(*st, *io, none); break;
-    case 4: gdn_step_kernel<4, false><<<grid, 512, 0, s>>>(*st, *io, none); break;
+  switch (st->HV / st->H) {
+    case 1: gdn_step_kernel<K_, V_, 1, CONV><<<grid, V_, 0, s>>>(*st, *io, cv); break;
+    case 2: gdn_step_kernel<K_, V_, 2, CONV><<<grid, 2 * V_, 0, s>>>(*st, *io, cv); break;
+    case 4: gdn_step_kernel<K_, V_, 4, CONV><<<grid, 4 * V_, 0, s>>>(*st, *io, cv); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+template <bool CONV>
+static int launch_gdn_dims(const lq_state* st, const lq_step_io* io, const lq_conv& cv, void* stream) {
+  hipStream_t s = (hipStream_t)stream;
+  if (st->K == 128) return launch_gdn<128, 128, CONV>(st, io, cv, s);
+  return st->V == 128 ? launch_gdn<64, 128, CONV>(st, io, cv, s) : launch_gdn<64, 64, CONV>(st, io, cv, s);
+}
+
+extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream) {
+  int rc = check_step(st, io);
+  if (rc) return rc;
+  if (io->N == 0) return LQ_OK;
+  const lq_conv none = {};
+  return launch_gdn_dims<false>(st, io, none, stream);
 }
 
 extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
@@ -856,23 +881,14 @@ extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const 
   // the state taps of a slot must stay inside its slot_stride elements
   if ((C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride) return LQ_ERR_ARG;
   if (((uintptr_t)cv->weight & 7) != 0) return LQ_ERR_ARG;
-  const int G = st->HV / st->H;
   if (io->N == 0) return LQ_OK;
-  dim3 grid((unsigned)(io->N * st->H));
-  hipStream_t s = (hipStream_t)stream;
-  switch (G) {
-    case 1: gdn_step_kernel<1, true><<<grid, 128, 0, s>>>(*st, *io, *cv); break;
-    case 2: gdn_step_kernel<2, true><<<grid, 256, 0, s>>>(*st, *io, *cv); break;
-    case 4: gdn_step_kernel<4, true><<<grid, 512, 0, s>>>(*st, *io, *cv); break;
-    default: return LQ_ERR_ARG;
-  }
-  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+  return launch_gdn_dims<true>(st, io, *cv, stream);
 }
 
 extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream) {
   int rc = check_step(st, io);
   if (rc) return rc;
-  if (!st->Gbuf) return LQ_ERR_ARG;
+  if (!st->Gbuf || st->K != KD || st->V != VD) return LQ_ERR_ARG;
   if (io->N == 0) return LQ_OK;
   dim3 grid((unsigned)(io->N * st->HV));
   kda_step_kernel<<<grid, 128, 0, (hipStream_t)stream>>>(*st, *io, glb);

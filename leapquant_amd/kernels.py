@@ -53,8 +53,12 @@ def _need(t, dtype, shape, name):
         raise ValueError("%s must be contiguous" % name)
 
 
-def _check_dims(K, V, L, R):
-    assert (K, V) == (128, 128), "liblq: head dims (K, V) = (128, 128) only, got (%d, %d)" % (K, V)
+GDN_DIMS = ((128, 128), (64, 128), (64, 64))        # kernels.py:62, 1089 (KDA: 128 x 128 only, 727)
+
+
+def _check_dims(K, V, L, R, kda=False):
+    dims = ((128, 128),) if kda else GDN_DIMS
+    assert (K, V) in dims, "liblq: head dims (K, V) in %s, got (%d, %d)" % (dims, K, V)
     assert 1 <= L <= LMAX, "liblq: window 1 <= L <= %d, got %d" % (LMAX, L)
     assert 1 <= R <= 4, "liblq: rank 1 <= R <= 4, got %d" % R
     assert V * K // 4 + K + V + R * (K + V) // 2 <= V * K, "checkpoint must fit inside the fp32 slot"
@@ -125,7 +129,7 @@ def make_kda_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=6, NSTAGEQ=4, NC
                   MAXIT=256, GLB=0.0):
     """Kimi Delta Attention decode step (kernels.py:694-1075), per-key-channel gate; GLB != 0 selects GLM's bounded
     gate.  Returns step(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o)."""
-    _check_dims(K, V, L, R)
+    _check_dims(K, V, L, R, kda=True)
     assert HV % H == 0, "liblq: HV % H == 0"
     L_ = _lib.lib()
     glb = float(GLB)
@@ -154,7 +158,7 @@ def make_flush(NS, HV, K, V, L, SS, R=4, ITERS=1, SMS=None, NCG=3, MAXIT=128, PA
     """End-of-window flush (kernels.py:1077-2033).  Returns
     flush(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx).  Due heads (hcnt == L) are found on
     the device; ITERS = 1 and PNMIN = 1e-20 as in the reference's use (state.py:79)."""
-    _check_dims(K, V, L, R)
+    _check_dims(K, V, L, R, kda=KDA)
     assert ITERS == 1, "liblq: one subspace iteration per flush (ITERS = 1)"
     assert PNMIN == 1e-20
     L_ = _lib.lib()

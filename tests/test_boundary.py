@@ -60,7 +60,7 @@ def _io(**kw):
     return _lib.LqStepIO(**d)
 
 
-BAD_STATES = [dict(K=64), dict(V=64), dict(L=0), dict(L=65), dict(R=0), dict(R=5), dict(H=0), dict(HV=3),
+BAD_STATES = [dict(K=96), dict(V=64), dict(K=32, V=32), dict(L=0), dict(L=65), dict(R=0), dict(R=5), dict(H=0), dict(HV=3),
               dict(NS=0), dict(slot_stride=100), dict(slot_stride=4 * 128 * 128 + 1), dict(ssm=8), dict(ssm=None),
               dict(hcnt=None), dict(Wbuf=None)]
 
@@ -81,6 +81,23 @@ def test_entry_points_reject_bad_state(lib, bad):
                                z) == -1
         assert lib.lq_kda_checkpoint(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
                                      ctypes.c_float(127.0), z) == -1
+
+
+@pytest.mark.parametrize("K,V", [(64, 128), (64, 64)])
+def test_head_dims_gdn_only(lib, K, V):
+    """(K, V) = (64, 128), (64, 64) (kernels.py:62, 1089): accepted by the GDN step, flush, quantize and dequant,
+    rejected by every KDA entry point (kernels.py:727)."""
+    st, io = _state(K=K, V=V), _io()
+    z, p = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == 0
+    assert lib.lq_flush(ctypes.byref(st), p, p, 0, 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_quantize(ctypes.byref(st), p, p, 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_dequant(ctypes.byref(st), p, 0, ctypes.c_float(127.0), z) == 0
+    assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == -1
+    assert lib.lq_flush(ctypes.byref(st), p, p, 0, 1, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_kda_dequant(ctypes.byref(st), p, 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_kda_checkpoint(ctypes.byref(st), p, p, 0, ctypes.c_float(127.0), z) == -1
+    assert lib.lq_lowrank(p, p, p, p, 0, K, V, 4, 3, z) == -1
 
 
 def test_entry_points_accept_empty_calls(lib):
@@ -156,7 +173,7 @@ def test_fused_conv_entry_points_check_their_arguments(lib):
         assert lib.lq_conv_update(ctypes.byref(_conv(**bad)), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                   ctypes.c_void_p(16), 1, 1024, 8, z) == -1, bad
     assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), None, z) == -1
-    assert lib.lq_gdn_step_conv(ctypes.byref(_state(K=64)), ctypes.byref(io), ctypes.byref(_conv()), z) == -1
+    assert lib.lq_gdn_step_conv(ctypes.byref(_state(K=96)), ctypes.byref(io), ctypes.byref(_conv()), z) == -1
     assert lib.lq_conv_update(ctypes.byref(_conv()), ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               0, 1024, 8, z) == 0
     assert lib.lq_conv_update(ctypes.byref(_conv()), None, ctypes.c_void_p(16), ctypes.c_void_p(16), 1, 1024, 8,
@@ -234,7 +251,13 @@ def test_host_tensors_never_reach_the_kernels(lib):
 def test_factories_check_static_shapes(lib):
     from leapquant_amd import kernels as KN
     with pytest.raises(AssertionError):
-        KN.make_gdn_step(4, 32, 16, 64, 128, 16, 32 * 128 * 128)
+        KN.make_gdn_step(4, 32, 16, 128, 64, 16, 32 * 128 * 128)     # (K, V) = (128, 64): no such variant
+    with pytest.raises(AssertionError):
+        KN.make_kda_step(4, 32, 32, 64, 128, 16, 32 * 128 * 128)     # KDA: 128 x 128 only
+    with pytest.raises(AssertionError):
+        KN.make_flush(4, 32, 64, 64, 16, 32 * 128 * 128, KDA=True)
+    KN.make_gdn_step(4, 32, 16, 64, 128, 16, 32 * 64 * 128)          # the GDN head-dim variants (kernels.py:62)
+    KN.make_flush(4, 32, 64, 64, 16, 32 * 64 * 64)
     with pytest.raises(AssertionError):
         KN.make_gdn_step(4, 32, 16, 128, 128, 65, 32 * 128 * 128)
     with pytest.raises(AssertionError):

@@ -19,9 +19,12 @@ from tests.fixtures import from_bits, gate_params, make_inputs, make_state, stat
 
 K = V = 128
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
+# head dims (K, V): GDN (128, 128), (64, 128), (64, 64) (kernels.py:62, 1089); KDA 128 x 128 (kernels.py:727)
+GDN_DIMS = [(128, 128), (64, 128), (64, 64)]
+STEP_CASES = [(False, d) for d in GDN_DIMS] + [(True, (128, 128))]
 
 
-def _qk_from_mixed(mixed, H, HV):
+def _qk_from_mixed(mixed, H, HV, K=K, V=V):
     q = mixed[:, :H * K].reshape(-1, H, K).astype(np.float64)
     k = mixed[:, H * K:2 * H * K].reshape(-1, H, K).astype(np.float64)
     v = mixed[:, 2 * H * K:].reshape(-1, HV, V).astype(np.float64)
@@ -36,14 +39,15 @@ def _sign_fixed_qr(X):
 
 
 # ------------------------------------------------------------------------------------------------ steps vs dense rule
-@pytest.mark.parametrize("kda", [False, True])
+@pytest.mark.parametrize("kda,dims", STEP_CASES)
 @pytest.mark.parametrize("HV,H", [(2, 1), (2, 2), (4, 2)])
-def test_step_trajectory_matches_dense_rule(kda, HV, H):
+def test_step_trajectory_matches_dense_rule(kda, dims, HV, H):
     """Evolve a dense float64 state with the textbook rule beside the oracle's checkpoint + window representation
     (no flush: L = 64 > steps); the materialised oracle state and the outputs must track it."""
-    rng = np.random.default_rng(11 + HV + 10 * H + 100 * kda)
+    K, V = dims
+    rng = np.random.default_rng(11 + HV + 10 * H + 100 * kda + K + V)
     NS, L = 3, 64
-    st, _, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda)
+    st, _, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=L, kda=kda)
     idx = np.array([2, 1, 0])
     A_log, dt_bias = gate_params(HV, K, kda)
     A_log[:] = rng.uniform(-1.0, 0.5, HV)               # exercise A_log / dt_bias too
@@ -51,10 +55,10 @@ def test_step_trajectory_matches_dense_rule(kda, HV, H):
     scale = K ** -0.5
     Sdrift = O.materialize(st)                          # evolved densely from the checkpoint, never re-synced
     for t in range(20):
-        mixed, a, b = make_inputs(rng, 3, HV, H, kda=kda)
+        mixed, a, b = make_inputs(rng, 3, HV, H, K, V, kda=kda)
         rows = idx > 0
         s = idx[rows]
-        q, k, v = _qk_from_mixed(mixed[rows], H, HV)
+        q, k, v = _qk_from_mixed(mixed[rows], H, HV, K, V)
         hk = np.arange(HV) // (HV // H)
         beta = O.beta_of(b[rows]).astype(np.float64)
         S = O.materialize(st)                           # the oracle's logical state before this step
@@ -128,16 +132,17 @@ def test_step_special_cases_gdn():
 
 
 # ------------------------------------------------------------------------------------------------ flush
-@pytest.mark.parametrize("kda", [False, True])
+@pytest.mark.parametrize("kda,dims", STEP_CASES)
 @pytest.mark.parametrize("L", [16, 64])
-def test_flush_against_qr_and_bounds(kda, L):
-    rng = np.random.default_rng(5 + L + 7 * kda)
+def test_flush_against_qr_and_bounds(kda, dims, L):
+    K, V = dims
+    rng = np.random.default_rng(5 + L + 7 * kda + K + V)
     HV, H = 2, (2 if kda else 1)
-    st, _, Q0 = make_state(rng, 3, HV, H, L=L, kda=kda)
+    st, _, Q0 = make_state(rng, 3, HV, H, K=K, V=V, L=L, kda=kda)
     A_log, dt_bias = gate_params(HV, K, kda)
     idx = np.array([1, 2])
     for t in range(L):
-        mixed, a, b = make_inputs(rng, 2, HV, H, kda=kda)
+        mixed, a, b = make_inputs(rng, 2, HV, H, K, V, kda=kda)
         (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, idx)
     assert np.all(st["hcnt"][1:] == L)
     S_before = O.materialize(st)
@@ -202,8 +207,10 @@ def test_flush_fully_decayed_and_idle_heads():
 # ------------------------------------------------------------------------------------------------ quantize / lowrank
 @pytest.mark.parametrize("qmax", [127.0, 31.0])
 @pytest.mark.parametrize("heavy", [False, True])
-def test_quantize_against_qr_and_bounds(qmax, heavy):
-    rng = np.random.default_rng(21 + int(qmax) + heavy)
+@pytest.mark.parametrize("dims", GDN_DIMS)
+def test_quantize_against_qr_and_bounds(qmax, heavy, dims):
+    K, V = dims
+    rng = np.random.default_rng(21 + int(qmax) + heavy + K + V)
     D = 3
     S = (0.02 * (rng.standard_t(3, (D, V, K)) if heavy else rng.standard_normal((D, V, K)))).astype(np.float32)
     S[1] += np.outer(rng.standard_normal(V), rng.standard_normal(K)).astype(np.float32) * 0.05   # a dominant direction
@@ -244,9 +251,11 @@ def test_lowrank_against_qr_iteration():
         np.testing.assert_allclose(U[d], xx @ Qr, rtol=1e-4, atol=1e-4)
 
 
-def test_dequant_reproduces_logical_state_and_resets():
-    rng = np.random.default_rng(8)
-    st, S0, Q0 = make_state(rng, 3, 2, 1, L=16)
+@pytest.mark.parametrize("dims", GDN_DIMS)
+def test_dequant_reproduces_logical_state_and_resets(dims):
+    K, V = dims
+    rng = np.random.default_rng(8 + K + V)
+    st, S0, Q0 = make_state(rng, 3, 2, 1, K=K, V=V, L=16)
     # quantize -> dequant round trip of a fresh checkpoint stays within the quantisation bound of the fp32 source
     out = O.dequant(O.copy_state(st), [1, 2])
     for sl in (1, 2):
@@ -258,7 +267,7 @@ def test_dequant_reproduces_logical_state_and_resets():
     # with a partial window: dequant == dense evolution (checked through the pinned materialisation)
     A_log, dt_bias = gate_params(2)
     for t in range(5):
-        mixed, a, b = make_inputs(rng, 1, 2, 1)
+        mixed, a, b = make_inputs(rng, 1, 2, 1, K, V)
         O.gdn_step(st, mixed, a, b, A_log, dt_bias, np.array([2]))
     Sm = O.materialize(st)
     out = O.dequant(st, [2])
