@@ -147,6 +147,80 @@ def kda_bench(torch, dev, stream, capture):
     return res
 
 
+def head_dims_bench(torch, dev, stream, capture):
+    """GDN head-dim variants (K, V) = (64, 128), (64, 64) (reference kernels.py:62-65) at config 1's batch and heads
+    (B = 64, HV = 32, H = 16) and the reference's window for these shapes, W = 16 (R = 4), int8 state, 4 rotated slot
+    sets.  Per shape: the amortised decode call (step + flush), the step alone (mean over h = 0..15) with its
+    algorithmic GB/s, and the flush with every head of a set due."""
+    from leapquant_amd.state import LeapQuantState
+    B, HV, H, L, R, NSET = 64, 32, 16, 16, 4, 4
+    NS = B * NSET + 1
+    res = {"workload": "GDN decode, B=64, HV=32 value / H=16 key heads, W=16, R=4, int8 state, %d rotated slot sets"
+                       % NSET}
+    for K, V in ((64, 128), (64, 64)):
+        g = torch.Generator(device=dev)
+        g.manual_seed(1005 + K + V)
+        ssm = torch.empty(NS, HV, V, K, device=dev)
+        ssm.normal_(0.0, 0.02, generator=g)
+        lq = LeapQuantState(ssm, H, L=L, R=R)
+        lq.quantize(ssm, torch.arange(1, NS, device=dev, dtype=torch.int32))
+        sets = [torch.arange(1 + B * k, 1 + B * (k + 1), device=dev, dtype=torch.int32) for k in range(NSET)]
+        pool = []
+        for _ in range(8):
+            q = torch.randn(B, H, K, device=dev, generator=g)
+            k = torch.randn(B, H, K, device=dev, generator=g)
+            q = q / q.norm(dim=-1, keepdim=True)
+            k = k / k.norm(dim=-1, keepdim=True)
+            v = torch.randn(B, HV, V, device=dev, generator=g)
+            mixed = torch.cat([q.reshape(B, -1), k.reshape(B, -1), v.reshape(B, -1)], 1).to(torch.bfloat16).contiguous()
+            gl = (-0.1 * torch.rand(B, HV, device=dev, generator=g)).clamp(max=-1e-4)
+            a = torch.log(torch.expm1(-gl)).to(torch.bfloat16)
+            b = torch.randn(B, HV, device=dev, generator=g).to(torch.bfloat16)
+            pool.append((mixed, a, b))
+        A_log = torch.zeros(HV, device=dev)
+        dt_bias = torch.zeros(HV, device=dev)
+        out = torch.empty(B, HV, V, device=dev, dtype=torch.bfloat16)
+        vw = lq.views(ssm)
+
+        def decode(i):
+            mixed, a, b = pool[i % 8]
+            lq.decode(ssm, mixed, a, b, A_log, dt_bias, sets[i % NSET], out)
+
+        def step_only(i):
+            mixed, a, b = pool[i % 8]
+            lq.kstep(vw["q32"], vw["Sk"], vw["Sv"], vw["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.hcnt, mixed, a,
+                     b, A_log, dt_bias, vw["uq"], sets[i % NSET], out)
+
+        def flush_only(kk):
+            lq.kflush(vw["q32"], vw["Sk"], vw["Sv"], vw["skv"], lq.Kbuf, lq.Ubuf, lq.Wbuf, lq.Pbuf, lq.Gd, lq.hcnt,
+                      vw["sq16"], vw["uq"], lq.Q0, sets[kk])
+
+        CH = NSET * L                                   # one graph: every set's window from h = 0 to full
+        gdec = capture(decode, CH)
+        for _ in range(2):
+            gdec.replay()
+        torch.cuda.synchronize()
+        decode_us = event_ms(torch, stream, gdec.replay, 8) * 1e3 / CH
+        lq.quantize(ssm, torch.arange(1, NS, device=dev, dtype=torch.int32))
+        gst = capture(step_only, CH)
+        gfl = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
+        torch.cuda.synchronize()
+        st_ms, fl_ms = [], []
+        for r in range(4):                              # step graph (every window to full), then every set's flush
+            st_ms.append(event_ms(torch, stream, gst.replay, 1))
+            for kk in range(NSET):
+                fl_ms.append(event_ms(torch, stream, gfl[kk].replay, 1))
+        step_us = sum(st_ms[1:]) / len(st_ms[1:]) * 1e3 / CH
+        flush_us = sum(fl_ms[NSET:]) / len(fl_ms[NSET:]) * 1e3
+        bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L)) / L
+        res["K%d_V%d" % (K, V)] = {"decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
+                                   "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
+                                   "step_bytes_per_launch": int(bytes_step), "flush_due_us": round(flush_us, 2)}
+        del gdec, gst, gfl, lq, ssm
+        torch.cuda.empty_cache()
+    return res
+
+
 def flush_quantize_bench(torch, dev, stream):
     """standalone flush and quantize of 256 x 32 heads of 128 x 128 fp32 states with Student-t
     (nu = 3, scale 0.02) entries; the flush with a full window (64 buffered entries) on every head; INT8 and 6-bit."""
@@ -519,6 +593,7 @@ def main():
 
     kda = kda_bench(torch, dev, stream, capture)
     fq = flush_quantize_bench(torch, dev, stream)
+    hd = head_dims_bench(torch, dev, stream, capture)
 
     res = {
         "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
@@ -542,6 +617,7 @@ def main():
         "plain_step_us": round(step_us, 3)}
     res["kda_config2"] = kda
     res["flush_quantize_config3"] = fq
+    res["head_dims_W16"] = hd
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline()
     print(json.dumps(res))
