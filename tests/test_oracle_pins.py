@@ -22,6 +22,8 @@ GOLD = os.path.join(os.path.dirname(__file__), "golden")
 # head dims (K, V): GDN (128, 128), (64, 128), (64, 64) (kernels.py:62, 1089); KDA 128 x 128 (kernels.py:727)
 GDN_DIMS = [(128, 128), (64, 128), (64, 64)]
 STEP_CASES = [(False, d) for d in GDN_DIMS] + [(True, (128, 128))]
+# (kda, dims, glb): KDA also with GLM's bounded gate (kernels.py:702-712)
+TRAJ_CASES = [(False, d, 0.0) for d in GDN_DIMS] + [(True, (128, 128), 0.0), (True, (128, 128), -5.0)]
 
 
 def _qk_from_mixed(mixed, H, HV, K=K, V=V):
@@ -39,9 +41,9 @@ def _sign_fixed_qr(X):
 
 
 # ------------------------------------------------------------------------------------------------ steps vs dense rule
-@pytest.mark.parametrize("kda,dims", STEP_CASES)
+@pytest.mark.parametrize("kda,dims,glb", TRAJ_CASES)
 @pytest.mark.parametrize("HV,H", [(2, 1), (2, 2), (4, 2)])
-def test_step_trajectory_matches_dense_rule(kda, dims, HV, H):
+def test_step_trajectory_matches_dense_rule(kda, dims, glb, HV, H):
     """Evolve a dense float64 state with the textbook rule beside the oracle's checkpoint + window representation
     (no flush: L = 64 > steps); the materialised oracle state and the outputs must track it."""
     K, V = dims
@@ -64,10 +66,10 @@ def test_step_trajectory_matches_dense_rule(kda, dims, HV, H):
         S = O.materialize(st)                           # the oracle's logical state before this step
         st_prev = O.copy_state(st)
         if kda:
-            g, _ = O.kda_gate(a.reshape(3, HV, K)[rows], dt_bias, A_log, 0.0)
+            g, _ = O.kda_gate(a.reshape(3, HV, K)[rows], dt_bias, A_log, glb)
             S1, od, u, kh = O.dense_kda_step(S[s], q[:, hk], k[:, hk], v, g, beta, scale)
             Sdrift[s] = O.dense_kda_step(Sdrift[s], q[:, hk], k[:, hk], v, g, beta, scale)[0]
-            o = O.kda_step(st, mixed, a, b, A_log, dt_bias, idx)
+            o = O.kda_step(st, mixed, a, b, A_log, dt_bias, idx, glb=glb)
         else:
             alpha = O.gdn_alpha(a[rows], dt_bias, A_log).astype(np.float64)
             S1, od, u, kh = O.dense_gdn_step(S[s], q[:, hk], k[:, hk], v, alpha, beta, scale)
@@ -97,6 +99,31 @@ def test_step_trajectory_matches_dense_rule(kda, dims, HV, H):
         # accumulated drift against the never re-synced dense evolution stays at the bf16 storage level
         assert np.abs(Sm[s] - Sdrift[s]).max() < (t + 1) * tol
     assert np.all(st["hcnt"][[1, 2]] == 20) and np.all(st["hcnt"][0] == 0)
+
+
+@pytest.mark.parametrize("glb", [0.0, -5.0, -0.5])
+def test_kda_gate_closed_forms(glb):
+    """The per-channel log-decay against closed forms written independently (kernels.py:702-712): GLM's bounded gate
+    glb sigmoid(e^A_log x) through scipy's expit, in [glb, 0] and decreasing in x for glb < 0; Kimi's -e^A_log softplus(x)
+    through log1p, linear above the softplus threshold 20."""
+    rng = np.random.default_rng(31)
+    HV, Kc = 3, 16
+    a = O.bf16(rng.uniform(-30.0, 30.0, (5, HV, Kc)))
+    dt = rng.uniform(-0.5, 0.5, (HV, Kc)).astype(np.float32)
+    A_log = rng.uniform(-1.0, 1.0, HV).astype(np.float32)
+    g, en = O.kda_gate(a, dt, A_log, glb)
+    x = (a.astype(np.float32) + dt).astype(np.float64)                 # the fp32 sum, as the kernels form it
+    ea = np.exp(A_log.astype(np.float64))[:, None]
+    if glb != 0.0:
+        from scipy.special import expit                                # library logistic, not the oracle's form
+        ref = glb * expit(ea * x)
+        assert np.all(g <= 0.0) and np.all(g >= glb)
+        order = np.argsort(x[:, 0, 0])
+        assert np.all(np.diff(g[order, 0, 0]) <= 0)                   # larger x: a log-decay closer to glb
+    else:
+        ref = np.where(x <= 20.0, -ea * np.log1p(np.exp(np.minimum(x, 20.0))), -ea * x)
+    np.testing.assert_allclose(g, ref, rtol=1e-12, atol=1e-300)
+    np.testing.assert_allclose(en.astype(np.float64), np.exp(ref), rtol=2 ** -23)
 
 
 def test_step_special_cases_gdn():
