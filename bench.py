@@ -608,7 +608,7 @@ def main():
         "speedup_vs_bf16_step": round(bf16_us / step_us, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(),
-                     "kernel": "gdn_step_kernel<2>", "bytes_per_launch": int(bytes_step)},
+                     "kernel": "gdn_step_kernel<128, 128, 2, false>", "bytes_per_launch": int(bytes_step)},
     }
     res["conv_fused_config1"] = {
         "workload": "config 1 step with vLLM's causal_conv1d_update (width 4, SiLU, bf16 state [NS, C, 3]) fused in, "
