@@ -76,6 +76,12 @@ template <int K>
 __device__ __forceinline__ float quad_bcast(float x) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), K * 0x55, 0xf, 0xf, false));
 }
+// a bulk load with or without the non-temporal hint
+template <bool NT, typename T>
+__device__ __forceinline__ T ld_nt(const T* p) {
+  if constexpr (NT) return ld_once(p);
+  else return *p;
+}
 constexpr float KSPLIT = 64.0f;   // kn / qn scaled by 2^6 before the fp16 hi / lo split (keeps the lo part normal)
 
 template <int K_, int V_, int G>
@@ -114,6 +120,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   constexpr int WPH = VD / 64;  // waves per value head
   constexpr int NE = KD / 64;   // channels per lane in the scalar work
   constexpr int KS32 = KD / 32, KS64 = KD / 64;   // k-steps of the 16x16x32 (bf16 / fp16) and 16x16x64 (int8) MFMAs
+  constexpr bool NT = KD == 128;                  // non-temporal bulk loads (see ld_once)
   __shared__ StepShared<K_, V_, G> sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
@@ -298,7 +305,8 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
     const int nch = live ? (h + RPK - 1) / RPK : 0;
     for (int c = wi; c < nch; c += WPH) {
       const int row = min(RPK * c + lane / LPR, L - 1);
-      lds_load16(ubg + row * (VD * 2) + 16 * (lane % LPR), (char*)&sh.ub[g][0][0] + c * 1024);
+      if (NT) lds_load16_nt(ubg + row * (VD * 2) + 16 * (lane % LPR), (char*)&sh.ub[g][0][0] + c * 1024);
+      else lds_load16(ubg + row * (VD * 2) + 16 * (lane % LPR), (char*)&sh.ub[g][0][0] + c * 1024);
     }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -313,7 +321,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
       const int j = 16 * (wv + NWV * t) + n16;
       const int jr = j < hmax ? j : 0;
 #pragma unroll
-      for (int ks = 0; ks < KS32; ++ks) kfr[t][ks] = *(const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4);
+      for (int ks = 0; ks < KS32; ++ks) kfr[t][ks] = ld_nt<NT>((const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4));
     }
   }
   i32x4 afr[4][KS64];           // the int8 tile: A fragments, row 64 wi + 16 rt + n16
@@ -322,7 +330,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int ks = 0; ks < KS64; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+      for (int ks = 0; ks < KS64; ++ks) afr[rt][ks] = ld_nt<NT>((const i32x4*)(rp + 16 * rt * KD + 64 * ks));
   }
   // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
   // stores at the end, so this count is exact)
@@ -584,7 +592,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   const int h = hfill;
   if (h >= L) { out[lt] = 0; return; }    // a full window is never stepped (the flush follows every step)
   // the four factor rows (2 KiB, inside the checkpoint block whatever R) to LDS, one KiB per wave
-  lds_load16((const char*)UQp + 1024 * wi + 16 * lane, (char*)&sh.uq[2 * wi][0]);
+  lds_load16_nt((const char*)UQp + 1024 * wi + 16 * lane, (char*)&sh.uq[2 * wi][0]);
   // The window's live entries j < h split between the waves: wave 0 takes [0, h0), wave 1 [h0, h), h0 a multiple of 4
   // (or h), each at most 32 entries.  Each wave's decays go straight to its own LDS rows (1 KiB = 4 rows per wave
   // instruction, rows past the buffer's last re-reading it); its values u_j and keys K_j go to registers, a channel
@@ -596,7 +604,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
     const char* gg = (const char*)((const f16_t*)st.Gbuf + sh_ * L * KD);
     for (int r = 0; r < cnt; r += 4) {
       const int row = min(jb + r + q4, L - 1);
-      lds_load16(gg + row * (KD * 2) + 16 * n16, (char*)&sh.gk[jb + r][0]);
+      lds_load16_nt(gg + row * (KD * 2) + 16 * n16, (char*)&sh.gk[jb + r][0]);
     }
     const uint32_t* ug = (const uint32_t*)((const bf16_t*)st.Ubuf + sh_ * L * VD) + lane;
     const uint32_t* kg = (const uint32_t*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD) + lane;
@@ -604,13 +612,13 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
     for (int g4 = 0; g4 < 8; ++g4)
       if (4 * g4 < cnt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ur[4 * g4 + i] = ug[(jb + min(4 * g4 + i, cnt - 1)) * (VD / 2)];
+        for (int i = 0; i < 4; ++i) ur[4 * g4 + i] = ld_once(ug + (jb + min(4 * g4 + i, cnt - 1)) * (VD / 2));
       }
 #pragma unroll
     for (int g4 = 0; g4 < 8; ++g4)
       if (4 * g4 < cnt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[4 * g4 + i] = kg[(jb + min(4 * g4 + i, cnt - 1)) * (KD / 2)];
+        for (int i = 0; i < 4; ++i) kr[4 * g4 + i] = ld_once(kg + (jb + min(4 * g4 + i, cnt - 1)) * (KD / 2));
       }
   }
   __builtin_amdgcn_sched_barrier(0);
@@ -620,7 +628,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 #pragma unroll
     for (int rt = 0; rt < 4; ++rt)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = *(const i32x4*)(rp + 16 * rt * KD + 64 * ks);
+      for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = ld_once((const i32x4*)(rp + 16 * rt * KD + 64 * ks));
   }
   constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the window's loads: the tile
   __builtin_amdgcn_sched_barrier(0);
