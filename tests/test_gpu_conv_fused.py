@@ -11,14 +11,17 @@ from tests import lqgpu as G
 from tests.fixtures import make_state
 
 pytestmark = pytest.mark.gpu
-H, HV, K, NS, L = 2, 4, 128, 6, 16
-C = 2 * H * K + HV * K
+NS, L = 6, 16
 
 
-@pytest.mark.parametrize("dim_first,with_bias", [(True, False), (False, True)])
-def test_fused_conv_step_matches_conv_then_step(dim_first, with_bias):
+# (conv-state layout, bias, key heads H, value heads HV, K, V): GQA 2 / 1 / 4 (the kernel's G) and the 64-dim heads
+@pytest.mark.parametrize("dim_first,with_bias,H,HV,K,V", [
+    (True, False, 2, 4, 128, 128), (False, True, 2, 4, 128, 128), (True, True, 4, 4, 128, 128),
+    (True, False, 1, 4, 128, 128), (True, True, 2, 4, 64, 128), (False, False, 2, 4, 64, 64)])
+def test_fused_conv_step_matches_conv_then_step(dim_first, with_bias, H, HV, K, V):
+    C = 2 * H * K + HV * V
     rng = np.random.default_rng(31)
-    st, _, _ = make_state(rng, NS, HV, H, L=L)
+    st, _, _ = make_state(rng, NS, HV, H, K=K, V=V, L=L)
     ssm_a, lq_a = G.to_gpu(st)
     ssm_b, lq_b = G.to_gpu(st)
     gen = torch.Generator(device=G.DEV).manual_seed(3)
@@ -41,7 +44,7 @@ def test_fused_conv_step_matches_conv_then_step(dim_first, with_bias):
             x = torch.randn(n, C, generator=gen, device=G.DEV).to(torch.bfloat16)
             a = (torch.rand(n, HV, generator=gen, device=G.DEV) * 2).to(torch.bfloat16)
             b = torch.randn(n, HV, generator=gen, device=G.DEV).to(torch.bfloat16)
-            out_a = torch.zeros(n, HV, K, dtype=torch.bfloat16, device=G.DEV)
+            out_a = torch.zeros(n, HV, V, dtype=torch.bfloat16, device=G.DEV)
             out_b = torch.zeros_like(out_a)
             live = idx.long() > 0                                  # padding rows keep their conv state (as vLLM's)
             mixed = torch.zeros(n, C, dtype=torch.bfloat16, device=G.DEV)
@@ -68,6 +71,7 @@ def test_conv_update_kernel_matches_stand_in():
     """The standalone conv update (lq_conv_update, the bench's unfused baseline) against the stand-in vLLM conv on the
     device: outputs equal up to SiLU's last fp32 bit before bf16 rounding, conv states identical, padding rows untouched."""
     from leapquant_amd import kernels as KN
+    C = 2 * 2 * 128 + 4 * 128
     gen = torch.Generator(device=G.DEV).manual_seed(9)
     conv_a = torch.randn(NS, C, 3, generator=gen, device=G.DEV).to(torch.bfloat16)
     conv_b = conv_a.clone()
