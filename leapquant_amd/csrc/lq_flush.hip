@@ -174,16 +174,20 @@ __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
 // modified Gram-Schmidt on the R columns of the 128 x 4 matrix whose rows l, l + 64 a lane of wave 0 holds
 // (kernels.py:2170-2183, 2190-2203)
 __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
-  for (int j = 0; j < R; ++j) {
-    for (int c = 0; c < j; ++c) {
-      const float sc = sum64u(fmaf(p0[c], p0[j], p1[c] * p1[j]));
-      p0[j] = p0[j] - sc * p0[c];
-      p1[j] = p1[j] - sc * p1[c];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {               // unrolled over the largest rank (no run-time register indexing)
+    if (j < R) {
+#pragma unroll
+      for (int c = 0; c < j; ++c) {
+        const float sc = sum64u(fmaf(p0[c], p0[j], p1[c] * p1[j]));
+        p0[j] = p0[j] - sc * p0[c];
+        p1[j] = p1[j] - sc * p1[c];
+      }
+      const float nrm = sum64u(fmaf(p0[j], p0[j], p1[j] * p1[j]));
+      const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
+      p0[j] *= rs;
+      p1[j] *= rs;
     }
-    const float nrm = sum64u(fmaf(p0[j], p0[j], p1[j] * p1[j]));
-    const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
-    p0[j] *= rs;
-    p1[j] *= rs;
   }
 }
 
@@ -805,14 +809,16 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     if ((l & 15) == 0) sh.sk[16 * w + 4 * q + i] = skc;
   }
   __syncthreads();
-  float skr[4];
+  // E / Sk and E / (Sk Sv) (kernels.py:2224-2229) as products with reciprocals taken once per column and once per row
+  // (12 divisions per lane instead of 64; within a few ulp of the quotients, below the codes' rounding step)
+  float rsk[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) skr[i] = sh.sk[16 * w + 4 * q + i];
+  for (int i = 0; i < 4; ++i) rsk[i] = 1.0f / sh.sk[16 * w + 4 * q + i];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] / skr[i]));   // kernels.py:2224-2227
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] * rsk[i]));   // kernels.py:2224-2227
     m = fmaxf(m, __shfl_xor(m, 16));
     m = fmaxf(m, __shfl_xor(m, 32));
     if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
@@ -827,10 +833,11 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
     const float svv = fmaxf(max_parts(sh.rowmax, v), LQ_EPS);
+    const float rsv = qmax / svv;
     uint32_t word = 0;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = (t.a[nt][i] / (skr[i] * svv)) * qmax;   // kernels.py:2229
+      const float x = (t.a[nt][i] * rsk[i]) * rsv;            // kernels.py:2229
       const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
       word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
     }
