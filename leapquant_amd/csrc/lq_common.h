@@ -71,19 +71,28 @@ __device__ __forceinline__ float max16(float x) {
   x = fmaxf(x, dpp<DPP_MIRROR>(x));
   return x;
 }
+// Lanes l and l ^ 16 (l ^ 32) through v_permlane16_swap (v_permlane32_swap), gfx950: a VALU exchange instead of
+// __shfl_xor's LDS-crossbar permute.  With both operands x, the two halves returned are x[l] and x[l ^ 16] (x[l ^ 32])
+// in some order, so the sum / max equals x + __shfl_xor(x, 16) bit for bit.
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 // all-reduce over the wave
-__device__ __forceinline__ float sum64(float x) {
-  x = sum16(x);
-  x += __shfl_xor(x, 16);
-  x += __shfl_xor(x, 32);
-  return x;
-}
-__device__ __forceinline__ float max64(float x) {
-  x = max16(x);
-  x = fmaxf(x, __shfl_xor(x, 16));
-  x = fmaxf(x, __shfl_xor(x, 32));
-  return x;
-}
+__device__ __forceinline__ float sum64(float x) { return xor32_sum(xor16_sum(sum16(x))); }
+__device__ __forceinline__ float max64(float x) { return xor32_max(xor16_max(max16(x))); }
 
 // ---- gates (scalar, per (row, head) or per channel); evaluated in fp64 and rounded once ----------------------------
 __device__ __forceinline__ double softplus20(double x) {

@@ -135,8 +135,7 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
     }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      s[r] += __shfl_xor(s[r], 16);
-      s[r] += __shfl_xor(s[r], 32);
+      s[r] = xor32_sum(xor16_sum(s[r]));
     }
     if (q == 0) part[w][16 * nt + (l & 15)] = s;
   }
@@ -819,8 +818,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     float m = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] * rsk[i]));   // kernels.py:2224-2227
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
+    m = xor32_max(xor16_max(m));
     if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
   }
   __syncthreads();
