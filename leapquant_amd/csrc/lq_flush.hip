@@ -82,14 +82,8 @@ __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane
 __device__ __forceinline__ float rl(float x, int l) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
 }
-__device__ __forceinline__ float sum64u(float x) {
-  x = sum16(x);
-  return ((rl(x, 0) + rl(x, 16)) + rl(x, 32)) + rl(x, 48);
-}
-__device__ __forceinline__ float max64u(float x) {
-  x = max16(x);
-  return fmaxf(fmaxf(rl(x, 0), rl(x, 16)), fmaxf(rl(x, 32), rl(x, 48)));
-}
+// wave all-reduce for the serial factor steps (MGS, CholeskyQR): VALU lane swaps, every lane gets the result
+__device__ __forceinline__ float sum64u(float x) { return sum64(x); }
 
 // fn(i, s): s[r] = sum_v M[c_i][v] X[v][r] for the lane's 4 key channels c_i = 16 w + 4 (l >> 4) + i (complete in
 // every lane of the 16-lane row)
