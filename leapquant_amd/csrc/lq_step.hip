@@ -159,10 +159,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int c = lane + 64 * e;
-    if (CONV) {
-      ktap[e] = conv_taps(cv, mrow, cvb, H * KD + hk * KD + c);
-      qtap[e] = conv_taps(cv, mrow, cvb, hk * KD + c);
-    } else {
+    if (!CONV) {
       kxr[e] = mrow[H * KD + hk * KD + c];
       qxr[e] = mrow[hk * KD + c];
     }
@@ -204,7 +201,12 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   if (wi == 0) {
     const float alpha = gdn_alpha_f(bf2f(araw), dtb, alog);
     const float beta = beta_f(bf2f(braw));
-    if (CONV) {
+    if (CONV) {                 // the key / query taps: loaded by the scalar-work waves only (the other waves skip them)
+#pragma unroll
+      for (int e = 0; e < NE; ++e) {
+        ktap[e] = conv_taps(cv, mrow, cvb, H * KD + hk * KD + lane + 64 * e);
+        qtap[e] = conv_taps(cv, mrow, cvb, hk * KD + lane + 64 * e);
+      }
 #pragma unroll
       for (int e = 0; e < NE; ++e) {
         kxr[e] = f2bf(conv_out(ktap[e], cv.silu));
