@@ -90,22 +90,22 @@ __device__ __forceinline__ float sum64u(float x) { return sum64(x); }
 template <class F>
 __device__ __forceinline__ void colred(const Tile& t, const f32x4* X, F fn) {
   const int l = lane_id();
-  f32x4 xv[8];
+  f32x4 acc[4] = {};                                  // one row of X at a time (the sums keep the order of the rows)
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) xv[nt] = X[16 * nt + (l & 15)];
+  for (int nt = 0; nt < 8; ++nt) {
+    const f32x4 xv = X[16 * nt + (l & 15)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m = t.a[nt][i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(m, xv[r], acc[i][r]);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+    f32x4 s;
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const float m = t.a[nt][i];
-      s[0] = fmaf(m, xv[nt][0], s[0]);
-      s[1] = fmaf(m, xv[nt][1], s[1]);
-      s[2] = fmaf(m, xv[nt][2], s[2]);
-      s[3] = fmaf(m, xv[nt][3], s[3]);
-    }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = sum16(s[r]);
+    for (int r = 0; r < 4; ++r) s[r] = sum16(acc[i][r]);
     fn(i, s);
   }
 }
@@ -763,19 +763,16 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     }
     __syncthreads();
   }
-  // U = fp16(S^T Q), Q16 = fp16(Q)
-  f32x4 ucol[4];
-  colred(t, sh.qv, [&](int i, f32x4 s) { ucol[i] = s; });
-  __syncthreads();
-  if ((l & 15) == 0) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
+  // U = fp16(S^T Q) straight to LDS (sh.pp is not read again before the next barrier), Q16 = fp16(Q)
+  colred(t, sh.qv, [&](int i, f32x4 s) {
+    if ((l & 15) == 0) {
       f32x4 u;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(ucol[i][r]) : 0.f;
+      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(s[r]) : 0.f;
       sh.pp[16 * w + 4 * q + i] = u;
     }
-  }
+  });
+  __syncthreads();                                    // every wave has read Q (sh.qv)
   if (tid < VD) {
     f32x4 x = sh.qv[tid];
 #pragma unroll
