@@ -19,14 +19,10 @@ __device__ __forceinline__ float bf2f(bf16_t h) { return __uint_as_float(((uint3
 
 // fp32 -> bf16 / fp16, round to nearest even: the gfx950 conversions v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32
 typedef __bf16 lq_bf16x2 __attribute__((ext_vector_type(2)));
-typedef _Float16 lq_f16x2 __attribute__((ext_vector_type(2)));
 __device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16_t, (__bf16)f); }
 // two values in one word: lo in bits 0-15, hi in bits 16-31
 __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, lq_bf16x2{(__bf16)lo, (__bf16)hi});
-}
-__device__ __forceinline__ uint32_t pk_f16(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, lq_f16x2{(_Float16)lo, (_Float16)hi});
 }
 // bf16 halves of a word as fp32
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
@@ -123,7 +119,7 @@ __device__ __forceinline__ float rsqrtf_rn(float x) { return 1.0f / sqrtf(x); }
 
 // ---- direct global -> LDS loads (gfx950 global_load_lds_dwordx4): lane l's 16 bytes land at lds_wave_base + 16 l ----
 // Issued through inline asm: the compiler's own form makes every such load wait for all loads in flight (it cannot
-// tell that successive loads write disjoint LDS).  The caller waits (s_waitcnt vmcnt(0)) before reading the LDS data.
+// tell that successive loads write disjoint LDS).  The caller waits (s_waitcnt vmcnt) before reading the LDS data.
 // Nothing else in these kernels keeps a value in M0.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
@@ -144,7 +140,6 @@ __device__ __forceinline__ void lds_load16_nt(const void* gsrc, void* lds_wave_b
 // the hint), and not for the 64-dim GDN tiles (measured slightly slower).
 template <typename T>
 __device__ __forceinline__ T ld_once(const T* p) { return __builtin_nontemporal_load(p); }
-__device__ __forceinline__ void wait_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // ---- depthwise causal conv1d update (lq_conv, W = 4) ----------------------------------------------------------
 // Conv taps of one channel (lq_conv, W = 4): the raw projection x, the slot's three state taps and the four weights.
@@ -190,12 +185,6 @@ __device__ __forceinline__ void mark_due(int* ctl) {
 }
 
 // ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------
-struct Block {
-  const int8_t* Sq;   // [V][K]
-  float* Sk;          // [K]
-  float* Sv;          // [V]
-  f16_t* UQ;          // [R][K+V]
-};
 __device__ __forceinline__ char* block_base(const lq_state& st, int slot, int hv) {
   return (char*)st.ssm + 4ll * ((long long)slot * st.slot_stride + (long long)hv * st.V * st.K);
 }

@@ -18,37 +18,6 @@ constexpr int KD = 128;   // key dim
 constexpr int VD = 128;   // value dim
 constexpr int LMAX = 64;  // largest window the kernels are built for
 
-__device__ __forceinline__ void unpack8(uint4 w, float* f) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = __uint_as_float(u[i] << 16);
-    f[2 * i + 1] = __uint_as_float(u[i] & 0xffff0000u);
-  }
-}
-__device__ __forceinline__ void unpack8h(uint4 w, float* f) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    f[2 * i] = h2f((f16_t)(u[i] & 0xffffu));
-    f[2 * i + 1] = h2f((f16_t)(u[i] >> 16));
-  }
-}
-
-// 16 codes of one row chunk against the lane's 16 column operands
-__device__ __forceinline__ void dot16_i8(uint4 w, const float* kf, const float* qf, float& m, float& y) {
-  const uint32_t u[4] = {w.x, w.y, w.z, w.w};
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const float x = (float)(int)(int8_t)(u[i] >> (8 * b));
-      m = fmaf(x, kf[4 * i + b], m);
-      y = fmaf(x, qf[4 * i + b], y);
-    }
-  }
-}
-
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
