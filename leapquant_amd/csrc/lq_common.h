@@ -160,6 +160,7 @@ __device__ __forceinline__ ConvTaps conv_taps(const lq_conv& cv, const bf16_t* x
 }
 // mixed[c] = bf16(act(w0 s0 + w1 s1 + w2 s2 + w3 x + bias)): products and sums rounded one at a time, left to right
 __device__ __forceinline__ float conv_out(const ConvTaps& t, bool silu) {
+#pragma clang fp contract(off)                        // __fmul_rn / __fadd_rn are plain * / +: keep them unfused
   const float w[4] = {bf_lo(t.w.x), bf_hi(t.w.x), bf_lo(t.w.y), bf_hi(t.w.y)};
   float y = __fmul_rn(w[0], bf2f(t.s[0]));
   y = __fadd_rn(y, __fmul_rn(w[1], bf2f(t.s[1])));

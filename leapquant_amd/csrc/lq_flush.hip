@@ -184,7 +184,7 @@ __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
   }
 }
 
-// the 8 code words of the lane's tile entries (issued early; consumed by tile_from_words).  A head of K_ x V_ < 128 x
+// the 8 code words of the lane's tile entries (issued early; consumed by tile_add_words).  A head of K_ x V_ < 128 x
 // 128 sits zero-padded in the tile: entries past its rows / columns read as 0 (clamped addresses, no divergent load).
 template <int K_ = KD, int V_ = VD>
 __device__ __forceinline__ void load_code_words(uint32_t wds[8], const int8_t* Sq) {
@@ -198,8 +198,11 @@ __device__ __forceinline__ void load_code_words(uint32_t wds[8], const int8_t* S
     wds[nt] = (cok && (V_ == VD || v < V_)) ? x : 0u;
   }
 }
-// Tile init with the dequantised checkpoint codes  x svr[v] x skl[c]
-__device__ __forceinline__ void tile_from_words(Tile& t, const uint32_t wds[8], const float* svr, const float* skl) {
+// t += the dequantised checkpoint codes  x svr[v] x skl[c], each term rounded to fp32 before the add.  The flush adds
+// them after the window's MFMA products, which it accumulates from zero: the window terms are up to ~20x larger than
+// their sum (they cancel), and an accumulator seeded with the checkpoint term rounds them at a coarser step.
+__device__ __forceinline__ void tile_add_words(Tile& t, const uint32_t wds[8], const float* svr, const float* skl) {
+#pragma clang fp contract(off)
   const int l = lane_id(), w = wave_id(), q = l >> 4;
   const int c0 = 16 * w + 4 * q;
   float kc[4];
@@ -209,7 +212,7 @@ __device__ __forceinline__ void tile_from_words(Tile& t, const uint32_t wds[8], 
   for (int nt = 0; nt < 8; ++nt) {
     const float rv = svr[16 * nt + (l & 15)];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t.a[nt][i] = ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * rv) * kc[i];
+    for (int i = 0; i < 4; ++i) t.a[nt][i] = t.a[nt][i] + ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * rv) * kc[i];
   }
 }
 
@@ -255,7 +258,7 @@ __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int 
 }
 // Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write.  GDN: op0 =
 // K_j[c], op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 = raw K_j[c] / e_j[c] (turned
-// into the decayed key operands by kda_key_scan), op2 = u_j[v].
+// into the decayed key operands by kda_key_scan), op2 = u_j[v].  Rows j >= h carry zero values and, for KDA, decay 1.
 template <bool KDA>
 __device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP) {
   const int ch = win_chunk(LP);
@@ -277,13 +280,15 @@ __device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, 
     uint32_t* o2 = (uint32_t*)&sh.op[2][c8 + e][j0];
     *o0 = __builtin_amdgcn_perm(kb[x], ka[x], sel);
     if (!KDA) {
+      // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
+#pragma clang fp contract(off)
       const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
       const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
       const uint32_t hi = pk_bf16(wu0, wu1);
       *o1 = hi;
       *o2 = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
     } else {
-      *o1 = __builtin_amdgcn_perm(gb[x], ga[x], sel);
+      *o1 = (__builtin_amdgcn_perm(gb[x], ga[x], sel) & keep) | (0x3c003c00u & ~keep);   // rows >= h: decay 1
       *o2 = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
     }
   }
@@ -291,14 +296,16 @@ __device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, 
 // KDA key operands, in place over the raw keys op[0] and decays op[1] ([c][j]): op[0..NT-1] = the NT-term bf16 split
 // (hi, [mid,] lo) of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, state.py:124-127).
 // Four lanes per channel: lane s of a quad takes the s-th quarter of the window (LP / 4 = 8 or 16 entries, held in
-// registers), forms its decay product, takes the product of the later quarters from its neighbours by DPP and walks
-// its quarter backwards from there, as the reference's running product does.  FT = 4 KD threads, all of them take part.
+// registers) and walks it backwards.  The decay product it starts from, D at the top of its quarter, is the running
+// product of the later decays taken in the reference's own order (from the window's end down, one rounding per factor),
+// so every D_j is bit-identical to the sequential walk's: a product regrouped by quarters rounds differently, and the
+// key operands' cancellation in the rebuild turns those last-bit differences into fp16 flips of B.  The prefix costs a
+// lane up to 3 LP / 4 dependent multiplies; the per-entry split work stays divided four ways.  FT = 4 KD threads.
 template <int NT>
 __device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float* wj, int h, int LP) {
   static_assert(FT == 4 * KD, "one quad of lanes per channel");
   const int tid = opaque_tid(), c = tid >> 2, s = tid & 3, seg = LP >> 2, jb = s * seg;
   uint32_t ku[2][4], eu[2][4];
-  float p = 1.0f;
 #pragma unroll
   for (int x = 1; x >= 0; --x) {
     if (8 * x < seg) {
@@ -306,15 +313,26 @@ __device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float*
       const uint4 er = *(const uint4*)&op[1][c][jb + 8 * x];
       ku[x][0] = kr.x; ku[x][1] = kr.y; ku[x][2] = kr.z; ku[x][3] = kr.w;
       eu[x][0] = er.x; eu[x][1] = er.y; eu[x][2] = er.z; eu[x][3] = er.w;
-#pragma unroll
-      for (int e = 7; e >= 0; --e)
-        if (jb + 8 * x + e < h) p = p * h2f((f16_t)(eu[x][e >> 1] >> (16 * (e & 1))));
     }
   }
-  const float p1 = dpp<0x55>(p), p2 = dpp<0xaa>(p), p3 = dpp<0xff>(p);   // quarter products of lanes 1..3
-  float dcur = s < 3 ? p3 : 1.0f;
-  if (s < 2) dcur = dcur * p2;
-  if (s < 1) dcur = dcur * p1;
+  float dcur = 1.0f;
+#pragma unroll
+  for (int sq = 3; sq >= 1; --sq) {                   // the later quarters, last first
+    const int q0 = sq * seg;
+    if (q0 < h) {                                     // rows >= h hold decay 1 (exact factors)
+      float t = dcur;
+#pragma unroll
+      for (int x = 1; x >= 0; --x) {
+        if (8 * x < seg) {
+          const uint4 er = *(const uint4*)&op[1][c][q0 + 8 * x];
+          const uint32_t ew[4] = {er.x, er.y, er.z, er.w};
+#pragma unroll
+          for (int e = 7; e >= 0; --e) t = t * h2f((f16_t)(ew[e >> 1] >> (16 * (e & 1))));
+        }
+      }
+      dcur = s < sq ? t : dcur;
+    }
+  }
 #pragma unroll
   for (int x = 1; x >= 0; --x) {
     if (8 * x < seg) {
@@ -324,6 +342,8 @@ __device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float*
       for (int e = 7; e >= 0; --e) {
         const int j = j0 + e;
         if (j < h) {
+          // the split is of the fp32-rounded product (kernels.py:1456-1463): no fusing into the first subtraction
+#pragma clang fp contract(off)
           float r = bf2f((bf16_t)(ku[x][e >> 1] >> (16 * (e & 1)))) * (wj[j] * dcur);
 #pragma unroll
           for (int t = 0; t < NT; ++t) {
@@ -478,7 +498,8 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   f16x4 bh[8], bt[8];                                 // B packed: k = c (tile layout) and k = v (transposed)
   {
     Tile t;
-    tile_from_words(t, wds, sh.svr, sh.skl);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     if (!KDA) {
       rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
       rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
@@ -486,6 +507,7 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
       rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
       rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
     }
+    tile_add_words(t, wds, sh.svr, sh.skl);
     f16x4 ident;
 #pragma unroll
     for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
@@ -928,7 +950,7 @@ void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
         const int x = e >> 1;
         const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
         *(uint32_t*)&sh.op[0][c8 + e][j0] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
-        *(uint32_t*)&sh.op[1][c8 + e][j0] = __builtin_amdgcn_perm(gb[x], ga[x], sel);
+        *(uint32_t*)&sh.op[1][c8 + e][j0] = (__builtin_amdgcn_perm(gb[x], ga[x], sel) & keep) | (0x3c003c00u & ~keep);
         *(uint32_t*)&sh.op[3][c8 + e][j0] = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
       }
     }

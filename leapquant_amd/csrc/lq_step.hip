@@ -224,6 +224,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
         const float xs[2] = {kn[e], qn[e]};
 #pragma unroll
         for (int v2 = 0; v2 < 2; ++v2) {
+#pragma clang fp contract(off)                        // split of the rounded kn / qn: no fusing of x = k / |k| into x - hi
           const float x = xs[v2];
           const bf16_t hi = f2bf(x);
           const float r1 = x - bf2f(hi);
@@ -650,6 +651,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       const float xs[2] = {kn[e], qn[e]};
 #pragma unroll
       for (int v2 = 0; v2 < 2; ++v2) {
+#pragma clang fp contract(off)                        // split of the rounded kn / qn: no fusing of x = k / |k| into x - hi
         const float x = xs[v2];
         const bf16_t hi = f2bf(x);
         const float r1 = x - bf2f(hi);

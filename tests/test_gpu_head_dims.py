@@ -92,7 +92,7 @@ def test_flush_matches_oracle(K, V, L):
     assert len(dbg["pairs"]) == 2 * HV
     _run_flush(lq, ssm, torch.from_numpy(idx.astype(np.int32)).to(G.DEV))
     g = G.from_gpu(ssm, lq)
-    frac, mx = G.code_mismatch(g["Sq"], st["Sq"])
+    frac, mx = G.code_mismatch(g["Sq"][[1, 3]], st["Sq"][[1, 3]])           # the flushed heads only
     assert mx <= 1 and frac <= 1e-3, (frac, mx)
     np.testing.assert_allclose(g["Sk"], st["Sk"], rtol=2e-3)
     np.testing.assert_allclose(g["Sv"], st["Sv"], rtol=2e-3)
