@@ -127,15 +127,12 @@ __device__ __forceinline__ void lds_load16(const void* gsrc, void* lds_wave_base
   const unsigned lds = (unsigned)(size_t)(__attribute__((address_space(3))) char*)(char*)lds_wave_base;
   asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" :: "v"(gsrc), "s"(lds) : "memory", "m0");
 }
-// the same with the non-temporal hint (see ld_once)
-__device__ __forceinline__ void lds_load16_nt(const void* gsrc, void* lds_wave_base) {
-  const unsigned lds = (unsigned)(size_t)(__attribute__((address_space(3))) char*)(char*)lds_wave_base;
-  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off nt" :: "v"(gsrc), "s"(lds) : "memory", "m0");
-}
 #pragma clang diagnostic pop
 // Loads of data that a launch reads once and that no other workgroup of the launch reads (the steps' int8 tiles and
-// window rows): non-temporal, so that they stream through L2 / MALL without displacing what is still to be read.
-// Measured at config 1 (GDN step 17.1 -> 16.2 us) and config 2 (KDA step 47.3 -> 45.5 us).  Not for data two
+// buffered keys, the KDA step's window keys and values): non-temporal, so that they stream through L2 / MALL without
+// displacing what is still to be read.  Measured at config 1 (GDN step 17.1 -> 16.2 us) and config 2 (KDA step 47.3
+// -> 45.5 us).  The direct-to-LDS loads (GDN window rows, KDA factor rows and decays) measured faster without the hint
+// (GDN 15.98 -> 15.86 us, KDA 45.1 -> 44.1 us).  Not for data two
 // workgroups share (the flush reads a key head's window from each of its value heads' workgroups: 92 -> 100 us with
 // the hint), and not for the 64-dim GDN tiles (measured slightly slower).
 template <typename T>
