@@ -22,6 +22,7 @@ import os
 import sys
 import time
 
+T_START = time.perf_counter()
 ROOT = os.path.dirname(os.path.abspath(__file__))
 if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
@@ -58,6 +59,11 @@ def kda_step_bytes(N, HV, K, V, R, h):
 def quantize_bytes(n_heads, K, V):
     """One standalone quantize: the fp32 state in, the checkpoint (codes, scales, factors) out."""
     return n_heads * (4 * V * K + V * K + 4 * (K + V) + 2 * 4 * (K + V))
+
+
+def progress(msg):
+    """One line per finished stage on stderr (the result stays the only line on stdout)."""
+    print("[bench] %s (%.0f s)" % (msg, time.perf_counter() - T_START), file=sys.stderr, flush=True)
 
 
 def event_ms(torch, stream, fn, reps):
@@ -480,6 +486,7 @@ def main():
     ms_total = e0.elapsed_time(e1)
     us_per_step = ms_total * 1e3 / args.steps
 
+    progress("decode loop: %.3f us per call" % us_per_step)
     # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
     # of the NSET sets 64 / NSET steps; NSET replays take every window from h = 0 to h = 64, then every head is due) ----
     lq.quantize(ssm, all_slots)                                   # every window back to h = 0
@@ -513,6 +520,7 @@ def main():
     achieved = bytes_step / (step_us * 1e-6) / 1e9
     amort_bytes = bytes_step + bytes_flush / L
 
+    progress("step %.3f us, flush due %.1f us, idle %.2f us" % (step_us, flush_due_us, flush_idle_us))
     # ---- bf16-state baseline (same step on a dense bf16 state), rotated sets ----
     del gsteps, gflush, gidle, gdec, grem
     Sd = torch.empty(NS, HV, V, K, device=dev, dtype=torch.bfloat16)
@@ -591,9 +599,13 @@ def main():
     torch.cuda.synchronize()
     del src, dst
 
+    progress("bf16 baseline, fused conv, calibration copies")
     kda = kda_bench(torch, dev, stream, capture)
+    progress("KDA config 2")
     fq = flush_quantize_bench(torch, dev, stream)
+    progress("config-3 flush / quantize")
     hd = head_dims_bench(torch, dev, stream, capture)
+    progress("head-dim variants")
 
     res = {
         "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
