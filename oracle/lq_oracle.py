@@ -494,14 +494,25 @@ def quantize_dense(S, Q0, qmax=QMAX, iters=1):
         Q = mgs_cols(np.einsum("dvc,dcr->dvr", S64, P))                                         # kernels.py:2184-2203
     U16 = fp16(np.einsum("dvc,dvr->dcr", S64, Q)).astype(np.float64)                            # kernels.py:2204-2209
     Q16 = fp16(Q).astype(np.float64)                                                             # kernels.py:2210-2211
+    codes, sk, sv = quantize_residual(S, U16, Q16, qmax)
+    UQ = np.concatenate([fp16(U16.transpose(0, 2, 1)), fp16(Q16.transpose(0, 2, 1))], axis=-1)
+    return codes, sk, sv, UQ
+
+
+def quantize_residual(S, U16, Q16, qmax=QMAX):
+    """The residual stage of the standalone quantize: fp32 states S [D,V,K] and fp16 factors U16 [D,K,R], Q16 [D,V,R]
+    (values, any float dtype) -> (codes int8 [D,V,K], Sk [D,K], Sv [D,V]).  kernels.py:2212-2229."""
+    S64 = np.asarray(S, F32).astype(np.float64)
+    V = S64.shape[1]
+    U16 = np.asarray(U16, np.float64)
+    Q16 = np.asarray(Q16, np.float64)
     E = r32(S64 - np.einsum("dvr,dcr->dvc", Q16, U16))                                          # kernels.py:2212-2217
     colsum = r32(np.abs(E.astype(np.float64)).sum(1))
     sk = np.maximum(r32(np.sqrt(r32(colsum / F32(V)).astype(np.float64))), F32(EPS)).astype(F32)   # kernels.py:2222
     sv = np.maximum(np.abs(r32(E / sk[:, None, :])).max(-1), F32(EPS)).astype(F32)             # kernels.py:2224-2227
     t = r32(r32(E / r32(sk[:, None, :] * sv[:, :, None])) * F32(qmax))
     codes = np.clip(np.rint(t), -qmax, qmax).astype(np.int8)                                    # kernels.py:2229
-    UQ = np.concatenate([fp16(U16.transpose(0, 2, 1)), fp16(Q16.transpose(0, 2, 1))], axis=-1)
-    return codes, sk, sv, UQ
+    return codes, sk, sv
 
 
 def quantize(st, S_slots, Q0, idx, qmax=QMAX):
