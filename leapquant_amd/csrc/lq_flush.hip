@@ -726,16 +726,86 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
 // low-rank factoriser's iters = 3, kernels.py:2318-2326), then the residual codes.  KDA resets its window as
 // state.py:138-142 does (Pbuf = 0 per channel, Gbuf = 1).
 // ------------------------------------------------------------------------------------------------------------------
+// Four waves per head (256 threads), so that four heads fit on a CU at <= 128 VGPRs (the flush's eight-wave layout
+// fits two): wave w holds key channels 32 w .. 32 w + 31 as two groups of 16, lane l rows 16 nt + (l & 15) and, in group
+// cg, channels 32 w + 16 cg + 4 (l >> 4) + i, i < 4 -- 64 fp32 of the state per lane.
+constexpr int QW = 4;                 // waves per head
+constexpr int QT = 64 * QW;           // threads per workgroup
+
+struct QTile {
+  f32x4 a[2][8];
+};
+
 struct QuantShared {
   f32x4 qv[VD];
   f32x4 pp[KD];
-  f32x4 qpart[NW][VD];
-  float rowmax[NW][VD];
+  f32x4 qpart[QW][VD];
+  float rowmax[QW][VD];
   float sk[KD];
 };
 
+// column sums sum_v M[v][c] X[v][r] for this lane's channels: fn(cg, i, s) once per (group, channel) with the full sum
+// over the 128 rows (the rows of one lane first, in order, then across its 16 lanes)
+template <typename F>
+__device__ __forceinline__ void colred_q(const QTile& t, const f32x4* X, F fn) {
+  const int l = lane_id();
+#pragma unroll
+  for (int cg = 0; cg < 2; ++cg) {
+    f32x4 acc[4] = {};
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f32x4 xv = X[16 * nt + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float m = t.a[cg][nt][i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(m, xv[r], acc[i][r]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = sum16(acc[i][r]);
+      fn(cg, i, s);
+    }
+  }
+}
+
+// part[w][v][r] = sum over this wave's 32 channels c of M[v][c] Y[c][r]  (caller sums the QW waves)
+__device__ __forceinline__ void rowred_q(const QTile& t, const f32x4* Y, f32x4 (*part)[VD]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  f32x4 yc[2][4];
+#pragma unroll
+  for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) yc[cg][i] = Y[32 * w + 16 * cg + 4 * q + i];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float m = t.a[cg][nt][i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s[r] = fmaf(m, yc[cg][i][r], s[r]);
+      }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = xor32_sum(xor16_sum(s[r]));
+    if (q == 0) part[w][16 * nt + (l & 15)] = s;
+  }
+}
+
+__device__ __forceinline__ f32x4 sum_parts_q(const f32x4 (*part)[VD], int v) {
+  f32x4 s = part[0][v];
+#pragma unroll
+  for (int w = 1; w < QW; ++w) s += part[w][v];
+  return s;
+}
+
 template <bool KDA, int K_ = KD, int V_ = VD>
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(QT) __attribute__((amdgpu_waves_per_eu(4)))
 void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax, int iters) {
   static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
   __shared__ QuantShared sh;
@@ -747,15 +817,16 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   char* base = block_base(st, slot, hv);
   const float* S = (const float*)base;
-  Tile t;                                             // a K_ x V_ < 128 x 128 head zero-padded (see flush_head)
-  {
-    const int c = 16 * w + 4 * q;
+  QTile t;                                            // a K_ x V_ < 128 x 128 head zero-padded (see flush_head)
+#pragma unroll
+  for (int cg = 0; cg < 2; ++cg) {
+    const int c = 32 * w + 16 * cg + 4 * q;
     const bool cok = K_ == KD || c < K_;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + (l & 15);
       const float4 x = *(const float4*)(S + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
-      t.a[nt] = (cok && (V_ == VD || v < V_)) ? f32x4{x.x, x.y, x.z, x.w} : f32x4{0.f, 0.f, 0.f, 0.f};
+      t.a[cg][nt] = (cok && (V_ == VD || v < V_)) ? f32x4{x.x, x.y, x.z, x.w} : f32x4{0.f, 0.f, 0.f, 0.f};
     }
   }
   if (tid < VD) {
@@ -766,7 +837,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   __syncthreads();
   // P = S^T Q, MGS; Q = S P, MGS (`iters` rounds)
   for (int it = 0; it < iters; ++it) {
-    colred(t, sh.qv, [&](int i, f32x4 s) { if ((l & 15) == 0) sh.pp[16 * w + 4 * q + i] = s; });
+    colred_q(t, sh.qv, [&](int cg, int i, f32x4 s) { if ((l & 15) == 0) sh.pp[32 * w + 16 * cg + 4 * q + i] = s; });
     __syncthreads();
     if (w == 0) {
       f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
@@ -775,10 +846,10 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
       sh.pp[l + 64] = p1;
     }
     __syncthreads();
-    rowred(t, sh.pp, sh.qpart);
+    rowred_q(t, sh.pp, sh.qpart);
     __syncthreads();
     if (w == 0) {
-      f32x4 p0 = sum_parts(sh.qpart, l), p1 = sum_parts(sh.qpart, l + 64);
+      f32x4 p0 = sum_parts_q(sh.qpart, l), p1 = sum_parts_q(sh.qpart, l + 64);
       mgs(p0, p1, R);
       sh.qv[l] = p0;
       sh.qv[l + 64] = p1;
@@ -786,12 +857,12 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     __syncthreads();
   }
   // U = fp16(S^T Q) straight to LDS (sh.pp is not read again before the next barrier), Q16 = fp16(Q)
-  colred(t, sh.qv, [&](int i, f32x4 s) {
+  colred_q(t, sh.qv, [&](int cg, int i, f32x4 s) {
     if ((l & 15) == 0) {
       f32x4 u;
 #pragma unroll
       for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(s[r]) : 0.f;
-      sh.pp[16 * w + 4 * q + i] = u;
+      sh.pp[32 * w + 16 * cg + 4 * q + i] = u;
     }
   });
   __syncthreads();                                    // every wave has read Q (sh.qv)
@@ -804,33 +875,40 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   __syncthreads();
   // E = S - Q U^T (fp32), column scales
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const f32x4 unc = sh.pp[16 * w + 4 * q + i];
-    float s = 0.f;
+  for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const f32x4 qnv = sh.qv[16 * nt + (l & 15)];
-      float e = t.a[nt][i];
+    for (int i = 0; i < 4; ++i) {
+      const int c = 32 * w + 16 * cg + 4 * q + i;
+      const f32x4 unc = sh.pp[c];
+      float s = 0.f;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
-      t.a[nt][i] = e;
-      s += fabsf(e);
+      for (int nt = 0; nt < 8; ++nt) {
+        const f32x4 qnv = sh.qv[16 * nt + (l & 15)];
+        float e = t.a[cg][nt][i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
+        t.a[cg][nt][i] = e;
+        s += fabsf(e);
+      }
+      s = sum16(s);
+      const float skc = fmaxf(sqrtf(s / (float)V_), LQ_EPS);      // kernels.py:2222
+      if ((l & 15) == 0) sh.sk[c] = skc;
     }
-    s = sum16(s);
-    const float skc = fmaxf(sqrtf(s / (float)V_), LQ_EPS);      // kernels.py:2222
-    if ((l & 15) == 0) sh.sk[16 * w + 4 * q + i] = skc;
-  }
   __syncthreads();
   // E / Sk and E / (Sk Sv) (kernels.py:2224-2229) as products with reciprocals taken once per column and once per row
-  // (12 divisions per lane instead of 64; within a few ulp of the quotients, below the codes' rounding step)
-  float rsk[4];
+  // (within a few ulp of the quotients, below the codes' rounding step)
+  float rsk[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) rsk[i] = 1.0f / sh.sk[16 * w + 4 * q + i];
+  for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rsk[cg][i] = 1.0f / sh.sk[32 * w + 16 * cg + 4 * q + i];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] * rsk[i]));   // kernels.py:2224-2227
+    for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[cg][nt][i] * rsk[cg][i]));   // kernels.py:2224-2227
     m = xor32_max(xor16_max(m));
     if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
   }
@@ -843,19 +921,24 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
-    const float svv = fmaxf(max_parts(sh.rowmax, v), LQ_EPS);
-    const float rsv = qmax / svv;
-    uint32_t word = 0;
+    float rm = sh.rowmax[0][v];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float x = (t.a[nt][i] * rsk[i]) * rsv;            // kernels.py:2229
-      const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
-      word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
+    for (int w2 = 1; w2 < QW; ++w2) rm = fmaxf(rm, sh.rowmax[w2][v]);
+    const float svv = fmaxf(rm, LQ_EPS);
+    const float rsv = qmax / svv;
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg) {
+      uint32_t word = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float x = (t.a[cg][nt][i] * rsk[cg][i]) * rsv;     // kernels.py:2229
+        const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
+        word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
+      }
+      const int c = 32 * w + 16 * cg + 4 * q;
+      if ((V_ == VD || v < V_) && (K_ == KD || c < K_)) *(uint32_t*)(Sq + v * K_ + c) = word;
     }
-    if (V_ == VD || v < V_) {
-      if (K_ == KD || 16 * w + 4 * q < K_) *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = word;
-      if (w == 0 && q == 0) Sv[v] = svv;
-    }
+    if ((V_ == VD || v < V_) && w == 0 && q == 0) Sv[v] = svv;
   }
   if (tid < KD) {
     if (K_ == KD || tid < K_) {
@@ -871,7 +954,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   if (KDA) {
     if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
     uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
-    for (int i = tid; i < L * KD / 8; i += FT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+    for (int i = tid; i < L * KD / 8; i += QT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
   }
   if (tid == 0) {
     if (!KDA) st.Pbuf[sh_] = 1.f;
@@ -1083,10 +1166,16 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
 // ------------------------------------------------------------------------------------------------------------------
 // low-rank factoriser (kernels.py:2246-2314): x [n][K][V]; P = MGS(x Q), Q = MGS(x^T P) x iters; U = x Q
 // ------------------------------------------------------------------------------------------------------------------
+struct LowrankShared {           // the eight-wave layout's subspace vectors and per-wave row partial sums
+  f32x4 qv[VD];
+  f32x4 pp[KD];
+  f32x4 qpart[NW][VD];
+};
+
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void lowrank_kernel(const float* __restrict__ x, const float* __restrict__ Q0, float* __restrict__ U,
                     float* __restrict__ Qo, int R, int iters) {
-  __shared__ QuantShared sh;
+  __shared__ LowrankShared sh;
   const int b = blockIdx.x;
   const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
   const float* X = x + (long long)b * KD * VD;
@@ -1185,9 +1274,9 @@ extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, 
   if (N == 0) return LQ_OK;
   const dim3 g((unsigned)(N * st->HV));
   hipStream_t s = (hipStream_t)stream;
-  if (st->K == KD) quantize_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
-  else if (st->V == VD) quantize_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
-  else quantize_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  if (st->K == KD) quantize_kernel<false><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else if (st->V == VD) quantize_kernel<false, 64, 128><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else quantize_kernel<false, 64, 64><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
@@ -1196,7 +1285,7 @@ extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int*
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  quantize_kernel<true><<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax, 3);
+  quantize_kernel<true><<<dim3((unsigned)(N * st->HV)), QT, 0, (hipStream_t)stream>>>(*st, Q0, idx, qmax, 3);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
