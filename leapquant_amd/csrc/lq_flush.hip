@@ -367,12 +367,6 @@ __device__ __forceinline__ f32x4 sum_parts(const f32x4 (*part)[VD], int v) {
   for (int w = 1; w < NW; ++w) s += part[w][v];
   return s;
 }
-__device__ __forceinline__ float max_parts(const float (*part)[VD], int v) {
-  float m = part[0][v];
-#pragma unroll
-  for (int w = 1; w < NW; ++w) m = fmaxf(m, part[w][v]);
-  return m;
-}
 
 // ------------------------------------------------------------------------------------------------------------------
 // flush (kernels.py:1077-2033): one due (slot, head)
