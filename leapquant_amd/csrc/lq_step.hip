@@ -253,8 +253,10 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   // Every wave holds its bulk loads until its own small loads are back.  Under load the memory system serves requests
   // roughly in arrival order, chip-wide: a small load issued after the first bulk loads waits behind them (several
   // us), and the scalar work of the CU's later workgroups, hence their bulk issue, with it.  Waiting here keeps the
-  // small loads of the four workgroups of a CU ahead of the bulk traffic (measured 16.09 -> 15.98 us at config 1).
-  if (!CONV) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  // small loads of the four workgroups of a CU ahead of the bulk traffic (measured 16.09 -> 15.98 us at config 1, GQA
+  // 2; GQA 1, four workgroups of two waves per CU as well: 19.85 -> 19.28 us with the plain window loads below).  At GQA
+  // 4 two workgroups of eight waves share a CU and the wait measured slower (16.27 -> 16.49 us): not used there.
+  if (!CONV && G <= 2) asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   int h = hg[0], hmax = hg[0];
 #pragma unroll
   for (int g2 = 1; g2 < G; ++g2) {
