@@ -142,12 +142,20 @@ def kda_bench(torch, dev, stream, capture):
             fl_ms.append(event_ms(torch, stream, gfl[kk].replay, 1))
     step_us = sum(st_ms[1:]) / len(st_ms[1:]) * 1e3 / CH
     flush_us = sum(fl_ms[NSET:]) / len(fl_ms[NSET:]) * 1e3
+    # the KDA prefill round trip of one slot set (B x HV heads): dequant (fp32 state with the decayed window) and the
+    # checkpoint (three subspace rounds, residual codes, window reset)
+    rt_d, rt_q = [], []
+    for r in range(3):
+        rt_d.append(event_ms(torch, stream, lambda: lq.dequantize(ssm, sets[0]), 1))
+        rt_q.append(event_ms(torch, stream, lambda: lq.quantize(ssm, sets[0]), 1))
     bytes_step = sum(kda_step_bytes(B, HV, K, V, R, h) for h in range(L)) / L
     res = {"workload": "KDA decode, BASELINE config 2: B=128, HV=H=32, d=128, W=64, R=4, int8 state, %d rotated slot "
                        "sets" % NSET,
            "decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
            "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1), "step_bytes_per_launch": int(bytes_step),
-           "flush_due_us": round(flush_us, 2)}
+           "flush_due_us": round(flush_us, 2),
+           "prefill_dequant_us": round(sum(rt_d[1:]) / 2 * 1e3, 1),
+           "prefill_checkpoint_us": round(sum(rt_q[1:]) / 2 * 1e3, 1)}
     del gdec, gst, gfl, lq, ssm
     torch.cuda.empty_cache()
     return res
@@ -262,6 +270,17 @@ def flush_quantize_bench(torch, dev, stream):
             torch.cuda.synchronize()
             ts.append(event_ms(torch, stream, qrun, 1))
         q_us = sum(ts[1:]) / 2 * 1e3
+        if tag == "int8":
+            # the prefill dequant of the same heads (window empty after the quantize): 19 KiB in, 64 KiB out per head;
+            # then the checkpoints again for the flush below
+            td = []
+            for r in range(3):
+                torch.cuda.synchronize()
+                td.append(event_ms(torch, stream, lambda: lq.dequantize(ssm, slots), 1))
+                ssm.copy_(S0)
+                qrun()
+            res["dequant_int8_us"] = round(sum(td[1:]) / 2 * 1e3, 1)
+            res["dequant_int8_gbps"] = round(quantize_bytes(nheads, K, V) / (res["dequant_int8_us"] * 1e-6) / 1e9, 1)
         # a full window on every head: unit keys, values, gate products of U(-0.1, 0) log-gates
         lq.Kbuf.copy_(torch.nn.functional.normalize(torch.randn(lq.Kbuf.shape, device=dev, generator=g), dim=-1))
         lq.Ubuf.normal_(0.0, 0.02, generator=g)
