@@ -8,12 +8,16 @@ g ~ U(-0.1, 0), beta = sigmoid(N(0,1)); states N(0, 0.02^2) quantised once), res
 Measurement:
   * `value` = amortised microseconds per decode call (step + flush, flushes included), from HIP events around graph
     replays of the decode loop.  The loop rotates NSET disjoint slot sets (> 1 GB of state) so the 256 MB MALL
-    cannot hold the working set between uses of a set.
+    cannot hold the working set between uses of a set, and times whole rotations (every set's windows from empty
+    through the all-due flush): --steps / --warmup are rounded up to rotations of 64 * NSET calls, and `steps` /
+    `warmup` report the calls actually run.  `achieved_gbps` divides the algorithmic bytes of those calls by their time.
+  * `cpu_baseline`: the numpy oracle on config 0, its independent heads split over the host's cores (forked before the
+    GPU is touched).
   * roofline of the dominant kernel (the step): algorithmic bytes per launch (layout-independent minimum) over the
     average launch duration, from HIP events around graph replays of step launches that rotate the same slot sets
     (every window runs h = 0..63); traffic = the HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters
     read for this same command, calibrated on the 64 MiB copies it ends with.
-  * the same step on a dense bf16 state (`lq_dense_step`) as the baseline, and the CPU oracle on config 0.
+  * the same step on a dense bf16 state (`lq_dense_step`) as the baseline.
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 128] [--no-cpu]
 """
 import argparse
@@ -372,33 +376,77 @@ def traffic_bytes():
         return json.load(f).get("hbm_bytes_per_launch")
 
 
-def cpu_baseline(max_seconds=20.0):
-    """The CPU oracle (numpy, one thread) on config 0: GDN B=1, HV=H=16, d=128, W=64, R=4; steps until ~max_seconds
-    or 256 steps."""
+def _cpu_worker(heads, seed, calls, barrier, out):
+    """One host process of the CPU baseline: `calls` decode calls (step + flush) of config 0 on its own `heads` value
+    heads (GQA 1: each with its own key head), timed between a barrier shared by all workers and its last call."""
     import numpy as np
     from threadpoolctl import threadpool_limits
     from oracle import lq_oracle as O
     from tests.fixtures import gate_params, make_inputs, make_state
-    rng = np.random.default_rng(1000)
-    NS, HV, H, L = 2, 16, 16, 64
     with threadpool_limits(limits=1):
-        st, S, Q0 = make_state(rng, NS, HV, H, L=L)
-        A_log, dt_bias = gate_params(HV)
+        rng = np.random.default_rng(seed)
+        st, S, Q0 = make_state(rng, 2, heads, heads, L=64)
+        A_log, dt_bias = gate_params(heads)
         idx = np.array([1])
-        pool = [make_inputs(rng, 1, HV, H) for _ in range(8)]
+        pool = [make_inputs(rng, 1, heads, heads) for _ in range(8)]
+        barrier.wait()
         t0 = time.perf_counter()
-        n = 0
-        while n < 256:
+        for n in range(calls):
             mixed, a, b = pool[n % 8]
             O.gdn_step(st, mixed, a, b, A_log, dt_bias, idx)
             O.flush(st, Q0, idx)
-            n += 1
-            if time.perf_counter() - t0 > max_seconds and n % 64 == 0:
-                break
-        dt = time.perf_counter() - t0
-    return dict(value=round(dt / n * 1e6, 1), unit="us/step", cores=1, kind="port",
-                sample="config 0 (GDN B=1, HV=H=16, d=128, W=64, R=4): %d decode steps incl. %d flushes, numpy oracle, "
-                       "1 thread" % (n, n // 64))
+        out.put((t0, time.perf_counter()))
+
+
+def cpu_baseline(target_seconds=10.0):
+    """The CPU oracle (numpy) on config 0: GDN B = 1, HV = H = 16, d = 128, W = 64, R = 4, decode calls of step + flush,
+    on the host's cores: the 16 heads are independent (GQA 1), so they are split over one process per core (at most
+    16, the box's share, and one per head).  Runs before anything touches the GPU (the workers are forked).  The call
+    count is a multiple of 256 (four windows: every head flushes once per 64 calls) sized to ~target_seconds of wall
+    time from a one-process calibration.  Returns the wall time per decode call of the whole batch."""
+    import multiprocessing as mp
+    import numpy as np
+    from oracle import lq_oracle as O
+    from tests.fixtures import gate_params, make_inputs, make_state
+    HV = 16
+    try:
+        ncpu = len(os.sched_getaffinity(0))
+    except AttributeError:
+        ncpu = os.cpu_count() or 1
+    P = max(1, min(ncpu, 16, HV))
+    split = [HV // P + (1 if i < HV % P else 0) for i in range(P)]
+    # calibration: 64 calls of the largest worker's share, one process
+    rng = np.random.default_rng(999)
+    st, S, Q0 = make_state(rng, 2, max(split), max(split), L=64)
+    A_log, dt_bias = gate_params(max(split))
+    mixed, a, b = make_inputs(rng, 1, max(split), max(split))
+    t0 = time.perf_counter()
+    for _ in range(64):
+        O.gdn_step(st, mixed, a, b, A_log, dt_bias, np.array([1]))
+        O.flush(st, Q0, np.array([1]))
+    per_call = (time.perf_counter() - t0) / 64
+    calls = 256 * max(1, min(64, int(target_seconds / (256 * per_call))))
+    ctx = mp.get_context("fork")
+    barrier = ctx.Barrier(P)
+    out = ctx.Queue()
+    procs = [ctx.Process(target=_cpu_worker, args=(split[i], 1000 + i, calls, barrier, out)) for i in range(P)]
+    for p in procs:
+        p.start()
+    spans = [out.get() for _ in procs]
+    for p in procs:
+        p.join()
+    if any(p.exitcode != 0 for p in procs):
+        raise RuntimeError("a CPU baseline worker failed")
+    wall = max(t1 for _, t1 in spans) - min(t0 for t0, _ in spans)
+    us = wall / calls * 1e6
+    nbytes = (sum(step_bytes(1, HV, HV, 128, 128, 4, h) for h in range(64)) / 64
+              + flush_bytes(1, HV, HV, 128, 128, 4, 64) / 64)
+    return dict(value=round(us, 1), unit="us/step", cores=P, kind="port",
+                gbps=round(nbytes / (us * 1e-6) / 1e9, 3), host_cpus=ncpu,
+                sample="config 0 (GDN B=1, HV=H=16, d=128, W=64, R=4): %d decode calls (step + flush, %d flushes) of "
+                       "the numpy oracle, its 16 independent heads split over %d host processes (%s heads each), one "
+                       "BLAS thread per process; wall time per call" % (calls, calls // 64, P,
+                                                                       "/".join(str(x) for x in sorted(set(split)))))
 
 
 def main():
@@ -417,6 +465,10 @@ def main():
         print("--sets must divide 64 (each graph of 64 launches gives every set the same number of steps)",
               file=sys.stderr)
         sys.exit(2)
+    cpu = None
+    if not args.no_cpu:                        # host processes are forked before anything touches the GPU
+        cpu = cpu_baseline()
+        progress("CPU baseline: %.1f us per call on %d processes" % (cpu["value"], cpu["cores"]))
 
     import torch
     from leapquant_amd import kernels as KN
@@ -482,30 +534,36 @@ def main():
         return gr
 
     # ---- main loop: decode (step + flush) in graphs of 64 calls ----
+    # The graph's call i uses set i % NSET and input i % P.  A rotation is NSET replays (L * NSET calls): every set's
+    # windows go from empty through the full-window flush back to empty, so a timed region of whole rotations holds
+    # each window fill h = 0..63 and each flush in its real proportion, whatever --steps is (rounded up to rotations).
     CH = 64
-    # the graph's call i uses set i % NSET and input i % P; it is replayed as a block, so the rotation repeats
+    ROT = L * NSET
     gdec = capture(decode, CH)
-    rem = args.steps % CH
-    grem = capture(decode, rem) if rem else None
     torch.cuda.synchronize()                                      # capturing executes nothing
-    nw = -(-args.warmup // CH)
-    for _ in range(nw):
+    warm_rot = max(1, -(-args.warmup // ROT))
+    timed_rot = max(1, -(-args.steps // ROT))
+    for _ in range(warm_rot * NSET):
         gdec.replay()
     torch.cuda.synchronize()
+    assert int(lq.hcnt[1:].max()) == 0                           # every window back at the start of a rotation
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
         e0.record(stream)
-        for _ in range(args.steps // CH):
+        for _ in range(timed_rot * NSET):
             gdec.replay()
-        if grem is not None:
-            grem.replay()
         e1.record(stream)
     e1.synchronize()
     torch.cuda.synchronize()
     ms_total = e0.elapsed_time(e1)
-    us_per_step = ms_total * 1e3 / args.steps
+    calls = timed_rot * ROT
+    us_per_step = ms_total * 1e3 / calls
+    # bytes of exactly those calls: per set and window, the 64 steps at fills 0..63 and one all-due flush
+    timed_bytes = timed_rot * NSET * (sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L))
+                                      + flush_bytes(B, HV, H, K, V, R, L))
 
-    progress("decode loop: %.3f us per call" % us_per_step)
+    progress("decode loop: %.3f us per call over %d calls (%d whole rotations of %d sets)"
+             % (us_per_step, calls, timed_rot, NSET))
     # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
     # of the NSET sets 64 / NSET steps; NSET replays take every window from h = 0 to h = 64, then every head is due) ----
     lq.quantize(ssm, all_slots)                                   # every window back to h = 0
@@ -537,11 +595,10 @@ def main():
     bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(CH)) / CH      # mean over h = 0..63
     bytes_flush = flush_bytes(B, HV, H, K, V, R, L)
     achieved = bytes_step / (step_us * 1e-6) / 1e9
-    amort_bytes = bytes_step + bytes_flush / L
 
     progress("step %.3f us, flush due %.1f us, idle %.2f us" % (step_us, flush_due_us, flush_idle_us))
     # ---- bf16-state baseline (same step on a dense bf16 state), rotated sets ----
-    del gsteps, gflush, gidle, gdec, grem
+    del gsteps, gflush, gidle, gdec
     Sd = torch.empty(NS, HV, V, K, device=dev, dtype=torch.bfloat16)
     Sd.normal_(0.0, 0.02, generator=g)
 
@@ -627,13 +684,17 @@ def main():
     progress("head-dim variants")
 
     res = {
-        "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": args.steps,
-        "warmup": nw * CH, "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
+        "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": calls,
+        "warmup": warm_rot * ROT, "steps_requested": args.steps, "warmup_requested": args.warmup,
+        "steps_note": "decode calls timed: --steps rounded up to whole rotations of %d calls (every set's window "
+                      "from empty through its flush), so flushes are timed in their real proportion" % ROT,
+        "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "GDN decode, BASELINE config 1: B=64, HV=32 value / H=16 key heads, d=128, W=64, R=4, "
-                               "int8 state + fp32 scales, step + flush per call, %d rotated slot sets" % NSET,
+                               "int8 state + fp32 scales, step + flush per call (the flush does work on one call in "
+                               "64), whole windows of %d rotated slot sets" % NSET,
                    "batch": B, "value_heads": HV, "key_heads": H, "head_dim": K, "window": L, "rank": R},
-        "achieved_gbps": round(amort_bytes / (us_per_step * 1e-6) / 1e9, 1),
+        "achieved_gbps": round(timed_bytes / (ms_total * 1e-3) / 1e9, 1),
         "step_us": round(step_us, 3), "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
         "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
         "speedup_vs_bf16_step": round(bf16_us / step_us, 3),
@@ -649,8 +710,8 @@ def main():
     res["kda_config2"] = kda
     res["flush_quantize_config3"] = fq
     res["head_dims_W16"] = hd
-    if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline()
+    if cpu is not None:
+        res["cpu_baseline"] = cpu
     print(json.dumps(res))
 
 

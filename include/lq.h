@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 2
+#define LQ_ABI_VERSION 3
 
 enum lq_status {
   LQ_OK = 0,
@@ -46,10 +46,12 @@ typedef struct lq_state {
   int* hcnt;              /* [NS][HV] */
   int NS, HV, H, K, V, L, R;
   int* ctl;               /* optional (NULL: unused): int[2] = {due flag: nonzero when a step has filled some head's
-                             window since the last flush, flush workgroups done}, zero-initialised by the owner and
-                             kept by the kernels.  With it, a flush that reads a clear flag returns at once instead of
-                             scanning hcnt; the last flush workgroup clears both.  Without it, the flush scans hcnt
-                             (the contract). */
+                             window (or met a full one) since the last flush, flush workgroups done}, zero-initialised
+                             by the owner and kept by the kernels.  With it, a flush that reads a clear flag returns at
+                             once instead of scanning hcnt; the last flush workgroup clears both.  Without it, the
+                             flush scans hcnt (the contract). */
+  float qmax;             /* code range of the stored checkpoint: 127 (INT8) or 31 (6-bit codes in the int8
+                             container); 0 means 127.  The decode steps dequantise with it (Sq Sk Sv / qmax). */
 } lq_state;
 
 /* Decode inputs of one call: N rows, one token each. */
@@ -77,6 +79,8 @@ typedef struct lq_conv {
   long long slot_stride, ch_stride, tap_stride;   /* in elements */
   int W;                  /* taps: 4 */
   int silu;               /* 1: SiLU after the bias; 0: none */
+  int NS;                 /* slots of the conv state: a row whose slot is >= NS (or >= the state's NS) is a padding
+                             row, so no tap is read or written outside the conv-state tensor */
 } lq_conv;
 
 int lq_abi_version(void);

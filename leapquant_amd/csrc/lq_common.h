@@ -182,6 +182,9 @@ __device__ __forceinline__ void mark_due(int* ctl) {
     __hip_atomic_fetch_or(ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// code range of the stored checkpoint (lq_state.qmax; 0: INT8)
+__device__ __forceinline__ float code_range(const lq_state& st) { return st.qmax > 0.f ? st.qmax : LQ_QMAX; }
+
 // ---- state-block addressing (state.py:29-40) ----------------------------------------------------------------------
 __device__ __forceinline__ char* block_base(const lq_state& st, int slot, int hv) {
   return (char*)st.ssm + 4ll * ((long long)slot * st.slot_stride + (long long)hv * st.V * st.K);

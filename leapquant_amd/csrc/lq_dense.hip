@@ -115,7 +115,7 @@ __global__ __launch_bounds__(256) void conv_update_kernel(lq_conv cv, const bf16
   const int n = blockIdx.y;
   const int c = blockIdx.x * 256 + threadIdx.x;
   const int slot = idx[n];
-  if (c >= C || slot <= 0 || slot >= NS) return;
+  if (c >= C || slot <= 0 || slot >= NS || slot >= cv.NS) return;
   const long long sb = (long long)slot * cv.slot_stride;
   const ConvTaps t = conv_taps(cv, x + (long long)n * C, sb, c);
   out[(long long)n * C + c] = f2bf(conv_out(t, cv.silu));
@@ -144,7 +144,8 @@ extern "C" int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, in
 
 extern "C" int lq_conv_update(const lq_conv* cv, const void* x, void* out, const int* idx, int N, int C, int NS,
                               void* stream) {
-  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || N < 0 || C <= 0 || NS <= 0)
+  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || N < 0 || C <= 0 || NS <= 0
+      || cv->NS <= 0)
     return LQ_ERR_ARG;
   if (cv->ch_stride <= 0 || cv->tap_stride <= 0 || (C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride)
     return LQ_ERR_ARG;

@@ -106,7 +106,8 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
 
   const int slot = io.idx[n];
-  if (slot <= 0 || slot >= st.NS) {   // padding row (kernels.py:374-378); a slot outside the cache counts as one
+  // padding row (kernels.py:374-378); a slot outside the cache (or, fused conv, outside the conv state) counts as one
+  if (slot <= 0 || slot >= st.NS || (CONV && slot >= cv.NS)) {
     out[lt] = 0;
     return;
   }
@@ -196,7 +197,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
     const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
     const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
     const float kappa = nkq * inq * ink;
-    const float inv = 1.0f / LQ_QMAX;
+    const float inv = 1.0f / code_range(st);   // codes Sq dequantise as Sq Sk Sv / qmax (kernels.py:255-256)
     float kn[NE], qn[NE], kf[NE], qf[NE];
     float kmax = 0.f, qmax = 0.f;
 #pragma unroll
@@ -381,7 +382,11 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   // this wave's u_j rows have landed in LDS (they precede the keys and the tile in the counter) ...
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
   __syncthreads();              // ... and the other wave's, with the key and factor dots of every wave
-  if (!live) { out[lt] = 0; return; }
+  if (!live) {                  // a full window (a flush that did not cover this row): zero output, nothing written;
+    if (lt == 0) mark_due(st.ctl);   // flag it again so that the flush after this step takes it
+    out[lt] = 0;
+    return;
+  }
 
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
   const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
@@ -568,7 +573,11 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   const float sv = Svp[lt];
   __builtin_amdgcn_sched_barrier(0);
   const int h = hfill;
-  if (h >= L) { out[lt] = 0; return; }    // a full window is never stepped (the flush follows every step)
+  if (h >= L) {                 // a full window is never stepped: zero output, and the head is flagged again so that
+    if (lt == 0) mark_due(st.ctl);   // the flush after this step takes it
+    out[lt] = 0;
+    return;
+  }
   // the four factor rows (2 KiB, inside the checkpoint block whatever R) to LDS, one KiB per wave
   lds_load16((const char*)UQp + 1024 * wi + 16 * lane, (char*)&sh.uq[2 * wi][0]);
   // The window's live entries j < h split between the waves: wave 0 takes [0, h0), wave 1 [h0, h), h0 a multiple of 4
@@ -631,7 +640,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
     const float inq = rsqrtf_rn(nq + (float)LQ_NORM_EPS) * io.scale;
     const float ink = rsqrtf_rn(nk + (float)LQ_NORM_EPS);
     const float kappa = nkq * inq * ink;
-    const float inv = 1.0f / LQ_QMAX;
+    const float inv = 1.0f / code_range(st);   // kernels.py:900-901
     float kn[2], qn[2], kf[2], qf[2];
     float kmax = 0.f, qmax = 0.f;
 #pragma unroll
@@ -827,6 +836,7 @@ static int check_step(const lq_state* st, const lq_step_io* io) {
   // 16-byte loads of the int8 rows and of the scale / factor block need a 16-byte aligned block start
   if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3) || ((uintptr_t)st->ssm & 15))
     return LQ_ERR_ARG;
+  if (!(st->qmax == 0.f || (st->qmax >= 1.f && st->qmax <= 127.f))) return LQ_ERR_ARG;
   if (io->N > 0 && (!io->mixed || !io->a || !io->b || !io->A_log || !io->dt_bias || !io->idx || !io->out))
     return LQ_ERR_ARG;
   return LQ_OK;
@@ -862,7 +872,8 @@ extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* strea
 extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
   int rc = check_step(st, io);
   if (rc) return rc;
-  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1)) return LQ_ERR_ARG;
+  if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || cv->NS <= 0)
+    return LQ_ERR_ARG;
   const long long C = 2ll * st->H * st->K + (long long)st->HV * st->V;
   if (cv->ch_stride <= 0 || cv->tap_stride <= 0 || cv->slot_stride <= 0) return LQ_ERR_ARG;
   // the state taps of a slot must stay inside its slot_stride elements

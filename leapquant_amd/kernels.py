@@ -11,10 +11,11 @@ Deliberate differences (documented in the package's design notes):
   * The NVIDIA schedule knobs (SMS, NSTAGE, NSTAGEQ, NCG, NNW, MAXIT, PAD, MMT, NTP, RSG, threads, BV) are accepted
     and ignored: the HIP kernels have one schedule for gfx950.
   * The window may be up to 64 entries (the reference's kernels stop at 16 / 32).
-  * make_flush / make_quantize / make_dequant take a code range `qmax` (127: INT8, default; 31: 6-bit codes in the
-    same int8 container).
+  * make_gdn_step / make_kda_step / make_flush / make_quantize / make_dequant take a code range `qmax` (127: INT8,
+    default; 31: 6-bit codes in the same int8 container).
 """
 import ctypes
+import functools
 
 import torch
 
@@ -64,14 +65,21 @@ def _check_dims(K, V, L, R, kda=False):
     assert V * K // 4 + K + V + R * (K + V) // 2 <= V * K, "checkpoint must fit inside the fp32 slot"
 
 
-def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, ctl=None):
+def _check_qmax(qmax):
+    if not 1.0 <= float(qmax) <= 127.0:
+        raise ValueError("qmax: code range in [1, 127] expected (127: INT8, 31: 6-bit), got %r" % (qmax,))
+    return float(qmax)
+
+
+def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, ctl=None, qmax=QMAX):
     """lq_state of a layer: `Sq` is any view whose data pointer is the checkpoint of (slot 0, head 0), i.e. the fp32
-    cache's data pointer.  `ctl`: optional int32 [2] due flag + flush counter kept by the kernels (None: the flush scans hcnt)."""
+    cache's data pointer.  `ctl`: optional int32 [2] due flag + flush counter kept by the kernels (None: the flush scans
+    hcnt).  `qmax`: code range of the stored checkpoint (the decode steps dequantise Sq Sk Sv / qmax)."""
     if ctl is not None and (ctl.dtype != torch.int32 or ctl.numel() < 2):
         raise ValueError("ctl: int32 [2] expected")
     return _lib.LqState(_dev(Sq), SS, _dev(Kbuf), _dev(Ubuf), _dev(Wbuf), _dev(Pbuf),
                         _dev(Gbuf) if Gbuf is not None else 0, _dev(hcnt), NS, HV, H, K, V, L, R,
-                        _dev(ctl) if ctl is not None else 0)
+                        _dev(ctl) if ctl is not None else 0, _check_qmax(qmax))
 
 
 def _check_view(Sq, NS, HV, V, K, SS):
@@ -101,10 +109,13 @@ def _check_step_inputs(N, HV, H, K, V, mixed, a, b, A_log, dt_bias, idx, o, KA):
         raise ValueError("o: bf16 contiguous [N, HV, V] expected")
 
 
-def make_gdn_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=None, NCG=None, NNW=None, scale=None, MAXIT=256):
+def make_gdn_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=None, NCG=None, NNW=None, scale=None, MAXIT=256,
+                  qmax=QMAX):
     """Gated DeltaNet decode step on the 8-bit state (kernels.py:27-692).  Returns
-    step(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o)."""
+    step(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o).  `qmax`: the code range
+    of the stored checkpoint (127: INT8, 31: 6-bit)."""
     _check_dims(K, V, L, R)
+    qmax = _check_qmax(qmax)
     assert HV % H == 0 and HV // H in (1, 2, 4), "liblq: HV / H in {1, 2, 4}"
     scale = K ** -0.5 if scale is None else scale
     L_ = _lib.lib()
@@ -118,7 +129,7 @@ def make_gdn_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=None, NCG=None, 
         _need(Pbuf, torch.float32, (NS, HV, 1), "Pbuf")
         _need(hcnt, torch.int32, (NS, HV), "hcnt")
         _check_step_inputs(N, HV, H, K, V, mixed, a, b, A_log, dt_bias, idx, o, 1)
-        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, None, hcnt, NS, HV, H, K, V, L, R)
+        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, None, hcnt, NS, HV, H, K, V, L, R, qmax=qmax)
         io = _step_io(mixed, a, b, A_log, dt_bias, idx, o, scale)
         _lib.check(L_.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), _stream(mixed)), "lq_gdn_step")
 
@@ -126,10 +137,12 @@ def make_gdn_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=None, NCG=None, 
 
 
 def make_kda_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=6, NSTAGEQ=4, NCG=2, NNW=2, scale=128 ** -0.5,
-                  MAXIT=256, GLB=0.0):
+                  MAXIT=256, GLB=0.0, qmax=QMAX):
     """Kimi Delta Attention decode step (kernels.py:694-1075), per-key-channel gate; GLB != 0 selects GLM's bounded
-    gate.  Returns step(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o)."""
+    gate.  Returns step(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o).
+    `qmax`: the code range of the stored checkpoint (127: INT8, 31: 6-bit)."""
     _check_dims(K, V, L, R, kda=True)
+    qmax = _check_qmax(qmax)
     assert HV % H == 0, "liblq: HV % H == 0"
     L_ = _lib.lib()
     glb = float(GLB)
@@ -145,7 +158,7 @@ def make_kda_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=6, NSTAGEQ=4, NC
             raise ValueError("Gbuf: 16-bit [NS, HV, L, K] expected")
         _need(hcnt, torch.int32, (NS, HV), "hcnt")
         _check_step_inputs(N, HV, H, K, V, mixed, a, b, A_log, dt_bias, idx, o, K)
-        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R)
+        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, qmax=qmax)
         io = _step_io(mixed, a, b, A_log, dt_bias, idx, o, scale)
         _lib.check(L_.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(glb), _stream(mixed)),
                    "lq_kda_step")
@@ -242,28 +255,29 @@ def make_lowrank(K, V, R, ITERS, threads=128):
     return lowrank
 
 
-_LOWRANK = {}
-_Q0_LR = {}
+@functools.lru_cache(maxsize=None)
+def _lowrank_start(device, V, r):
+    """The factoriser's fixed start, randn(V, r) from a CPU generator seeded 0 (kernels.py:2318-2331), on `device`."""
+    return torch.randn(V, r, generator=torch.Generator().manual_seed(0)).to(device)
+
+
+_lowrank_kernel = functools.lru_cache(maxsize=None)(make_lowrank)
 
 
 def lowrank_factor(x, r, iters=3):
-    """x: [..., K, V] fp32 on the GPU -> U [..., K, r], Q [..., V, r] (kernels.py:2321-2331)."""
+    """Rank-r factors of x [..., K, V] (fp32, on the GPU): U [..., K, r], Q [..., V, r] with x ~ U Q^T, from `iters`
+    rounds of subspace iteration with MGS (kernels.py:2321-2331)."""
     *lead, K, V = x.shape
-    key = (str(x.device), V, r)
-    if key not in _Q0_LR:
-        _Q0_LR[key] = torch.randn(V, r, generator=torch.Generator().manual_seed(0)).to(x.device)
-    fk = (K, V, r, iters)
-    if fk not in _LOWRANK:
-        _LOWRANK[fk] = make_lowrank(K, V, r, iters)
-    xf = x.reshape(-1, K, V).contiguous().float()
-    U = torch.empty(xf.shape[0], K, r, device=x.device, dtype=torch.float32)
-    Q = torch.empty(xf.shape[0], V, r, device=x.device, dtype=torch.float32)
-    _LOWRANK[fk](xf, _Q0_LR[key], U, Q)
-    return U.reshape(*lead, K, r), Q.reshape(*lead, V, r)
+    xs = x.reshape(-1, K, V).float().contiguous()
+    U = xs.new_empty(xs.shape[0], K, r)
+    Q = xs.new_empty(xs.shape[0], V, r)
+    _lowrank_kernel(K, V, r, iters)(xs, _lowrank_start(x.device, V, r), U, Q)
+    return U.view(*lead, K, r), Q.view(*lead, V, r)
 
 
 def conv_struct(conv_state, weight, bias=None, silu=True):
-    """lq_conv of a conv state [NS, C, W - 1] view (any strides), bf16 weights [C, 4] and optional bf16 bias [C]."""
+    """lq_conv of a conv state [NS, C, W - 1] view (any strides), bf16 weights [C, 4] and optional bf16 bias [C]; the
+    kernels treat a row whose slot is not below the conv state's NS as a padding row."""
     C = weight.shape[0]
     w = weight.reshape(C, -1)
     if conv_state.dtype != torch.bfloat16 or conv_state.dim() != 3 or conv_state.shape[1:] != (C, 3):
@@ -273,7 +287,7 @@ def conv_struct(conv_state, weight, bias=None, silu=True):
     if bias is not None and (bias.dtype != torch.bfloat16 or bias.numel() != C or not bias.is_contiguous()):
         raise ValueError("conv bias: bf16 [C] expected")
     return _lib.LqConv(_dev(conv_state), _dev(w), _dev(bias) if bias is not None else 0, conv_state.stride(0),
-                       conv_state.stride(1), conv_state.stride(2), 4, 1 if silu else 0)
+                       conv_state.stride(1), conv_state.stride(2), 4, 1 if silu else 0, conv_state.shape[0])
 
 
 def conv_update(x, conv_state, weight, bias, idx, out, silu=True):

@@ -6,6 +6,7 @@ Layout of one (slot, head) inside the fp32 [V, K] state slot (state.py:1-6, 29-4
 The window buffer (keys, values, weights of the tokens since the last flush) and the per-slot counters are separate
 tensors; the keys are kept once per key head (Kbuf [NS, H, L, K]).
 """
+import collections
 import ctypes
 import functools
 
@@ -21,9 +22,13 @@ _make_dequant = functools.lru_cache(maxsize=None)(KN.make_dequant)
 _make_quantize = functools.lru_cache(maxsize=None)(KN.make_quantize)
 
 
+_CacheId = collections.namedtuple("_CacheId", "storage offset shape stride")
+
+
 def _ident(t):
-    """Same storage + same view -> same layer state."""
-    return (t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), tuple(t.stride()))
+    """Identity of a state-cache tensor: where its storage lives and which view of it the tensor is.  The engine
+    re-allocating its caches (after the profiling run) shows up as a new identity."""
+    return _CacheId(t.untyped_storage().data_ptr(), t.storage_offset(), tuple(t.shape), t.stride())
 
 
 def _alias(ssm, dtype, shape, stride, offset):
@@ -84,9 +89,9 @@ class LeapQuantState:
         self.Q0 = torch.randn(V, R, generator=torch.Generator().manual_seed(0)).to(dev)
 
         if kda:
-            self.kstep = KN.make_kda_step(NS, HV, H, K, V, L, SS, R=R, GLB=float(gate_lower_bound))
+            self.kstep = KN.make_kda_step(NS, HV, H, K, V, L, SS, R=R, GLB=float(gate_lower_bound), qmax=qmax)
         else:
-            self.kstep = KN.make_gdn_step(NS, HV, H, K, V, L, SS, R=R)
+            self.kstep = KN.make_gdn_step(NS, HV, H, K, V, L, SS, R=R, qmax=qmax)
         self.kflush = KN.make_flush(NS, HV, K, V, L, SS, R=R, ITERS=1, KDA=kda, NMAX=nmax, qmax=qmax)
         if not kda:                          # the KDA prefill round trip has its own entry points
             self.kdeq = _make_dequant(NS, HV, K, V, L, SS, buf_dtype=KN.BF16, R=R, qmax=qmax)
@@ -94,14 +99,18 @@ class LeapQuantState:
         self._lib = _lib.lib()
         self._vkey = None
         self._skey = None
-        self._f32 = {}
+        self._param_f32 = {}
 
-    def _p32(self, t):
-        """fp32 copy of a layer parameter, cached per tensor (several layers can share one state tensor)."""
-        c = self._f32.get(t.data_ptr())
-        if c is None:
-            c = self._f32[t.data_ptr()] = t.detach().to(torch.float32).contiguous()
-        return c
+    def _as_f32(self, t):
+        """A gate parameter (A_log, dt_bias) as the fp32 tensor the kernels read.  A parameter in another dtype is
+        converted once and the copy kept, keyed by the parameter's address and dtype (a state tensor may be shared by
+        layers that each bring their own parameters)."""
+        if t.dtype == torch.float32:
+            return t
+        key = (t.data_ptr(), t.dtype)
+        if key not in self._param_f32:
+            self._param_f32[key] = t.detach().float().contiguous()
+        return self._param_f32[key]
 
     def views(self, ssm):
         k = _ident(ssm)
@@ -117,17 +126,18 @@ class LeapQuantState:
                 raise ValueError("the fp32 state cache must be 16-byte aligned with a slot stride divisible by 4")
             self._st = KN.state_struct(ssm, self.SS, self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf,
                                        self.Gbuf if self.kda else None, self.hcnt, self.NS, self.HV, self.H, self.K,
-                                       self.V, self.L, self.R, ctl=self.ctl)
+                                       self.V, self.L, self.R, ctl=self.ctl, qmax=self.qmax)
             self._skey = k
         return self._st
 
     def decode(self, ssm, mixed, a, b, A_log, dt_bias, idx, out):
         """One decode token per row, then the end-of-window flush of the heads whose window became full.
         a: GDN (N, HV) | KDA (N, HV, K) raw gate;  dt_bias: GDN (HV,) | KDA (HV*K,)."""
-        A_log = A_log if A_log.dtype == torch.float32 else self._p32(A_log)
-        dt_bias = dt_bias if dt_bias.dtype == torch.float32 else self._p32(dt_bias)
+        A_log = self._as_f32(A_log)
+        dt_bias = self._as_f32(dt_bias)
         KA = self.K if self.kda else 1
         N = idx.shape[0]
+        self._check_gate(a, N, KA)
         a = a.reshape(N, self.HV, KA).contiguous()
         dt_bias = dt_bias.reshape(self.HV, KA).contiguous()
         A_log = A_log.reshape(self.HV).contiguous()
@@ -169,9 +179,10 @@ class LeapQuantState:
         if conv_bias is not None and (conv_bias.dtype != torch.bfloat16 or conv_bias.numel() != C
                                       or not conv_bias.is_contiguous()):
             raise ValueError("conv_bias: bf16 [C] expected")
-        A_log = A_log if A_log.dtype == torch.float32 else self._p32(A_log)
-        dt_bias = dt_bias if dt_bias.dtype == torch.float32 else self._p32(dt_bias)
+        A_log = self._as_f32(A_log)
+        dt_bias = self._as_f32(dt_bias)
         N = idx.shape[0]
+        self._check_gate(a, N, 1)
         a = a.reshape(N, self.HV).contiguous()
         dt_bias = dt_bias.reshape(self.HV).contiguous()
         A_log = A_log.reshape(self.HV).contiguous()
@@ -192,6 +203,12 @@ class LeapQuantState:
         _lib.check(L.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), stream), "lq_gdn_step_conv")
         _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 0, ctypes.c_float(self.qmax), stream),
                    "lq_flush")
+
+    def _check_gate(self, a, N, KA):
+        """The raw gate `a` is read as bf16, N x HV (GDN) or N x HV x K (KDA) values (kernels.py:86, 738)."""
+        if a.dtype != torch.bfloat16 or a.numel() != N * self.HV * KA:
+            raise ValueError("a: bf16 with N * HV%s = %d elements expected, got %s with %d"
+                             % (" * K" if KA > 1 else "", N * self.HV * KA, a.dtype, a.numel()))
 
     def flush(self, ssm, idx):
         """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due flag lets a
@@ -238,29 +255,42 @@ class LeapQuantState:
                     idx.to(torch.int32).contiguous())
 
 
-_STATES = {}
-_GEN = [0]
+_STATES = {}        # cache identity -> the LeapQuantState built for it
+_GEN = [0]          # generation of the engine's caches: bumped when they are re-allocated
+
+
+def _forget_states():
+    """The engine has re-allocated its caches: every state built for the old ones addresses freed memory."""
+    _GEN[0] += 1
+    _STATES.clear()
+    if torch.cuda.is_available():
+        torch.cuda.empty_cache()
+
+
+def _refuse_prefix_caching(layer):
+    """Each sequence's window buffer lives beside its state slot, which recurrent-state prefix caching would share."""
+    mode = getattr(getattr(layer, "cache_config", None), "mamba_cache_mode", "none")
+    if mode != "none":
+        raise RuntimeError("LeapQuant keeps each sequence's window buffer next to its state slot and does not support "
+                           "prefix caching of the recurrent state: run vLLM with --no-enable-prefix-caching")
 
 
 def get_state(layer, ssm, **kw):
-    """The LeapQuantState of `layer` for its current state tensor (rebuilt when the engine swaps the cache after
-    profiling)."""
-    st = layer.__dict__.get("_leapquant")
-    k = _ident(ssm)
-    if st is not None and st.key == k:
-        return st
-    if st is not None and st.gen == _GEN[0]:            # cache re-allocated: drop all buffers of the old one
-        _GEN[0] += 1
-        _STATES.clear()
-        if torch.cuda.is_available():
-            torch.cuda.empty_cache()
-    st = _STATES.get(k)
+    """The LeapQuantState of `layer` for its current state tensor `ssm`, built on first use.  When a layer presents a
+    different tensor than the one its state was built for in the current generation, the engine has swapped its caches
+    (it does so after profiling): all states are dropped and rebuilt on demand."""
+    key = _ident(ssm)
+    mine = layer.__dict__.get("_leapquant")
+    if mine is not None:
+        if mine.key == key:
+            return mine
+        if mine.gen == _GEN[0]:
+            _forget_states()
+    st = _STATES.get(key)
     if st is None:
-        cc = getattr(layer, "cache_config", None)
-        if cc is not None and getattr(cc, "mamba_cache_mode", "none") != "none":
-            raise RuntimeError("LeapQuant keeps each sequence's window buffer next to its state slot and does not support "
-                               "prefix caching of the recurrent state: run vLLM with --no-enable-prefix-caching")
-        st = _STATES[k] = LeapQuantState(ssm, **kw)
+        _refuse_prefix_caching(layer)
+        st = LeapQuantState(ssm, **kw)
         st.gen = _GEN[0]
+        _STATES[key] = st
     layer._leapquant = st
     return st

@@ -63,6 +63,18 @@ def _io(**kw):
 BAD_STATES = [dict(K=96), dict(V=64), dict(K=32, V=32), dict(L=0), dict(L=65), dict(R=0), dict(R=5), dict(H=0), dict(HV=3),
               dict(NS=0), dict(slot_stride=100), dict(slot_stride=4 * 128 * 128 + 1), dict(ssm=8), dict(ssm=None),
               dict(hcnt=None), dict(Wbuf=None)]
+BAD_STEP_STATES = [dict(qmax=0.5), dict(qmax=128.0), dict(qmax=-31.0), dict(qmax=float("nan"))]
+
+
+@pytest.mark.parametrize("bad", BAD_STEP_STATES)
+def test_steps_reject_a_bad_code_range(lib, bad):
+    """The decode steps dequantise with lq_state.qmax (0: INT8; else 1 <= qmax <= 127)."""
+    st, io = _state(**bad), _io()
+    z = ctypes.c_void_p(0)
+    assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == -1
+    assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == -1
+    for ok in (0.0, 31.0, 127.0):
+        assert lib.lq_gdn_step(ctypes.byref(_state(qmax=ok)), ctypes.byref(io), z) == 0
 
 
 @pytest.mark.parametrize("bad", BAD_STATES)
@@ -157,18 +169,19 @@ def test_other_argument_errors(lib):
 def _conv(**kw):
     from leapquant_amd import _lib
     C = 2 * 2 * 128 + 4 * 128
-    d = dict(state=16, weight=32, bias=None, slot_stride=3 * C, ch_stride=3, tap_stride=1, W=4, silu=1)
+    d = dict(state=16, weight=32, bias=None, slot_stride=3 * C, ch_stride=3, tap_stride=1, W=4, silu=1, NS=8)
     d.update(kw)
     return _lib.LqConv(**d)
 
 
 def test_fused_conv_entry_points_check_their_arguments(lib):
-    """lq_gdn_step_conv / lq_conv_update: width 4 only, state taps inside a slot, 8-byte aligned weights, null pointers."""
+    """lq_gdn_step_conv / lq_conv_update: width 4 only, state taps inside a slot, 8-byte aligned weights, null pointers,
+    a conv-state slot count."""
     z = ctypes.c_void_p(0)
     st, io = _state(), _io()
     assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(_conv()), z) == 0      # N = 0
     for bad in (dict(W=3), dict(silu=2), dict(state=None), dict(weight=None), dict(weight=36), dict(slot_stride=100),
-                dict(ch_stride=0), dict(tap_stride=0)):
+                dict(ch_stride=0), dict(tap_stride=0), dict(NS=0), dict(NS=-1)):
         assert lib.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(_conv(**bad)), z) == -1, bad
         assert lib.lq_conv_update(ctypes.byref(_conv(**bad)), ctypes.c_void_p(16), ctypes.c_void_p(16),
                                   ctypes.c_void_p(16), 1, 1024, 8, z) == -1, bad
@@ -292,3 +305,44 @@ def test_get_state_registry(lib):
 
     with pytest.raises(RuntimeError, match="prefix caching"):
         S.get_state(PrefixLayer(), torch.zeros(2, 4, 128, 128), H=2, L=16)
+
+
+@pytest.mark.parametrize("kda", [False, True])
+def test_decode_checks_the_gate(lib, kda):
+    """The raw gate is read as bf16 [N, HV] (GDN) or [N, HV, K] (KDA) (kernels.py:86, 738): another dtype or element
+    count is refused before any pointer is taken."""
+    from leapquant_amd.state import LeapQuantState
+    ssm = torch.zeros(3, 4, 128, 128)
+    st = LeapQuantState(ssm, 4 if kda else 2, kda=kda, L=16)
+    N, KA = 2, 128 if kda else 1
+    H = st.H
+    mixed = torch.zeros(N, 2 * H * 128 + 4 * 128, dtype=torch.bfloat16)
+    b = torch.zeros(N, 4, dtype=torch.bfloat16)
+    out = torch.zeros(N, 4, 128, dtype=torch.bfloat16)
+    dt = torch.zeros(4 * KA)
+    for a in (torch.zeros(N, 4 * KA), torch.zeros(N, 4 * KA + 1, dtype=torch.bfloat16),
+              torch.zeros(N + 1, 4 * KA, dtype=torch.bfloat16)):
+        with pytest.raises(ValueError, match="a: bf16"):
+            st.decode(ssm, mixed, a, b, torch.zeros(4), dt, torch.tensor([1, 2]), out)
+    if not kda:
+        x = torch.zeros(N, 2 * H * 128 + 4 * 128, dtype=torch.bfloat16)
+        cs = torch.zeros(3, x.shape[1], 3, dtype=torch.bfloat16)
+        w = torch.zeros(x.shape[1], 4, dtype=torch.bfloat16)
+        with pytest.raises(ValueError, match="a: bf16"):
+            st.decode_conv(ssm, x, cs, w, None, True, torch.zeros(N, 4), b, torch.zeros(4), dt,
+                           torch.tensor([1, 2]), out)
+
+
+def test_reference_import_name_reaches_the_same_modules(lib):
+    """`leapquant.kernels / .state / .vllm` (the reference's names, pyproject entry point leapquant.vllm:register) are
+    this build's modules, so the per-layer registry is one object whichever name a caller imports."""
+    import leapquant
+    import leapquant.state as LS
+    import leapquant_amd.state as AS
+    from leapquant.kernels import QMAX, make_flush, make_gdn_step, make_quantize, lowrank_factor  # noqa: F401
+    from leapquant.vllm import register
+    import leapquant_amd.vllm as AV
+    assert LS is AS and LS._STATES is AS._STATES and register is AV.register
+    assert leapquant.__version__ == "0.1.0" and QMAX == 127.0
+    toml = open(os.path.join(ROOT, "pyproject.toml")).read()
+    assert 'leapquant = "leapquant.vllm:register"' in toml

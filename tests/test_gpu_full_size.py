@@ -72,7 +72,7 @@ def _assert_checkpoints(g, r, slots, qmax=127.0, S=None):
     rounded to the other fp16 neighbour (an fp32 sum of a different order on the other side of a rounding boundary)
     moves a row or column of the residual by ~2^-11 |Q U|, and when that moves a row's maximum every code of the row
     rescales (its scale moves by up to a few 1e-3, its codes by up to 2 LSB).  Heads with codes more than 1 LSB or
-    scales more than 2e-3 apart (at most 1 %) are compared by their materialised checkpoints Q U^T + codes Sk Sv / qmax,
+    scales more than 2e-3 apart (at most 1 %, or one head of a small case) are compared by their materialised checkpoints Q U^T + codes Sk Sv / qmax,
     within one quantisation step of each side plus the factor products' difference, and must have differing factors.
     S (the standalone quantize's fp32 input, one fp16 rounding of each factor): the factors agree entrywise (rtol 2e-3:
     one fp16 ulp; atol 2e-4 for entries near zero, where an fp32 sum's error is many of their ulps), and the oracle's
@@ -85,7 +85,7 @@ def _assert_checkpoints(g, r, slots, qmax=127.0, S=None):
     assert (d > 0).mean() <= 1e-3, (d > 0).mean()
     rel = lambda k: np.abs(gs[k].astype(np.float64) / rs[k] - 1.0).max(axis=-1)
     near = (d.max(axis=(-2, -1)) <= 1) & (rel("Sk") <= 2e-3) & (rel("Sv") <= 2e-3)     # [slot, head]
-    assert (~near).mean() <= 1e-2, (~near).sum()
+    assert (~near).sum() <= max(1, 1e-2 * near.size), (~near).sum()
     if (~near).any():
         sel = lambda c: {k: v[~near][None] for k, v in c.items()}
         mg, qg, stg = _materialized(sel(gs), qmax)
@@ -145,9 +145,10 @@ def test_decode_at_full_size_matches_oracle(kda):
     assert np.array_equal(G.from_gpu(ssm, lq)["hcnt"], st["hcnt"])
 
 
-def test_config3_quantize_and_flush_at_full_size():
-    """Config 3: 256 x 32 Student-t(3) x 0.02 heads; quantize of every head vs the oracle; all-due flush (64 buffered
-    entries per head) vs the oracle on 512 heads and through properties of the codes on all 8192."""
+@pytest.mark.parametrize("qmax", [127.0, 31.0])
+def test_config3_quantize_and_flush_at_full_size(qmax):
+    """Config 3: 256 x 32 Student-t(3) x 0.02 heads, INT8 and 6-bit; quantize of every head vs the oracle; all-due
+    flush (64 buffered entries per head) vs the oracle on 512 heads and through properties of the codes on all 8192."""
     rng = np.random.default_rng(1003)
     NSL, HV, H, L = 256, 32, 16, 64
     NS = NSL + 1
@@ -155,13 +156,13 @@ def test_config3_quantize_and_flush_at_full_size():
     st = O.new_state(NS, HV, H, L=L)
     Q0 = O.make_q0(128, 4)
     idx = np.arange(1, NS, dtype=np.int64)
-    print("config 3: oracle quantize of %d heads" % (NSL * HV), flush=True)
-    O.quantize(st, S, Q0, idx)
-    ssm, lq = G.to_gpu(st)
+    print("config 3 (qmax %g): oracle quantize of %d heads" % (qmax, NSL * HV), flush=True)
+    O.quantize(st, S, Q0, idx, qmax=qmax)
+    ssm, lq = G.to_gpu(st, qmax=qmax)
     ssm.copy_(torch.from_numpy(S))
     lq.quantize(ssm, torch.from_numpy(idx).to(G.DEV))
     g = G.from_gpu(ssm, lq)
-    _assert_checkpoints(g, st, slice(1, NS), S=S[1:])
+    _assert_checkpoints(g, st, slice(1, NS), qmax=qmax, S=S[1:])
 
     # the flush of a full window on every head, from the oracle's checkpoint on both sides
     _fill_windows(rng, st, L - 1, kda=False)
@@ -169,15 +170,14 @@ def test_config3_quantize_and_flush_at_full_size():
     A_log, dt_bias = gate_params(HV)
     mixed, a, b = make_inputs(rng, NSL, HV, H)
     G.load_state(lq, ssm, st)
-    print("config 3: oracle step + flush of %d heads" % (len(sub) * HV), flush=True)
-    O.gdn_step(st, mixed, a, b, A_log, dt_bias, idx)    # fills every window (64 entries)
-    qmax = 127
+    print("config 3 (qmax %g): oracle step + flush of %d heads" % (qmax, len(sub) * HV), flush=True)
+    O.gdn_step(st, mixed, a, b, A_log, dt_bias, idx, qmax=qmax)    # fills every window (64 entries)
     before = O.copy_state(st)
-    O.flush(st, Q0, sub)
+    O.flush(st, Q0, sub, qmax=qmax)
     _decode(lq, ssm, mixed, a, b, A_log, dt_bias, idx)  # step + flush of all 8192 heads on the GPU
     g = G.from_gpu(ssm, lq)
     assert np.all(before["hcnt"][1:] == L)
-    _assert_checkpoints(g, st, sub)
+    _assert_checkpoints(g, st, sub, qmax=qmax)
     codes = g["Sq"][1:].astype(np.int32)
     assert np.abs(codes).max() <= qmax
     rmax = np.abs(codes).max(axis=-1)                   # per (slot, head, row v)

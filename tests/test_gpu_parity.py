@@ -17,17 +17,18 @@ pytestmark = pytest.mark.gpu
 RT, AT = 2e-2, 1e-3
 
 
-def _prestep(rng, st, Q0, kda, steps, NS, HV, H, glb=0.0):
-    """Oracle decode steps (each + flush) on random subsets of the slots: every slot ends at its own window fill."""
+def _prestep(rng, st, Q0, kda, steps, NS, HV, H, glb=0.0, qmax=127.0):
+    """Oracle decode steps (each + flush) on random subsets of the slots: every slot ends at its own window fill.  The
+    steps and flushes read and write the state at its own code range qmax."""
     A_log, dt_bias = gate_params(HV, 128, kda)
     for _ in range(steps):
         sl = rng.permutation(np.arange(1, NS))[: rng.integers(1, NS)]
         mixed, a, b = make_inputs(rng, len(sl), HV, H, kda=kda)
         if kda:
-            O.kda_step(st, mixed, a, b, A_log, dt_bias, sl, glb=glb)
+            O.kda_step(st, mixed, a, b, A_log, dt_bias, sl, glb=glb, qmax=qmax)
         else:
-            O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
-        O.flush(st, Q0, sl)
+            O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl, qmax=qmax)
+        O.flush(st, Q0, sl, qmax=qmax)
 
 
 def _run_step(lq, ssm, mixed, a, b, A_log, dt_bias, idx):
@@ -197,13 +198,13 @@ def test_step_matches_oracle(kda, L, GQA):
 
 def _flush_case(rng, kda, L, qmax=127.0, NS=6, HV=4, H=2):
     st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda, qmax=qmax)
-    _prestep(rng, st, Q0, kda, steps=L + 5, NS=NS, HV=HV, H=H)
+    _prestep(rng, st, Q0, kda, steps=L + 5, NS=NS, HV=HV, H=H, qmax=qmax)
     # bring slots 1 and 3 to a full window (due), leave the others partial
     A_log, dt_bias = gate_params(HV, 128, kda)
     for s in (1, 3):
         while st["hcnt"][s, 0] < L:
             mixed, a, b = make_inputs(rng, 1, HV, H, kda=kda)
-            (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, np.array([s]))
+            (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, np.array([s]), qmax=qmax)
     return st, Q0
 
 

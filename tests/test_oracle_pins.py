@@ -158,6 +158,99 @@ def test_step_special_cases_gdn():
     np.testing.assert_allclose(o[0], kappa[:, None] * beta[:, None] * v[0], rtol=2 ** -7, atol=1e-6)
 
 
+@pytest.mark.parametrize("kda", [False, True])
+def test_6bit_steps_and_flush_match_dense_rule(kda):
+    """A 6-bit checkpoint (codes in [-31, 31], dequantised as Sq Sk Sv / 31) stepped through a window and flushed: the
+    outputs and the new logical state follow the dense float64 rule on the materialised 6-bit state, and the flush keeps
+    that state within the 6-bit quantisation bound.  Stepping the same state with the INT8 convention (1 / 127) misses the
+    dense rule by far more than the bar (the planted mistake this pin exists to catch)."""
+    qmax, L, HV, H = 31.0, 16, 2, (2 if kda else 1)
+    rng = np.random.default_rng(61 + kda)
+    st, _, Q0 = make_state(rng, 3, HV, H, L=L, kda=kda, qmax=qmax)
+    assert np.abs(st["Sq"][1:].astype(np.int32)).max() == 31
+    A_log, dt_bias = gate_params(HV, K, kda)
+    idx = np.array([2, 1, 0])
+    hk = np.arange(HV) // (HV // H)
+    step = O.kda_step if kda else O.gdn_step
+    for t in range(L):
+        mixed, a, b = make_inputs(rng, 3, HV, H, kda=kda)
+        rows = idx > 0
+        s = idx[rows]
+        q, k, v = _qk_from_mixed(mixed[rows], H, HV)
+        beta = O.beta_of(b[rows]).astype(np.float64)
+        S = O.materialize(st, qmax)
+        if t == 0:                                       # the planted mistake: the same state read with 1 / 127
+            wrong = O.copy_state(st)
+            o_wrong = step(wrong, mixed, a, b, A_log, dt_bias, idx)
+        if kda:
+            g, _ = O.kda_gate(a.reshape(3, HV, K)[rows], dt_bias, A_log, 0.0)
+            S1, od, u, kh = O.dense_kda_step(S[s], q[:, hk], k[:, hk], v, g, beta, K ** -0.5)
+        else:
+            alpha = O.gdn_alpha(a[rows], dt_bias, A_log).astype(np.float64)
+            S1, od, u, kh = O.dense_gdn_step(S[s], q[:, hk], k[:, hk], v, alpha, beta, K ** -0.5)
+        o = step(st, mixed, a, b, A_log, dt_bias, idx, qmax=qmax)
+        scale_o = np.abs(od).max()
+        assert np.abs(o[rows] - od).max() <= 2e-2 * scale_o, (t, np.abs(o[rows] - od).max() / scale_o)
+        if t == 0:
+            assert np.abs(o_wrong[rows] - od).max() > 0.2 * scale_o
+        Sm = O.materialize(st, qmax)
+        tol = 2 ** -7 * np.abs(u).max() * np.abs(kh).max() + 2 ** -10 * np.abs(S1).max()
+        assert np.abs(Sm[s] - S1).max() < tol, (t, np.abs(Sm[s] - S1).max(), tol)
+    assert np.all(st["hcnt"][1:] == L)
+    S_before = O.materialize(st, qmax)
+    O.flush(st, Q0, idx, qmax=qmax)
+    codes = st["Sq"][1:].astype(np.int32)
+    assert np.abs(codes).max() <= 31 and np.all(np.abs(codes).max(-1) == 31)
+    sk = st["Sk"][1:].astype(np.float64)[:, :, None, :]
+    sv = st["Sv"][1:].astype(np.float64)[:, :, :, None]
+    bound = 0.5 * sk * sv / qmax + 2 ** -9 * np.abs(S_before[1:]).max()
+    assert np.all(np.abs(O.materialize(st, qmax)[1:] - S_before[1:]) <= bound)
+
+
+def test_flush_of_a_rank_deficient_state():
+    """A state of rank 2 (empty checkpoint, a window whose 16 keys take two directions) takes CholeskyQR2's relative
+    pivot floor (kernels.py:1816-1825) on factors 3 and 4: the floor must keep every output finite, the first two
+    factors must span the state's columns (sign-fixed numpy QR of S S^T Q0), and the logical state must survive the
+    flush within its quantisation bound."""
+    st, Q0, S = _rank2_state()
+    # the floor is live: the third and fourth pivots of the Gram of S S^T Q0 vanish next to the diagonal
+    X = S @ (S.T @ O.fp16(Q0).astype(np.float64))
+    Gm = X.T @ X
+    Lc = np.linalg.cholesky(Gm[:2, :2])
+    d2 = Gm[2, 2] - np.sum(np.linalg.solve(Lc, Gm[:2, 2]) ** 2)
+    assert d2 < 1e-6 * Gm[2, 2]
+    dbg = O.flush(st, Q0, np.array([1]), return_debug=True)
+    assert len(dbg["pairs"]) == 1
+    for key in ("Sq", "Sk", "Sv", "UQ"):
+        assert np.all(np.isfinite(st[key][1].astype(np.float64))), key
+    Qref = _sign_fixed_qr(X)[:, :2]
+    assert np.abs(dbg["Q16"][0][:, :2] - Qref).max() < 2e-3
+    after = O.materialize(st)[1, 0]
+    sk, sv = st["Sk"][1, 0].astype(np.float64), st["Sv"][1, 0].astype(np.float64)
+    bound = 0.5 * sk[None, :] * sv[:, None] / 127.0 + 2 ** -9 * np.abs(S).max()
+    assert np.all(np.abs(after - S) <= bound)
+
+
+def _rank2_state(L=16, seed=71):
+    """(state, Q0, S): slot 1, head 0 holds the rank-2 logical state S = sum_j w_j u_j k_j^T with k_j in {ka, kb}, an
+    all-zero checkpoint and a full window (hcnt = L), so the next flush takes it."""
+    rng = np.random.default_rng(seed)
+    st = O.new_state(2, 1, 1, L=L)
+    Q0 = O.make_q0(128, 4)
+    st["Sk"][:] = 1.0
+    st["Sv"][:] = 1.0
+    kk = rng.standard_normal((2, 128))
+    kk /= np.linalg.norm(kk, axis=-1, keepdims=True)
+    sel = np.arange(L) % 2
+    st["Kbuf"][1, 0] = O.bf16(kk[sel])
+    st["Ubuf"][1, 0] = O.bf16(0.3 * rng.standard_normal((L, 128)))
+    st["Wbuf"][1, 0] = np.exp(-0.05 * np.arange(L)[::-1]).astype(np.float32)
+    st["hcnt"][1, 0] = L
+    S = O.materialize(st)[1, 0]
+    assert np.linalg.matrix_rank(S, tol=1e-9 * np.abs(S).max()) == 2
+    return st, Q0, S
+
+
 # ------------------------------------------------------------------------------------------------ flush
 @pytest.mark.parametrize("kda,dims", STEP_CASES)
 @pytest.mark.parametrize("L", [16, 64])

@@ -1,4 +1,6 @@
-"""CPU tests of the vLLM plugin's routing (leapquant_amd/vllm), against the stand-in vLLM of tests/fake_vllm.py.
+"""CPU tests of the vLLM plugin's routing (leapquant_amd/vllm), against the stand-in vLLM of tests/fake_vllm.py.  The
+plugin is reached as vLLM reaches it: through the entry point `leapquant.vllm:register` under the reference's package
+name.
 
 The layer state is replaced by a recorder, so these tests check which LeapQuant calls each kind of engine step makes,
 with which tensors and in which order (reference behaviour: leapquant/vllm/__init__.py:22-34, gdn.py:28-81,
@@ -41,8 +43,11 @@ class Recorder:
 @pytest.fixture
 def plugin(monkeypatch):
     FV.install()
-    import leapquant_amd.vllm as P
-    from leapquant_amd.vllm import gdn, glm
+    import importlib
+    mod, fn = "leapquant.vllm:register".split(":")          # the entry point, resolved as vLLM's plugin loader does
+    P = importlib.import_module(mod)
+    assert getattr(P, fn) is P.register
+    from leapquant.vllm import gdn, glm
     rec = {}
 
     def fake_get_state(layer, ssm, **kw):
