@@ -32,6 +32,7 @@ enum lq_status {
   LQ_OK = 0,
   LQ_ERR_ARG = -1,     /* a size, shape or pointer the kernels do not support */
   LQ_ERR_HIP = -2,     /* a HIP launch error (hipGetLastError after the launch) */
+  LQ_ERR_SIZE = -3,    /* lq_decode_noalloc: more (row, head) pairs than its static due list holds (LQ_DUE_MAX) */
 };
 
 /* Pointers and sizes of one layer's state: the fp32 cache the checkpoint aliases and the window buffer. */
@@ -141,6 +142,16 @@ int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N
  * Replaces make_lowrank / lowrank_factor (kernels.py:2246-2331).  Requires K = V = 128, 1 <= R <= 4. */
 int lq_lowrank(const float* x, const float* Q0, float* U, float* Q, int n, int K, int V, int R, int iters,
                void* stream);
+
+/* No counterpart in the reference: one decode call -- the step of every row (GDN, or KDA with gate glb), then the
+ * flush of the heads that step made due (codes in [-qmax, qmax], qmax = st->qmax, 0 meaning 127) -- that allocates
+ * nothing and takes no workspace: the due heads are passed from the step to the flush through a list in the library's
+ * own static device memory (256 KiB per GPU, held until the process ends), not through st->ctl, which it ignores.
+ * For callers that cannot allocate device memory: code under graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc.  Limit: N * HV <= LQ_DUE_MAX = 65536, else LQ_ERR_SIZE.  All calls on one GPU share the list: calls that
+ * overlap on one GPU (concurrent streams, threads) race and must not be issued.  Results equal lq_gdn_step /
+ * lq_kda_step followed by lq_flush on the same inputs. */
+int lq_decode_noalloc(const lq_state* st, const lq_step_io* io, const float* Q0, int kda, float glb, void* stream);
 
 /* Baseline (no reference counterpart): the standalone conv1d update that lq_gdn_step_conv fuses into the step, same
  * arithmetic (it stands for vLLM's causal_conv1d_update, leapquant/vllm/gdn.py:32): out [N][C] bf16 from the raw

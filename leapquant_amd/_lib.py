@@ -42,6 +42,8 @@ SIGNATURES = {
     "lq_conv_update": (c_int, [ctypes.POINTER(LqConv), c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_void_p]),
     "lq_dense_step": (c_int, [c_void_p, c_int, c_int, c_int, c_int, c_int, c_int, ctypes.POINTER(LqStepIO),
                               c_void_p]),
+    "lq_decode_noalloc": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_void_p, c_int, c_float,
+                                  c_void_p]),
 }
 
 _LIB = [None]
@@ -64,7 +66,8 @@ def lib():
     return _LIB[0]
 
 
-_ERR = {-1: "bad argument (unsupported shape / size / pointer)", -2: "HIP launch error"}
+_ERR = {-1: "bad argument (unsupported shape / size / pointer)", -2: "HIP launch error",
+        -3: "more (row, head) pairs than the static due list of lq_decode_noalloc holds (N * HV <= 65536)"}
 
 
 def check(rc, what):

@@ -13,7 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "liblq.so")
-SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dense.hip")
+SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dense.hip", "lq_noalloc.hip")
 ARCH = os.environ.get("LQ_OFFLOAD_ARCH", "gfx950")
 
 

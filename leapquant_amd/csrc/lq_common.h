@@ -182,6 +182,20 @@ __device__ __forceinline__ void mark_due(int* ctl) {
     __hip_atomic_fetch_or(ctl, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// ---- due list (lq_decode_noalloc): {count of due heads, flush workgroups done, list of p = n HV + hv} -------------
+// A step that fills a head's window (or meets a full one) appends the head instead of raising the due flag; the flush
+// then takes exactly the listed heads.  Appends past the list's capacity are dropped: such a head stays full and the
+// next step of its row lists it again.
+#define LQ_DUE_MAX 65536
+__device__ __forceinline__ void note_due(int* ctl, int* dlist, int p) {
+  if (dlist) {
+    const int i = __hip_atomic_fetch_add(dlist, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (i < LQ_DUE_MAX) dlist[2 + i] = p;
+  } else {
+    mark_due(ctl);
+  }
+}
+
 // code range of the stored checkpoint (lq_state.qmax; 0: INT8)
 __device__ __forceinline__ float code_range(const lq_state& st) { return st.qmax > 0.f ? st.qmax : LQ_QMAX; }
 
@@ -189,3 +203,15 @@ __device__ __forceinline__ float code_range(const lq_state& st) { return st.qmax
 __device__ __forceinline__ char* block_base(const lq_state& st, int slot, int hv) {
   return (char*)st.ssm + 4ll * ((long long)slot * st.slot_stride + (long long)hv * st.V * st.K);
 }
+
+// ---- checks and launches shared by the entry points of different source files (not exported) ----------------------
+// the argument checks of lq_gdn_step / lq_kda_step (the KDA step also needs Gbuf and K = V = 128) and of lq_flush
+__attribute__((visibility("hidden"))) int lq_check_step(const lq_state* st, const lq_step_io* io);
+__attribute__((visibility("hidden"))) int lq_check_flush(const lq_state* st, const float* Q0, const int* idx, int N,
+                                                         int kda, float qmax);
+// decode step of every row of io (GDN or KDA), due heads signalled through dlist when it is set (else st->ctl)
+__attribute__((visibility("hidden"))) int lq_launch_step(const lq_state* st, const lq_step_io* io, int kda, float glb,
+                                                         int* dlist, hipStream_t s);
+// flush of the due heads: the listed ones when dlist is set (the list is then reset), else found by the scan
+__attribute__((visibility("hidden"))) int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N,
+                                                          int kda, float qmax, int* dlist, hipStream_t s);

@@ -678,10 +678,47 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 // (wave 0, one per lane), and processes the due ones (slot > 0, hcnt == L; kernels.py:1200) one after another.
 // With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
 // otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
+// With a due list (dlist, lq_decode_noalloc) the flush takes exactly the listed heads instead: workgroup b the entries
+// b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, so
+// an entry left by an interrupted call is skipped; the last workgroup to finish empties the list.
+template <bool KDA, int K_, int V_>
+__device__ void flush_listed(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0,
+                             const int* __restrict__ idx, int N, float qmax, int* dlist) {
+  const int HV = st.HV, L = st.L;
+  const int cnt = min(__hip_atomic_load(dlist, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), LQ_DUE_MAX);
+  if (cnt == 0) return;                               // uniform: nothing due (the list is already empty)
+  for (int e = blockIdx.x; e < cnt; e += gridDim.x) {
+    if (threadIdx.x == 0) {
+      const int p = dlist[2 + e];
+      long long take = -1;
+      if (p >= 0 && p < N * HV) {
+        const int n = p / HV, hv = p - n * HV, slot = idx[n];
+        if (slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L) take = (long long)slot * HV + hv;
+      }
+      sh.due = (unsigned long long)take;
+    }
+    __syncthreads();
+    const long long take = (long long)sh.due;
+    __syncthreads();
+    if (take >= 0) flush_head<KDA, K_, V_>(sh, st, Q0, (int)(take / HV), (int)(take % HV), qmax);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && __hip_atomic_fetch_add(dlist + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                              (int)gridDim.x - 1) {
+    __hip_atomic_store(dlist, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(dlist + 1, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 template <bool KDA, int K_ = KD, int V_ = VD>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
-void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax) {
+void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
+                  int* dlist) {
   __shared__ FlushShared sh;
+  if (dlist) {
+    flush_listed<KDA, K_, V_>(sh, st, Q0, idx, N, qmax, dlist);
+    return;
+  }
   const int HV = st.HV, L = st.L;
   const int total = N * HV;
   const int stride = gridDim.x;
@@ -1256,19 +1293,29 @@ int check_block_state(const lq_state* st, bool need_buf, bool kda) {
 
 }  // namespace
 
-extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream) {
+int lq_check_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax) {
   int rc = check_block_state(st, true, kda != 0);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || (kda && !st->Gbuf)) return LQ_ERR_ARG;
+  return LQ_OK;
+}
+
+int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, int* dlist,
+                    hipStream_t s) {
   if (N == 0) return LQ_OK;
   const int total = N * st->HV;
   const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
-  hipStream_t s = (hipStream_t)stream;
-  if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
-  else if (st->K == KD) flush_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
-  else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
-  else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax);
+  if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if (st->K == KD) flush_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+}
+
+extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream) {
+  int rc = lq_check_flush(st, Q0, idx, N, kda, qmax);
+  if (rc) return rc;
+  return lq_launch_flush(st, Q0, idx, N, kda, qmax, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {

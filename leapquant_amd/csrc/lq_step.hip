@@ -84,7 +84,7 @@ struct StepShared {
 // ------------------------------------------------------------------------------------------------------------------
 template <int K_, int V_, int G, bool CONV>
 __global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
-void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
+void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist) {
   constexpr int KD = K_, VD = V_;
   constexpr int WPH = VD / 64;  // waves per value head
   constexpr int NE = KD / 64;   // channels per lane in the scalar work
@@ -383,7 +383,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
   __syncthreads();              // ... and the other wave's, with the key and factor dots of every wave
   if (!live) {                  // a full window (a flush that did not cover this row): zero output, nothing written;
-    if (lt == 0) mark_due(st.ctl);   // flag it again so that the flush after this step takes it
+    if (lt == 0) note_due(st.ctl, dlist, n * HV + hv);   // flag it again so that the flush after this step takes it
     out[lt] = 0;
     return;
   }
@@ -455,7 +455,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
-    if (h + 1 == L) mark_due(st.ctl);   // this head is due: the flush that follows will not skip
+    if (h + 1 == L) note_due(st.ctl, dlist, n * HV + hv);   // this head is due: the flush that follows takes it
   }
   if (wi == 0) {
 #pragma unroll
@@ -527,7 +527,7 @@ __device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr
   }
 }
 
-__global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io io, float glb) {
+__global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io io, float glb, int* dlist) {
   __shared__ KdaShared sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int G = HV / H;
@@ -574,7 +574,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   __builtin_amdgcn_sched_barrier(0);
   const int h = hfill;
   if (h >= L) {                 // a full window is never stepped: zero output, and the head is flagged again so that
-    if (lt == 0) mark_due(st.ctl);   // the flush after this step takes it
+    if (lt == 0) note_due(st.ctl, dlist, n * HV + hv);   // the flush after this step takes it
     out[lt] = 0;
     return;
   }
@@ -811,7 +811,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   if (lt == 0) {
     st.Wbuf[sh_ * L + h] = 1.0f;
     st.hcnt[sh_] = h + 1;
-    if (h + 1 == L) mark_due(st.ctl);   // this head is due: the flush that follows will not skip
+    if (h + 1 == L) note_due(st.ctl, dlist, n * HV + hv);   // this head is due: the flush that follows takes it
   }
   if (wi == 0) {                // gate state (kernels.py:895-896)
 #pragma unroll
@@ -828,7 +828,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 // head dims of the GDN step (kernels.py:62); the KDA step is K = V = 128 only (kernels.py:727)
 static bool gdn_dims(int K, int V) { return (K == 128 && V == 128) || (K == 64 && (V == 128 || V == 64)); }
 
-static int check_step(const lq_state* st, const lq_step_io* io) {
+int lq_check_step(const lq_state* st, const lq_step_io* io) {
   if (!st || !io) return LQ_ERR_ARG;
   if (!gdn_dims(st->K, st->V) || st->L < 1 || st->L > LMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
   if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0 || io->N < 0) return LQ_ERR_ARG;
@@ -843,34 +843,42 @@ static int check_step(const lq_state* st, const lq_step_io* io) {
 }
 
 template <int K_, int V_, bool CONV>
-static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, hipStream_t s) {
+static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
   dim3 grid((unsigned)(io->N * st->H));
   switch (st->HV / st->H) {
-    case 1: gdn_step_kernel<K_, V_, 1, CONV><<<grid, V_, 0, s>>>(*st, *io, cv); break;
-    case 2: gdn_step_kernel<K_, V_, 2, CONV><<<grid, 2 * V_, 0, s>>>(*st, *io, cv); break;
-    case 4: gdn_step_kernel<K_, V_, 4, CONV><<<grid, 4 * V_, 0, s>>>(*st, *io, cv); break;
+    case 1: gdn_step_kernel<K_, V_, 1, CONV><<<grid, V_, 0, s>>>(*st, *io, cv, dlist); break;
+    case 2: gdn_step_kernel<K_, V_, 2, CONV><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist); break;
+    case 4: gdn_step_kernel<K_, V_, 4, CONV><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
 template <bool CONV>
-static int launch_gdn_dims(const lq_state* st, const lq_step_io* io, const lq_conv& cv, void* stream) {
-  hipStream_t s = (hipStream_t)stream;
-  if (st->K == 128) return launch_gdn<128, 128, CONV>(st, io, cv, s);
-  return st->V == 128 ? launch_gdn<64, 128, CONV>(st, io, cv, s) : launch_gdn<64, 64, CONV>(st, io, cv, s);
+static int launch_gdn_dims(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
+  if (st->K == 128) return launch_gdn<128, 128, CONV>(st, io, cv, dlist, s);
+  return st->V == 128 ? launch_gdn<64, 128, CONV>(st, io, cv, dlist, s) : launch_gdn<64, 64, CONV>(st, io, cv, dlist, s);
+}
+
+// the plain GDN / KDA step of every row, arguments already checked
+int lq_launch_step(const lq_state* st, const lq_step_io* io, int kda, float glb, int* dlist, hipStream_t s) {
+  if (io->N == 0) return LQ_OK;
+  if (!kda) {
+    const lq_conv none = {};
+    return launch_gdn_dims<false>(st, io, none, dlist, s);
+  }
+  kda_step_kernel<<<dim3((unsigned)(io->N * st->HV)), 128, 0, s>>>(*st, *io, glb, dlist);
+  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
 extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream) {
-  int rc = check_step(st, io);
+  int rc = lq_check_step(st, io);
   if (rc) return rc;
-  if (io->N == 0) return LQ_OK;
-  const lq_conv none = {};
-  return launch_gdn_dims<false>(st, io, none, stream);
+  return lq_launch_step(st, io, 0, 0.f, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
-  int rc = check_step(st, io);
+  int rc = lq_check_step(st, io);
   if (rc) return rc;
   if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || cv->NS <= 0)
     return LQ_ERR_ARG;
@@ -880,17 +888,14 @@ extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const 
   if ((C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride) return LQ_ERR_ARG;
   if (((uintptr_t)cv->weight & 7) != 0) return LQ_ERR_ARG;
   if (io->N == 0) return LQ_OK;
-  return launch_gdn_dims<true>(st, io, *cv, stream);
+  return launch_gdn_dims<true>(st, io, *cv, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream) {
-  int rc = check_step(st, io);
+  int rc = lq_check_step(st, io);
   if (rc) return rc;
   if (!st->Gbuf || st->K != KD || st->V != VD) return LQ_ERR_ARG;
-  if (io->N == 0) return LQ_OK;
-  dim3 grid((unsigned)(io->N * st->HV));
-  kda_step_kernel<<<grid, 128, 0, (hipStream_t)stream>>>(*st, *io, glb);
-  return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+  return lq_launch_step(st, io, 1, glb, nullptr, (hipStream_t)stream);
 }
 
 extern "C" int lq_abi_version(void) { return LQ_ABI_VERSION; }
