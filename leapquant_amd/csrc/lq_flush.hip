@@ -41,6 +41,12 @@ __device__ __forceinline__ f16x4 to_h4(f32x4 x) {
   return f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
 }
 __device__ __forceinline__ f32x4 from_h4(f16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
+// The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
+// redo the conversion where the value is used (twice the registers).
+__device__ __forceinline__ f16x4 pinned(f16x4 x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
 
 struct Tile {
   f32x4 a[8];
@@ -681,9 +687,49 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
 // With a due list (dlist, lq_decode_noalloc) the flush takes exactly the listed heads instead: workgroup b the entries
 // b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, so
 // an entry left by an interrupted call is skipped; the last workgroup to finish empties the list.
-template <bool KDA, int K_, int V_>
-__device__ void flush_listed(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0,
-                             const int* __restrict__ idx, int N, float qmax, int* dlist) {
+// `head(slot, hv)` flushes one head with the whole workgroup; `due` is a word of the workgroup's shared memory.
+template <class Head>
+__device__ void flush_scan(unsigned long long& due, const lq_state& st, const int* __restrict__ idx, int N,
+                           Head head) {
+  const int HV = st.HV, L = st.L;
+  const int total = N * HV;
+  const int stride = gridDim.x;
+  if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
+  for (int base = blockIdx.x; base < total; base += 64 * stride) {
+    if (threadIdx.x < 64) {
+      const int p = base + stride * (int)threadIdx.x;
+      bool d = false;
+      if (p < total) {
+        const int n = p / HV, hv = p - n * HV;
+        const int slot = idx[n];
+        d = slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L;
+      }
+      const unsigned long long m = __ballot(d);
+      if (threadIdx.x == 0) due = m;
+    }
+    __syncthreads();
+    unsigned long long m = due;
+    __syncthreads();
+    while (m) {
+      const int b = __ffsll((long long)m) - 1;
+      m &= m - 1;
+      const int p = base + stride * b;
+      const int n = p / HV, hv = p - n * HV;
+      head(idx[n], hv);
+    }
+  }
+  if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
+    __syncthreads();
+    if (threadIdx.x == 0 && atomicAdd(st.ctl + 1, 1) == (int)gridDim.x - 1) {
+      __atomic_store_n(st.ctl, 0, __ATOMIC_RELAXED);
+      __atomic_store_n(st.ctl + 1, 0, __ATOMIC_RELAXED);
+    }
+  }
+}
+
+template <class Head>
+__device__ void flush_listed(unsigned long long& due, const lq_state& st, const int* __restrict__ idx, int N,
+                             int* dlist, Head head) {
   const int HV = st.HV, L = st.L;
   const int cnt = min(__hip_atomic_load(dlist, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), LQ_DUE_MAX);
   if (cnt == 0) return;                               // uniform: nothing due (the list is already empty)
@@ -695,12 +741,12 @@ __device__ void flush_listed(FlushShared& sh, const lq_state& st, const float* _
         const int n = p / HV, hv = p - n * HV, slot = idx[n];
         if (slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L) take = (long long)slot * HV + hv;
       }
-      sh.due = (unsigned long long)take;
+      due = (unsigned long long)take;
     }
     __syncthreads();
-    const long long take = (long long)sh.due;
+    const long long take = (long long)due;
     __syncthreads();
-    if (take >= 0) flush_head<KDA, K_, V_>(sh, st, Q0, (int)(take / HV), (int)(take % HV), qmax);
+    if (take >= 0) head((int)(take / HV), (int)(take % HV));
   }
   __syncthreads();
   if (threadIdx.x == 0 && __hip_atomic_fetch_add(dlist + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -715,44 +761,484 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
   __shared__ FlushShared sh;
-  if (dlist) {
-    flush_listed<KDA, K_, V_>(sh, st, Q0, idx, N, qmax, dlist);
-    return;
+  auto head = [&](int slot, int hv) { flush_head<KDA, K_, V_>(sh, st, Q0, slot, hv, qmax); };
+  if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
+  else flush_scan(sh.due, st, idx, N, head);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Four-wave GDN flush: one due head per workgroup of 256 threads, <= 40 KiB LDS and <= 128 VGPRs, so that four heads
+// share a CU (the eight-wave flush above fits two).  The flush is latency-bound -- each head is a chain of dependent,
+// barrier-separated phases -- so heads in flight per CU set its rate.  Same arithmetic, in the same order, as
+// flush_head; only the distribution over the lanes differs: wave w owns key channels [32 w, 32 w + 32) as two groups
+// g of 16, and lane l holds
+//     a[g][nt][i] = M[c][v],   c = 32 w + 16 g + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
+// The window is staged and multiplied in halves of 32 entries.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int FT4 = 256;             // threads per workgroup
+constexpr int NW4 = FT4 / 64;        // waves
+constexpr int HALF = 32;             // window entries staged at once
+constexpr int OPS4 = HALF + 8;       // operand row stride (bf16): 80 B rows, 16-byte aligned, conflict-free b128 reads
+
+struct Tile4 {
+  f32x4 a[2][8];
+};
+
+struct FlushShared4 {
+  union {
+    bf16_t op[3][KD][OPS4];    // rebuild operands of one window half [c or v][j]
+    struct {                   // after the rebuild
+      f32x4 qpart[NW4][VD];    // per-wave partial Q rows
+      float rmx[4 * NW4][VD];  // per-(wave, lane group) row maxima of the scaled residual
+      float rq[VD];            // qmax / row scale
+      f16_t ppT[4][KD];        // P16^T
+      f16_t uoT[4][KD];        // old U^T, fp16 (MFMA operand)
+      f16_t qoT[4][VD];        // old Q^T, fp16
+    } r;
+  };
+  float skl[KD];               // column factor of the dequant (Sk)
+  float svr[VD];               // row factor of the dequant (Sv pn / qmax)
+  float w[LPMAX];
+  f32x4 uoc[KD];               // old U rows [c][a], a >= R zero
+  f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
+  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
+  unsigned long long due;      // persistent flush: due mask of the current candidate chunk / listed head
+};
+static_assert(sizeof(FlushShared4) <= 40960, "four workgroups per CU: 160 KiB of LDS");
+
+// One window half's rows in registers: thread t takes entries 2 (t % 16), 2 (t % 16) + 1 of the half, columns
+// 8 (t / 16) .. 8 (t / 16) + 7 (16 x 16 = 256 threads).  Rows >= h read row 0 (in bounds; their weight is zero).
+struct WinHalf {
+  uint4 k[2], u[2];
+};
+template <int K_, int V_>
+__device__ __forceinline__ void load_half(WinHalf& r, const lq_state& st, int slot, int hv, int h, int hf) {
+  const int G = st.HV / st.H, hk = hv / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
+  const int t = opaque_tid(), jp = t % 16, c8 = (t / 16) * 8;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);        // columns past a K_ / V_ < 128 head: zero operands
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = HALF * hf + 2 * jp + k, jr = j < h ? j : 0;
+    const uint4 kx = *(const uint4*)(Kb + (long long)jr * K_ + (K_ == KD ? c8 : min(c8, K_ - 8)));
+    const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
+    r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
+    r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
   }
-  const int HV = st.HV, L = st.L;
-  const int total = N * HV;
-  const int stride = gridDim.x;
-  if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
-  for (int base = blockIdx.x; base < total; base += 64 * stride) {
-    if (threadIdx.x < 64) {
-      const int p = base + stride * (int)threadIdx.x;
-      bool due = false;
-      if (p < total) {
-        const int n = p / HV, hv = p - n * HV;
-        const int slot = idx[n];
-        due = slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L;
+}
+// Transposed into the rebuild operands [c or v][j - HALF hf], two entries per 32-bit LDS write: op0 = K_j[c],
+// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.
+__device__ __forceinline__ void store_half(FlushShared4& sh, const WinHalf& r, int h, int hf) {
+  // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
+#pragma clang fp contract(off)
+  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8;
+  const int j0 = HALF * hf + jl;
+  const bool v0 = j0 < h, v1 = j0 + 1 < h;
+  const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
+  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = e >> 1;
+    const bool odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
+    *(uint32_t*)&sh.op[0][c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
+    const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+    const uint32_t hi = pk_bf16(wu0, wu1);
+    *(uint32_t*)&sh.op[1][c8 + e][jl] = hi;
+    *(uint32_t*)&sh.op[2][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+  }
+}
+// acc[c][v] += sum_j A[c][j] B[v][j] over one staged half (bf16 operands, fp32 accumulate)
+__device__ __forceinline__ void rebuild_half4(Tile4& t, const bf16_t (*A)[OPS4], const bf16_t (*B)[OPS4]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  bf16x8 af[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) af[g] = *(const bf16x8*)&A[32 * w + 16 * g + (l & 15)][8 * q];
+#pragma unroll
+  for (int n2 = 0; n2 < 8; n2 += 2) {                 // two B fragments in flight at a time (register pressure)
+    const bf16x8 b0 = *(const bf16x8*)&B[16 * n2 + (l & 15)][8 * q];
+    const bf16x8 b1 = *(const bf16x8*)&B[16 * n2 + 16 + (l & 15)][8 * q];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b0, t.a[g][n2], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b1, t.a[g][n2 + 1], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+// the 16 code words of the lane's tile entries (zero past a K_ x V_ < 128 x 128 head's rows / columns)
+template <int K_, int V_>
+__device__ __forceinline__ void load_code_words4(uint32_t wds[2][8], const int8_t* Sq) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c = 32 * w + 16 * g + 4 * q;
+    const bool cok = K_ == KD || c < K_;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const uint32_t x = *(const uint32_t*)(Sq + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
+      wds[g][nt] = (cok && (V_ == VD || v < V_)) ? x : 0u;
+    }
+  }
+}
+// t += codes x svr[v] x skl[c], each term rounded to fp32 before the add (after the window products; see flush_head)
+__device__ __forceinline__ void tile_add_words4(Tile4& t, const uint32_t wds[2][8], const float* svr,
+                                                const float* skl) {
+#pragma clang fp contract(off)
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c0 = 32 * w + 16 * g + 4 * q;
+    float kc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const float rv = svr[16 * nt + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        t.a[g][nt][i] = t.a[g][nt][i] + ((float)(int)(int8_t)(wds[g][nt] >> (8 * i)) * rv) * kc[i];
+    }
+  }
+}
+// M[a][r] = sum_v Q_old[v][a] Q[v][r] (Q from sh.qT): every lane gets all 16 entries
+__device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4]) {
+  const int l = lane_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x8 z8 = {};
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 ao = rl4 ? *(const f16x8*)&sh.r.qoT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
+    macc = mma32(ao, bq, macc);
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+}
+// P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lanes
+// l < 16 return P[32 w + 16 g + l][0..3] (zero for r >= R) in p[g]; the other lanes zeros.  The contraction runs over
+// v, so each block of B is transposed on the way in (one exact MFMA against the identity: lane l then holds
+// B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]) rather than kept transposed in registers.
+__device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], float pn, int R,
+                                        f32x4 p[2]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x4 z4 = {};
+  float M[4][4];
+  gram_qold_q(sh, M);
+  f16x4 ident;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
+  f32x4 pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {                    // P^T[r][c] = sum_v Q^T[r][v] B[c][v] (k = v)
+    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const f16x4 bt = to_h4(mma16(bh[g][nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));
+      pacc[g] = mma16(aq, bt, pacc[g]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const f32x4 uo = sh.uoc[32 * w + 16 * g + l16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
+      p[g][r] = (q == 0 && r < R) ? hround(pacc[g][r] + pn * corr) : 0.f;
+    }
+  }
+}
+
+template <int K_ = KD, int V_ = VD>
+__device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+                            float qmax) {
+  const int HV = st.HV, L = st.L, R = st.R;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
+  char* base = block_base(st, slot, hv);
+  int8_t* Sq = (int8_t*)base;
+  float* Sk = (float*)(base + V_ * K_);
+  float* Sv = Sk + K_;
+  f16_t* UQ = (f16_t*)(Sv + V_);
+  const bool two = L > HALF;                          // window halves
+
+  // ---- stage 1: every load of the head up front ----
+  const float pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);     // kernels.py:1471
+  const float rpn = 1.0f / pn;                        // kernels.py:1477
+  const int cv = tid & 127;                           // column (tid < 128) or row of the stage-1 loads
+  const bool colt = tid < KD;
+  const int nc = colt ? K_ : V_;
+  const bool cok = (K_ == KD && V_ == VD) || cv < nc;
+  const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
+  const int vq = V_ == VD ? cv : min(cv, V_ - 1);
+  const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
+  float uqv[4], q0v[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
+    uqv[a] = cok ? x : 0.f;
+    const float y = Q0[vq * R + min(a, R - 1)];
+    q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
+  }
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinHalf win;
+  load_half<K_, V_>(win, st, slot, hv, L, 0);
+  uint32_t wds[2][8];
+  load_code_words4<K_, V_>(wds, Sq);
+
+  if (colt) {
+    sh.skl[cv] = scv;
+    f32x4 u;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) u[a] = a < R ? uqv[a] : 0.f;
+    sh.uoc[cv] = u;
+  } else {
+    sh.svr[cv] = scv * (pn / qmax);                                                   // kernels.py:1483
+    f32x4 o;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      o[a] = a < R ? uqv[a] : 0.f;
+      sh.qT[a][cv] = f2h(a < R ? hround(q0v[a]) : 0.f);                             // kernels.py:1573-1577
+    }
+    sh.qov[cv] = o;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
+  __syncthreads();
+
+  // ---- stage 2: B = deq(S0) pn + window, fp16 (kernels.py:1483-1571); the window half by half ----
+  f16x4 bh[2][8];                                     // B packed, fp16 (tile layout, k = c for the MFMAs)
+  {
+    Tile4 t;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) t.a[g][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    store_half(sh, win, L, 0);
+    __syncthreads();
+    rebuild_half4(t, sh.op[0], sh.op[1]);
+    rebuild_half4(t, sh.op[0], sh.op[2]);
+    if (two) {
+      // the second half's rows are loaded only now: held across the first half's products they would push the
+      // code words (live from stage 1 to the end of the rebuild) out of the 128 registers
+      load_half<K_, V_>(win, st, slot, hv, L, 1);
+      __syncthreads();                                // every wave is past the first half's operands
+      store_half(sh, win, L, 1);
+      __syncthreads();
+      rebuild_half4(t, sh.op[0], sh.op[1]);
+      rebuild_half4(t, sh.op[0], sh.op[2]);
+    }
+    tile_add_words4(t, wds, sh.svr, sh.skl);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) bh[g][nt] = pinned(to_h4(t.a[g][nt]));   // the fp16 rounding of B
+  }
+  __syncthreads();                                    // every wave is past the rebuild: the operand region is free
+  if (colt) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) sh.r.uoT[a][cv] = f2h(sh.uoc[cv][a]);
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) sh.r.qoT[a][cv] = f2h(sh.qov[cv][a]);
+  }
+  __syncthreads();
+
+  // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
+  f32x4 p16[2];
+  p_step4(sh, bh, pn, R, p16);                        // P16 rows of this wave's channels (lanes < 16)
+  if (q == 0) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 16 * g + l16] = f2h(p16[g][r]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  {                                                   // Q^T partial over the wave's 32 channels
+    const f16x4 z4 = {};
+    f16x4 ap[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) ap[g] = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][32 * w + 16 * g + 4 * q] : z4;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      f32x4 d = mma16(ap[0], bh[0][nt], f32x4{0.f, 0.f, 0.f, 0.f});
+      d = mma16(ap[1], bh[1][nt], d);
+      if (q == 0) sh.r.qpart[w][16 * nt + l16] = d;
+    }
+  }
+  __syncthreads();
+  if (tid < VD) {                                     // waves 0 and 1: one row v per thread
+    // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels
+    const f16x8 z8 = {};
+    f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.r.uoT[l16][32 * ks + 8 * q] : z8;
+      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
+      macc = mma32(ao, bp, macc);
+    }
+    float M2[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    const int v = tid;
+    f32x4 s = sh.r.qpart[0][v];
+#pragma unroll
+    for (int w2 = 1; w2 < NW4; ++w2) s += sh.r.qpart[w2][v];
+    const f32x4 qo = sh.qov[v];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += pn * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
+    sh.qv[v] = s;
+  }
+  __syncthreads();
+  if (w == 0) {                                       // CholeskyQR2, fp16 Q (kernels.py:1778-1835)
+    __builtin_amdgcn_s_setprio(3);
+    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+    cholqr_pass(p0, p1);
+    cholqr_pass(p0, p1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = r < R ? hround(p0[r]) : 0.f;
+      p1[r] = r < R ? hround(p1[r]) : 0.f;
+      sh.qT[r][l] = f2h(p0[r]);
+      sh.qT[r][l + 64] = f2h(p1[r]);
+    }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+  f32x4 u16[2];
+  p_step4(sh, bh, pn, R, u16);                        // U16 = P step with Q16 (lanes < 16)
+
+  // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
+  Tile4 t;
+  {
+    const f16x4 z4 = {};
+    f16x4 auo[2], aun[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      auo[g] = q == 0 ? to_h4(sh.uoc[32 * w + 16 * g + l16]) : z4;                  // A[c][a] = U_old
+      aun[g] = q == 0 ? to_h4(-u16[g]) : z4;                                        // A[c][r] = -U16
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                              // B[a][v] = Q_old^T
+      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                               // B[r][v] = Q16^T
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        f32x4 e = from_h4(bh[g][nt]) * rpn;
+        e = mma16(auo[g], bqo, e);
+        e *= pn;
+        e = mma16(aun[g], bqn, e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.a[g][nt][i] = hround(e[i]);
       }
-      const unsigned long long m = __ballot(due);
-      if (threadIdx.x == 0) sh.due = m;
-    }
-    __syncthreads();
-    unsigned long long m = sh.due;
-    __syncthreads();
-    while (m) {
-      const int b = __ffsll((long long)m) - 1;
-      m &= m - 1;
-      const int p = base + stride * b;
-      const int n = p / HV, hv = p - n * HV;
-      flush_head<KDA, K_, V_>(sh, st, Q0, idx[n], hv, qmax);
     }
   }
-  if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
-    __syncthreads();
-    if (threadIdx.x == 0 && atomicAdd(st.ctl + 1, 1) == (int)gridDim.x - 1) {
-      __atomic_store_n(st.ctl, 0, __ATOMIC_RELAXED);
-      __atomic_store_n(st.ctl + 1, 0, __ATOMIC_RELAXED);
+
+  // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
+  float rsk[2][4];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    float cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[g][nt][i]);
+      cs[i] = sum16(x);
+    }
+    // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
+    const int ic = l & 3;
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
+    const float sq = sqrtf(msum);
+    const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
+    const int cc = 32 * w + 16 * g + 4 * q + l16;
+    if (l16 < 4 && (K_ == KD || cc < K_)) Sk[cc] = fmaxf(sq, LQ_EPS);
+    rsk[g][0] = dpp<0x00>(rs);                        // quad_perm [i, i, i, i]: column i of the lane's quad
+    rsk[g][1] = dpp<0x55>(rs);
+    rsk[g][2] = dpp<0xaa>(rs);
+    rsk[g][3] = dpp<0xff>(rs);
+  }
+  // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    float m = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        t.a[g][nt][i] *= rsk[g][i];
+        m = fmaxf(m, fabsf(t.a[g][nt][i]));
+      }
+    sh.r.rmx[4 * w + q][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  if (tid < VD) {
+    float m = sh.r.rmx[0][tid];
+#pragma unroll
+    for (int k = 1; k < 4 * NW4; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
+    const float rmax = fmaxf(m, LQ_EPS);
+    if (V_ == VD || tid < V_) Sv[tid] = rmax;
+    sh.r.rq[tid] = qmax * (1.0f / rmax);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + l16;
+    const float rq = sh.r.rq[v];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      uint32_t b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[g][nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+      const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+      const int c = 32 * w + 16 * g + 4 * q;
+      if ((K_ == KD || c < K_) && (V_ == VD || v < V_))
+        *(uint32_t*)(Sq + v * K_ + c) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
   }
+  // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
+  if (q == 0) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int c = 32 * w + 16 * g + l16;
+      if (K_ == KD || c < K_)
+        for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16[g][r]);
+    }
+  }
+  if (tid < V_) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+  }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+  __syncthreads();                                    // LDS reuse by the next head of this workgroup
+}
+
+template <int K_ = KD, int V_ = VD>
+__global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
+void flush4_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
+                   int* dlist) {
+  __shared__ FlushShared4 sh;
+  auto head = [&](int slot, int hv) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax); };
+  if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
+  else flush_scan(sh.due, st, idx, N, head);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1305,8 +1791,9 @@ int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, 
   if (N == 0) return LQ_OK;
   const int total = N * st->HV;
   const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
+  const dim3 g4((unsigned)(total < 4 * num_cus() ? total : 4 * num_cus()));  // four-wave flush: four per CU
   if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if (st->K == KD) flush_kernel<false><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if (st->K == KD) flush4_kernel<><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
