@@ -97,6 +97,15 @@ int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream);
  * reference as one call: replaces vLLM's causal_conv1d_update (leapquant/vllm/gdn.py:32) followed by the step. */
 int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream);
 
+/* GDN decode call: the step of every row (with vLLM's conv1d update fused in when cv is not NULL, as in
+ * lq_gdn_step_conv), then the end-of-window flush of the heads whose window it filled (codes in [-qmax, qmax],
+ * qmax = st->qmax, 0 meaning 127) -- what lq_gdn_step (or lq_gdn_step_conv) followed by lq_flush computes, in one
+ * call.  Replaces make_gdn_step(...)(...) followed by make_flush(...)(...) as LeapQuantState.decode launches them
+ * (/root/reference/leapquant/state.py:99-116; kernels.py:27-692, 1077-2033).  For (K, V) = (128, 128) and HV = 2 H it
+ * is one launch: each step workgroup flushes the heads it has just filled (or found full) on the same threads; other
+ * shapes run the step and the flush as two launches.  Same limits as lq_gdn_step and lq_flush. */
+int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0, void* stream);
+
 /* KDA decode step (per-key-channel gate).  glb != 0: GLM's bounded gate glb * sigmoid(exp(A_log) (a + dt_bias));
  * glb == 0: Kimi's -exp(A_log) softplus(a + dt_bias).
  * Replaces make_kda_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ,

@@ -1,0 +1,1148 @@
+// Per-head flush core shared by liblq's kernels: the end-of-window flush of one (slot, head) on the matrix cores, in
+// an eight-wave (flush_head) and a four-wave (flush_head4) layout, with the helpers the standalone quantize, dequant
+// and low-rank kernels also use.  Semantics: /root/reference/leapquant/kernels.py:1077-2033 (flush).
+//
+// The head's 128 x 128 matrix lives in registers in the accumulator layout of v_mfma_f32_16x16x32_bf16: wave w owns
+// key channels c in [16w, 16w + 16), lane l holds
+//     acc[nt][i] = M[c][v],   c = 16 w + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
+// The window rebuild (a rank-L GEMM, ~29 flop/byte at L = 64) runs on MFMA with bf16 hi/lo operands exactly where the
+// reference splits.  The flush's rebuilt matrix B is fp16-exact, so every 128-long contraction of the subspace step
+// (P = B^T Q, Q = B P, the R x R Gram corrections, the rank-R residual updates) is an fp16 MFMA with fp32 accumulation
+// over operands held in registers: the packed tile itself is the B operand of v_mfma_f32_16x16x16_f16 (k = c), and one
+// MFMA against the identity gives the transposed packing (k = v).
+#pragma once
+#include "lq_common.h"
+
+namespace {
+namespace lqf {
+
+
+constexpr int KD = 128, VD = 128;
+constexpr int LPMAX = 64;            // largest window
+constexpr int OPS = LPMAX + 8;       // operand row stride (bf16): 144 B rows
+constexpr int FT = 512;              // threads per workgroup
+constexpr int NW = FT / 64;          // waves
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// D = A B + C over 16 x 16 blocks.  16x16x16: lane l holds A[l & 15][4 (l >> 4) + i] and B[4 (l >> 4) + i][l & 15];
+// 16x16x32: the same with 8 (l >> 4) + i; D (both): lane l holds D[4 (l >> 4) + i][l & 15], i < 4.
+__device__ __forceinline__ f32x4 mma16(f16x4 a, f16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma32(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f16x4 to_h4(f32x4 x) {
+  return f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
+}
+__device__ __forceinline__ f32x4 from_h4(f16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
+// The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
+// redo the conversion where the value is used (twice the registers).
+__device__ __forceinline__ f16x4 pinned(f16x4 x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+struct Tile {
+  f32x4 a[8];
+};
+
+struct FlushShared {
+  union {
+    bf16_t op[3][KD][OPS];     // rebuild operands [c or v][j]
+    struct {                   // after the rebuild
+      f32x4 qpart[NW][VD];     // per-wave partial Q rows
+      float rmx[4 * NW][VD];   // per-(wave, lane group) row maxima of the scaled residual
+      float rq[VD];            // qmax / row scale
+      f16_t ppT[4][KD];        // P16^T
+    } r;
+  };
+  float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
+  float svr[VD];               // row factor of the dequant (Sv pn / qmax, KDA: Sv / qmax)
+  float w[LPMAX];
+  f32x4 uoc[KD];               // old U rows [c][a] (KDA: fp16(U pc)), a >= R zero
+  f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
+  f16_t uoT[4][KD];            // the same, fp16 transposed (MFMA operands)
+  f16_t qoT[4][VD];
+  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
+  unsigned long long due;      // persistent flush: due mask of the current candidate chunk
+};
+
+// Thread index as seen by the per-head code.  Re-read through an empty asm at the start of every head so that the
+// persistent flush loop cannot hoist the ~100 per-lane LDS addresses derived from it (and keep them all live).
+__device__ __forceinline__ int opaque_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+__device__ __forceinline__ int lane_id() { return opaque_tid() & 63; }
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(opaque_tid() >> 6); }
+
+// wave-uniform reductions: DPP within each 16-lane row, then the 4 row results through readlane (no LDS traffic)
+__device__ __forceinline__ float rl(float x, int l) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x), l));
+}
+// wave all-reduce for the serial factor steps (MGS, CholeskyQR): VALU lane swaps, every lane gets the result
+__device__ __forceinline__ float sum64u(float x) { return sum64(x); }
+
+// fn(i, s): s[r] = sum_v M[c_i][v] X[v][r] for the lane's 4 key channels c_i = 16 w + 4 (l >> 4) + i (complete in
+// every lane of the 16-lane row)
+template <class F>
+__device__ __forceinline__ void colred(const Tile& t, const f32x4* X, F fn) {
+  const int l = lane_id();
+  f32x4 acc[4] = {};                                  // one row of X at a time (the sums keep the order of the rows)
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const f32x4 xv = X[16 * nt + (l & 15)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m = t.a[nt][i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(m, xv[r], acc[i][r]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    f32x4 s;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = sum16(acc[i][r]);
+    fn(i, s);
+  }
+}
+
+// part[w][v][r] = sum over this wave's 16 channels c of M[c][v] Y[c][r]  (caller sums the NW waves)
+__device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*part)[VD]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  f32x4 yc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) yc[i] = Y[16 * w + 4 * q + i];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float m = t.a[nt][i];
+      s[0] = fmaf(m, yc[i][0], s[0]);
+      s[1] = fmaf(m, yc[i][1], s[1]);
+      s[2] = fmaf(m, yc[i][2], s[2]);
+      s[3] = fmaf(m, yc[i][3], s[3]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      s[r] = xor32_sum(xor16_sum(s[r]));
+    }
+    if (q == 0) part[w][16 * nt + (l & 15)] = s;
+  }
+}
+
+// CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835) on the 2 rows a lane of wave 0 holds
+__device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
+  float gg[10];
+  int k = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
+  float ll[10];
+  ll[0] = rsqrtf_rn(fmaxf(gg[0], 1e-30f));
+  ll[1] = gg[1] * ll[0];
+  ll[2] = rsqrtf_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
+  ll[3] = gg[3] * ll[0];
+  ll[4] = (gg[4] - ll[3] * ll[1]) * ll[2];
+  ll[5] = rsqrtf_rn(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
+  ll[6] = gg[6] * ll[0];
+  ll[7] = (gg[7] - ll[6] * ll[1]) * ll[2];
+  ll[8] = (gg[8] - ll[6] * ll[3] - ll[7] * ll[4]) * ll[5];
+  ll[9] = rsqrtf_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    f32x4& p = s ? p1 : p0;
+    p[0] = p[0] * ll[0];
+    p[1] = (p[1] - p[0] * ll[1]) * ll[2];
+    p[2] = (p[2] - p[0] * ll[3] - p[1] * ll[4]) * ll[5];
+    p[3] = (p[3] - p[0] * ll[6] - p[1] * ll[7] - p[2] * ll[8]) * ll[9];
+  }
+}
+
+// modified Gram-Schmidt on the R columns of the 128 x 4 matrix whose rows l, l + 64 a lane of wave 0 holds
+// (kernels.py:2170-2183, 2190-2203)
+__device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {               // unrolled over the largest rank (no run-time register indexing)
+    if (j < R) {
+#pragma unroll
+      for (int c = 0; c < j; ++c) {
+        const float sc = sum64u(fmaf(p0[c], p0[j], p1[c] * p1[j]));
+        p0[j] = p0[j] - sc * p0[c];
+        p1[j] = p1[j] - sc * p1[c];
+      }
+      const float nrm = sum64u(fmaf(p0[j], p0[j], p1[j] * p1[j]));
+      const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
+      p0[j] *= rs;
+      p1[j] *= rs;
+    }
+  }
+}
+
+// the 8 code words of the lane's tile entries (issued early; consumed by tile_add_words).  A head of K_ x V_ < 128 x
+// 128 sits zero-padded in the tile: entries past its rows / columns read as 0 (clamped addresses, no divergent load).
+template <int K_ = KD, int V_ = VD>
+__device__ __forceinline__ void load_code_words(uint32_t wds[8], const int8_t* Sq) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  const int c = 16 * w + 4 * q;
+  const bool cok = K_ == KD || c < K_;
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + (l & 15);
+    const uint32_t x = *(const uint32_t*)(Sq + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
+    wds[nt] = (cok && (V_ == VD || v < V_)) ? x : 0u;
+  }
+}
+// t += the dequantised checkpoint codes  x svr[v] x skl[c], each term rounded to fp32 before the add.  The flush adds
+// them after the window's MFMA products, which it accumulates from zero: the window terms are up to ~20x larger than
+// their sum (they cancel), and an accumulator seeded with the checkpoint term rounds them at a coarser step.
+__device__ __forceinline__ void tile_add_words(Tile& t, const uint32_t wds[8], const float* svr, const float* skl) {
+#pragma clang fp contract(off)
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  const int c0 = 16 * w + 4 * q;
+  float kc[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const float rv = svr[16 * nt + (l & 15)];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t.a[nt][i] = t.a[nt][i] + ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * rv) * kc[i];
+  }
+}
+
+// acc[c][v] += sum_j A[c][j] B[v][j] over nks 32-entry steps (bf16 operands from LDS, fp32 accumulate)
+__device__ __forceinline__ void rebuild_mfma(Tile& t, const bf16_t (*A)[OPS], const bf16_t (*B)[OPS], int nks) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  for (int ks = 0; ks < nks; ++ks) {
+    const bf16x8 af = *(const bf16x8*)&A[16 * w + (l & 15)][32 * ks + 8 * q];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const bf16x8 bfr = *(const bf16x8*)&B[16 * nt + (l & 15)][32 * ks + 8 * q];
+      t.a[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, t.a[nt], 0, 0, 0);
+    }
+  }
+}
+
+// Window rows of one head, loaded up front (unconditional, clamped addresses; rows >= h and the padding to LP carry
+// zero weight).  Thread t takes the row pair (2 jp, 2 jp + 1), jp = t % (LP / 2), in the 8-column chunk t / (LP / 2)
+// (16 chunks; LP = 64 keeps every thread busy), so that each LDS write below holds two entries.  KDA also takes the
+// window's per-channel decays (Gbuf, same [j][c] layout as the keys).
+struct WinRegs {
+  uint4 k[2], u[2], g[2];
+};
+__device__ __forceinline__ int win_pair(int LP) { return opaque_tid() % (LP / 2); }
+__device__ __forceinline__ int win_chunk(int LP) { return opaque_tid() / (LP / 2); }
+template <bool KDA, int K_ = KD, int V_ = VD>
+__device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int slot, int hv, int h, int LP) {
+  const int G = st.HV / st.H, hk = hv / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
+  const f16_t* Gb = KDA ? (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD : nullptr;
+  const int jp = win_pair(LP), c8 = min(win_chunk(LP), 15) * 8;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);       // columns past a K_ / V_ < 128 head: zero operands
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = 2 * jp + k, jr = j < h ? j : 0;
+    const uint4 kx = *(const uint4*)(Kb + (long long)jr * K_ + (K_ == KD ? c8 : min(c8, K_ - 8)));
+    const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
+    r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
+    r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
+    if (KDA) r.g[k] = *(const uint4*)(Gb + (long long)jr * KD + c8);
+  }
+}
+// Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write.  GDN: op0 =
+// K_j[c], op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 = raw K_j[c] / e_j[c] (turned
+// into the decayed key operands by kda_key_scan), op2 = u_j[v].  Rows j >= h carry zero values and, for KDA, decay 1.
+template <bool KDA>
+__device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP) {
+  const int ch = win_chunk(LP);
+  if (ch >= 16) return;
+  const int j0 = 2 * win_pair(LP), c8 = ch * 8;
+  const bool v0 = j0 < h, v1 = j0 + 1 < h;
+  const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
+  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+  const uint32_t ga[4] = {r.g[0].x, r.g[0].y, r.g[0].z, r.g[0].w}, gb[4] = {r.g[1].x, r.g[1].y, r.g[1].z, r.g[1].w};
+  const uint32_t keep = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = e >> 1;
+    const bool odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
+    uint32_t* o0 = (uint32_t*)&sh.op[0][c8 + e][j0];
+    uint32_t* o1 = (uint32_t*)&sh.op[1][c8 + e][j0];
+    uint32_t* o2 = (uint32_t*)&sh.op[2][c8 + e][j0];
+    *o0 = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    if (!KDA) {
+      // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
+#pragma clang fp contract(off)
+      const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
+      const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+      const uint32_t hi = pk_bf16(wu0, wu1);
+      *o1 = hi;
+      *o2 = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+    } else {
+      *o1 = (__builtin_amdgcn_perm(gb[x], ga[x], sel) & keep) | (0x3c003c00u & ~keep);   // rows >= h: decay 1
+      *o2 = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
+    }
+  }
+}
+// KDA key operands, in place over the raw keys op[0] and decays op[1] ([c][j]): op[0..NT-1] = the NT-term bf16 split
+// (hi, [mid,] lo) of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, state.py:124-127).
+// Four lanes per channel: lane s of a quad takes the s-th quarter of the window (LP / 4 = 8 or 16 entries, held in
+// registers) and walks it backwards.  The decay product it starts from, D at the top of its quarter, is the running
+// product of the later decays taken in the reference's own order (from the window's end down, one rounding per factor),
+// so every D_j is bit-identical to the sequential walk's: a product regrouped by quarters rounds differently, and the
+// key operands' cancellation in the rebuild turns those last-bit differences into fp16 flips of B.  The prefix costs a
+// lane up to 3 LP / 4 dependent multiplies; the per-entry split work stays divided four ways.  FT = 4 KD threads.
+template <int NT>
+__device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float* wj, int h, int LP) {
+  static_assert(FT == 4 * KD, "one quad of lanes per channel");
+  const int tid = opaque_tid(), c = tid >> 2, s = tid & 3, seg = LP >> 2, jb = s * seg;
+  uint32_t ku[2][4], eu[2][4];
+#pragma unroll
+  for (int x = 1; x >= 0; --x) {
+    if (8 * x < seg) {
+      const uint4 kr = *(const uint4*)&op[0][c][jb + 8 * x];
+      const uint4 er = *(const uint4*)&op[1][c][jb + 8 * x];
+      ku[x][0] = kr.x; ku[x][1] = kr.y; ku[x][2] = kr.z; ku[x][3] = kr.w;
+      eu[x][0] = er.x; eu[x][1] = er.y; eu[x][2] = er.z; eu[x][3] = er.w;
+    }
+  }
+  float dcur = 1.0f;
+#pragma unroll
+  for (int sq = 3; sq >= 1; --sq) {                   // the later quarters, last first
+    const int q0 = sq * seg;
+    if (q0 < h) {                                     // rows >= h hold decay 1 (exact factors)
+      float t = dcur;
+#pragma unroll
+      for (int x = 1; x >= 0; --x) {
+        if (8 * x < seg) {
+          const uint4 er = *(const uint4*)&op[1][c][q0 + 8 * x];
+          const uint32_t ew[4] = {er.x, er.y, er.z, er.w};
+#pragma unroll
+          for (int e = 7; e >= 0; --e) t = t * h2f((f16_t)(ew[e >> 1] >> (16 * (e & 1))));
+        }
+      }
+      dcur = s < sq ? t : dcur;
+    }
+  }
+#pragma unroll
+  for (int x = 1; x >= 0; --x) {
+    if (8 * x < seg) {
+      const int j0 = jb + 8 * x;
+      uint32_t tw[NT][4] = {};
+#pragma unroll
+      for (int e = 7; e >= 0; --e) {
+        const int j = j0 + e;
+        if (j < h) {
+          // the split is of the fp32-rounded product (kernels.py:1456-1463): no fusing into the first subtraction
+#pragma clang fp contract(off)
+          float r = bf2f((bf16_t)(ku[x][e >> 1] >> (16 * (e & 1)))) * (wj[j] * dcur);
+#pragma unroll
+          for (int t = 0; t < NT; ++t) {
+            const bf16_t b = f2bf(r);
+            tw[t][e >> 1] |= (uint32_t)b << (16 * (e & 1));
+            r = r - bf2f(b);
+          }
+          dcur = dcur * h2f((f16_t)(eu[x][e >> 1] >> (16 * (e & 1))));
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < NT; ++t) *(uint4*)&op[t][c][j0] = make_uint4(tw[t][0], tw[t][1], tw[t][2], tw[t][3]);
+    }
+  }
+}
+
+// per-wave partial sums of the row reductions -> the full sum for row v (threads v < 128)
+__device__ __forceinline__ f32x4 sum_parts(const f32x4 (*part)[VD], int v) {
+  f32x4 s = part[0][v];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) s += part[w][v];
+  return s;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// flush (kernels.py:1077-2033): one due (slot, head)
+// ------------------------------------------------------------------------------------------------------------------
+// P = B^T Q + pn U_old (Q_old^T Q) for this wave's 16 key channels, fp16-rounded (kernels.py:1580-1700).  Q^T comes
+// from sh.qT; bt[nt] is the transposed packing of B (lane l: B[16 w + (l & 15)][16 nt + 4 (l >> 4) + i]).  Lanes
+// l < 16 return P[16 w + l][0..3] (zero for r >= R); the other lanes return zeros.
+__device__ __forceinline__ f32x4 p_step(const FlushShared& sh, const f16x4 bt[8], float pn, int R) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x8 z8 = {};
+  const f16x4 z4 = {};
+  // M[a][r] = sum_v Q_old[v][a] Q[v][r]: lanes l < 4 hold column r = l
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 ao = rl4 ? *(const f16x8*)&sh.qoT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
+    macc = mma32(ao, bq, macc);
+  }
+  // P^T[r][c] = sum_v Q^T[r][v] B[c][v]  (k = v from the transposed packing)
+  f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+    pacc = mma16(aq, bt[nt], pacc);
+  }
+  float M[4][4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+  const f32x4 uo = sh.uoc[16 * w + l16];
+  f32x4 p;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
+    p[r] = (q == 0 && r < R) ? hround(pacc[r] + pn * corr) : 0.f;
+  }
+  return p;
+}
+
+// A GDN head of K_ x V_ < 128 x 128 (kernels.py:1089: (64, 128), (64, 64)) runs zero-padded in the 128 x 128 tile:
+// its loads read zeros past its rows / columns, every product and Gram sum then only adds exact zeros, the column
+// means divide by V_, and the stores write its own rows / columns only.
+template <bool KDA, int K_ = KD, int V_ = VD>
+__device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+                           float qmax) {
+  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
+  const int HV = st.HV, L = st.L, R = st.R;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
+  char* base = block_base(st, slot, hv);
+  int8_t* Sq = (int8_t*)base;
+  float* Sk = (float*)(base + V_ * K_);
+  float* Sv = Sk + K_;
+  f16_t* UQ = (f16_t*)(Sv + V_);
+  const int LP = (L + 31) & ~31;
+
+  // ---- stage 1: every load of the head up front (scalars, scales, factors, window rows, code words) ----
+  float pn = 1.f, rpn = 1.f;
+  if (!KDA) {
+    pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);               // kernels.py:1471
+    rpn = 1.0f / pn;                                  // kernels.py:1477
+  }
+  const int cv = tid & 127;                           // column (tid < 128) or row (128 <= tid < 256) of the stage-1 loads
+  const bool colt = tid < KD;
+  const int nc = colt ? K_ : V_;                      // this thread's column / row count
+  const bool cok = (K_ == KD && V_ == VD) || cv < nc;
+  const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
+  const int vq = V_ == VD ? cv : min(cv, V_ - 1);
+  const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
+  float uqv[4], q0v[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
+    uqv[a] = cok ? x : 0.f;
+    const float y = Q0[vq * R + min(a, R - 1)];
+    q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
+  }
+  const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinRegs win;
+  load_window<KDA, K_, V_>(win, st, slot, hv, L, LP);
+  uint32_t wds[8];
+  load_code_words<K_, V_>(wds, Sq);
+
+  if (tid < KD) {
+    const int c = cv;
+    float pcv = 1.f;
+    if (KDA) pcv = expf(pbc);                                                          // kernels.py:1451
+    sh.skl[c] = KDA ? scv * pcv : scv;                                                // kernels.py:1519
+    f32x4 u;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      u[a] = a < R ? uqv[a] : 0.f;
+      if (KDA) u[a] = hround(u[a] * pcv);                                             // kernels.py:1464-1465
+      sh.uoT[a][c] = f2h(u[a]);
+    }
+    sh.uoc[c] = u;
+  } else if (tid < KD + VD) {
+    const int v = cv;
+    sh.svr[v] = KDA ? scv * (1.0f / qmax) : scv * (pn / qmax);                       // kernels.py:1468, 1483
+    f32x4 o;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      o[a] = a < R ? uqv[a] : 0.f;
+      sh.qoT[a][v] = f2h(o[a]);
+      sh.qT[a][v] = f2h(a < R ? hround(q0v[a]) : 0.f);                                // kernels.py:1573-1577
+    }
+    sh.qov[v] = o;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
+  __syncthreads();
+  store_window<KDA>(sh, win, L, LP);
+  __syncthreads();
+  if (KDA) {
+    kda_key_scan<2>(sh.op, sh.w, L, LP);
+    __syncthreads();
+  }
+
+  // ---- stage 2: B = deq(S0) (+ decay) + window, fp16 (kernels.py:1483-1571) ----
+  f16x4 bh[8], bt[8];                                 // B packed: k = c (tile layout) and k = v (transposed)
+  {
+    Tile t;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!KDA) {
+      rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+    } else {
+      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+      rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
+    }
+    tile_add_words(t, wds, sh.svr, sh.skl);
+    f16x4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      bh[nt] = to_h4(t.a[nt]);                        // the fp16 rounding of B
+      bt[nt] = to_h4(mma16(bh[nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));   // exact: B^T block through the identity
+    }
+  }
+
+  // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
+  const f32x4 p16 = p_step(sh, bt, pn, R);            // P16 rows of this wave (lanes < 16)
+  __syncthreads();                                    // every wave is past the rebuild: the op region is free
+  // Q = B P16 + pn Q_old (U_old^T P16): per-wave partials of B P16 over the wave's 16 channels, summed below
+  if (q == 0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) sh.r.ppT[r][16 * w + l16] = f2h(p16[r]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  {
+    const f16x4 z4 = {};
+    const f16x4 ap = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][16 * w + 4 * q] : z4;   // A[r][c] = P16^T
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const f32x4 d = mma16(ap, bh[nt], f32x4{0.f, 0.f, 0.f, 0.f});                 // Q^T[r][16 nt + l]
+      if (q == 0) sh.r.qpart[w][16 * nt + l16] = d;
+    }
+  }
+  __syncthreads();
+  if (tid < VD) {                                     // waves 0 and 1: one row v per thread
+    // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels (every column of P16 is in ppT now)
+    const f16x8 z8 = {};
+    f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.uoT[l16][32 * ks + 8 * q] : z8;
+      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
+      macc = mma32(ao, bp, macc);
+    }
+    float M2[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    const int v = tid;
+    f32x4 s = sum_parts(sh.r.qpart, v);
+    const f32x4 qo = sh.qov[v];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += pn * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
+    sh.qv[v] = s;
+  }
+  __syncthreads();
+  // CholeskyQR2 (wave 0), fp16 Q.  The serial phases of one wave run at raised wave priority: the CU's other workgroup
+  // competes for the same SIMDs while this one's other waves wait at the barrier (config 3: flush 339 -> 331 us,
+  // quantize 222 -> 214 us with the same in its MGS phases)
+  if (w == 0) {
+    __builtin_amdgcn_s_setprio(3);
+    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+    cholqr_pass(p0, p1);
+    cholqr_pass(p0, p1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = r < R ? hround(p0[r]) : 0.f;
+      p1[r] = r < R ? hround(p1[r]) : 0.f;
+      sh.qT[r][l] = f2h(p0[r]);
+      sh.qT[r][l + 64] = f2h(p1[r]);
+    }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+  const f32x4 u16 = p_step(sh, bt, pn, R);            // U16 = P step with Q16 (lanes < 16: rows 16 w + l)
+
+  // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
+  Tile t;
+  {
+    const f16x4 z4 = {};
+    const f16x4 auo = q == 0 ? to_h4(sh.uoc[16 * w + l16]) : z4;                     // A[c][a] = U_old
+    const f16x4 aun = q == 0 ? to_h4(-u16) : z4;                                     // A[c][r] = -U16
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                               // B[a][v] = Q_old^T
+      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                                // B[r][v] = Q16^T
+      f32x4 e = from_h4(bh[nt]);
+      if (!KDA) e *= rpn;
+      e = mma16(auo, bqo, e);
+      if (!KDA) e *= pn;
+      e = mma16(aun, bqn, e);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(e[i]);
+    }
+  }
+
+  // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
+  float rsk[4];
+  {
+    float cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[nt][i]);
+      cs[i] = sum16(x);
+    }
+    // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
+    const int ic = l & 3;
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
+    const float sq = sqrtf(msum);
+    const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
+    if (l16 < 4 && (K_ == KD || 16 * w + 4 * q + l16 < K_)) Sk[16 * w + 4 * q + l16] = fmaxf(sq, LQ_EPS);
+    rsk[0] = dpp<0x00>(rs);                           // quad_perm [i, i, i, i]: column i of the lane's quad
+    rsk[1] = dpp<0x55>(rs);
+    rsk[2] = dpp<0xaa>(rs);
+    rsk[3] = dpp<0xff>(rs);
+  }
+  // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      t.a[nt][i] *= rsk[i];
+      m = fmaxf(m, fabsf(t.a[nt][i]));
+    }
+    sh.r.rmx[4 * w + q][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  if (tid < VD) {
+    float m = sh.r.rmx[0][tid];
+#pragma unroll
+    for (int k = 1; k < 4 * NW; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
+    const float rmax = fmaxf(m, LQ_EPS);
+    if (V_ == VD || tid < V_) Sv[tid] = rmax;
+    sh.r.rq[tid] = qmax * (1.0f / rmax);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + l16;
+    const float rq = sh.r.rq[v];
+    uint32_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+    if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_))
+      *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
+  if (q == 0 && (K_ == KD || 16 * w + l16 < K_)) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + 16 * w + l16] = f2h(u16[r]);
+  }
+  if (tid < V_) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+  }
+  if (KDA) {
+    if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
+    uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
+    for (int i = tid; i < L * KD / 8; i += FT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    if (!KDA) st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+  __syncthreads();                                    // LDS reuse by the next head of this workgroup
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Four-wave GDN flush: one due head per workgroup of 256 threads, <= 40 KiB LDS and <= 128 VGPRs, so that four heads
+// share a CU (the eight-wave flush above fits two).  The flush is latency-bound -- each head is a chain of dependent,
+// barrier-separated phases -- so heads in flight per CU set its rate.  Same arithmetic, in the same order, as
+// flush_head; only the distribution over the lanes differs: wave w owns key channels [32 w, 32 w + 32) as two groups
+// g of 16, and lane l holds
+//     a[g][nt][i] = M[c][v],   c = 32 w + 16 g + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
+// The window is staged and multiplied in halves of 32 entries.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int FT4 = 256;             // threads per workgroup
+constexpr int NW4 = FT4 / 64;        // waves
+constexpr int HALF = 32;             // window entries staged at once
+constexpr int OPS4 = HALF + 8;       // operand row stride (bf16): 80 B rows, 16-byte aligned, conflict-free b128 reads
+
+struct Tile4 {
+  f32x4 a[2][8];
+};
+
+struct FlushShared4 {
+  union {
+    bf16_t op[3][KD][OPS4];    // rebuild operands of one window half [c or v][j]
+    struct {                   // after the rebuild
+      f32x4 qpart[NW4][VD];    // per-wave partial Q rows
+      float rmx[4 * NW4][VD];  // per-(wave, lane group) row maxima of the scaled residual
+      float rq[VD];            // qmax / row scale
+      f16_t ppT[4][KD];        // P16^T
+      f16_t uoT[4][KD];        // old U^T, fp16 (MFMA operand)
+      f16_t qoT[4][VD];        // old Q^T, fp16
+    } r;
+  };
+  float skl[KD];               // column factor of the dequant (Sk)
+  float svr[VD];               // row factor of the dequant (Sv pn / qmax)
+  float w[LPMAX];
+  f32x4 uoc[KD];               // old U rows [c][a], a >= R zero
+  f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
+  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
+  unsigned long long due;      // persistent flush: due mask of the current candidate chunk / listed head
+};
+static_assert(sizeof(FlushShared4) <= 40960, "four workgroups per CU: 160 KiB of LDS");
+
+// One window half's rows in registers: thread t takes entries 2 (t % 16), 2 (t % 16) + 1 of the half, columns
+// 8 (t / 16) .. 8 (t / 16) + 7 (16 x 16 = 256 threads).  Rows >= h read row 0 (in bounds; their weight is zero).
+struct WinHalf {
+  uint4 k[2], u[2];
+};
+template <int K_, int V_>
+__device__ __forceinline__ void load_half(WinHalf& r, const lq_state& st, int slot, int hv, int h, int hf) {
+  const int G = st.HV / st.H, hk = hv / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
+  const int t = opaque_tid(), jp = t % 16, c8 = (t / 16) * 8;
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);        // columns past a K_ / V_ < 128 head: zero operands
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = HALF * hf + 2 * jp + k, jr = j < h ? j : 0;
+    const uint4 kx = *(const uint4*)(Kb + (long long)jr * K_ + (K_ == KD ? c8 : min(c8, K_ - 8)));
+    const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
+    r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
+    r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
+  }
+}
+// Transposed into the rebuild operands [c or v][j - HALF hf], two entries per 32-bit LDS write: op0 = K_j[c],
+// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.
+__device__ __forceinline__ void store_half(FlushShared4& sh, const WinHalf& r, int h, int hf) {
+  // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
+#pragma clang fp contract(off)
+  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8;
+  const int j0 = HALF * hf + jl;
+  const bool v0 = j0 < h, v1 = j0 + 1 < h;
+  const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
+  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = e >> 1;
+    const bool odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
+    *(uint32_t*)&sh.op[0][c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
+    const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+    const uint32_t hi = pk_bf16(wu0, wu1);
+    *(uint32_t*)&sh.op[1][c8 + e][jl] = hi;
+    *(uint32_t*)&sh.op[2][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+  }
+}
+// acc[c][v] += sum_j A[c][j] B[v][j] over one staged half (bf16 operands, fp32 accumulate)
+__device__ __forceinline__ void rebuild_half4(Tile4& t, const bf16_t (*A)[OPS4], const bf16_t (*B)[OPS4]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  bf16x8 af[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) af[g] = *(const bf16x8*)&A[32 * w + 16 * g + (l & 15)][8 * q];
+#pragma unroll
+  for (int n2 = 0; n2 < 8; n2 += 2) {                 // two B fragments in flight at a time (register pressure)
+    const bf16x8 b0 = *(const bf16x8*)&B[16 * n2 + (l & 15)][8 * q];
+    const bf16x8 b1 = *(const bf16x8*)&B[16 * n2 + 16 + (l & 15)][8 * q];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b0, t.a[g][n2], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b1, t.a[g][n2 + 1], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+// the 16 code words of the lane's tile entries (zero past a K_ x V_ < 128 x 128 head's rows / columns)
+template <int K_, int V_>
+__device__ __forceinline__ void load_code_words4(uint32_t wds[2][8], const int8_t* Sq) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c = 32 * w + 16 * g + 4 * q;
+    const bool cok = K_ == KD || c < K_;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+      const uint32_t x = *(const uint32_t*)(Sq + (V_ == VD ? v : min(v, V_ - 1)) * K_ + (K_ == KD ? c : min(c, K_ - 4)));
+      wds[g][nt] = (cok && (V_ == VD || v < V_)) ? x : 0u;
+    }
+  }
+}
+// t += codes x svr[v] x skl[c], each term rounded to fp32 before the add (after the window products; see flush_head)
+__device__ __forceinline__ void tile_add_words4(Tile4& t, const uint32_t wds[2][8], const float* svr,
+                                                const float* skl) {
+#pragma clang fp contract(off)
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const int c0 = 32 * w + 16 * g + 4 * q;
+    float kc[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) kc[i] = skl[c0 + i];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const float rv = svr[16 * nt + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        t.a[g][nt][i] = t.a[g][nt][i] + ((float)(int)(int8_t)(wds[g][nt] >> (8 * i)) * rv) * kc[i];
+    }
+  }
+}
+// M[a][r] = sum_v Q_old[v][a] Q[v][r] (Q from sh.qT): every lane gets all 16 entries
+__device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4]) {
+  const int l = lane_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x8 z8 = {};
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 ao = rl4 ? *(const f16x8*)&sh.r.qoT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
+    macc = mma32(ao, bq, macc);
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+}
+// P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lanes
+// l < 16 return P[32 w + 16 g + l][0..3] (zero for r >= R) in p[g]; the other lanes zeros.  The contraction runs over
+// v, so each block of B is transposed on the way in (one exact MFMA against the identity: lane l then holds
+// B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]) rather than kept transposed in registers.
+__device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], float pn, int R,
+                                        f32x4 p[2]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  const bool rl4 = l16 < 4;
+  const f16x4 z4 = {};
+  float M[4][4];
+  gram_qold_q(sh, M);
+  f16x4 ident;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
+  f32x4 pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {                    // P^T[r][c] = sum_v Q^T[r][v] B[c][v] (k = v)
+    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const f16x4 bt = to_h4(mma16(bh[g][nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));
+      pacc[g] = mma16(aq, bt, pacc[g]);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    const f32x4 uo = sh.uoc[32 * w + 16 * g + l16];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
+      p[g][r] = (q == 0 && r < R) ? hround(pacc[g][r] + pn * corr) : 0.f;
+    }
+  }
+}
+
+template <int K_ = KD, int V_ = VD>
+__device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+                            float qmax) {
+  const int HV = st.HV, L = st.L, R = st.R;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
+  char* base = block_base(st, slot, hv);
+  int8_t* Sq = (int8_t*)base;
+  float* Sk = (float*)(base + V_ * K_);
+  float* Sv = Sk + K_;
+  f16_t* UQ = (f16_t*)(Sv + V_);
+  const bool two = L > HALF;                          // window halves
+
+  // ---- stage 1: every load of the head up front ----
+  const float pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);     // kernels.py:1471
+  const float rpn = 1.0f / pn;                        // kernels.py:1477
+  const int cv = tid & 127;                           // column (tid < 128) or row of the stage-1 loads
+  const bool colt = tid < KD;
+  const int nc = colt ? K_ : V_;
+  const bool cok = (K_ == KD && V_ == VD) || cv < nc;
+  const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
+  const int vq = V_ == VD ? cv : min(cv, V_ - 1);
+  const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
+  float uqv[4], q0v[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) {
+    const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
+    uqv[a] = cok ? x : 0.f;
+    const float y = Q0[vq * R + min(a, R - 1)];
+    q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
+  }
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinHalf win;
+  load_half<K_, V_>(win, st, slot, hv, L, 0);
+  uint32_t wds[2][8];
+  load_code_words4<K_, V_>(wds, Sq);
+
+  if (colt) {
+    sh.skl[cv] = scv;
+    f32x4 u;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) u[a] = a < R ? uqv[a] : 0.f;
+    sh.uoc[cv] = u;
+  } else {
+    sh.svr[cv] = scv * (pn / qmax);                                                   // kernels.py:1483
+    f32x4 o;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      o[a] = a < R ? uqv[a] : 0.f;
+      sh.qT[a][cv] = f2h(a < R ? hround(q0v[a]) : 0.f);                             // kernels.py:1573-1577
+    }
+    sh.qov[cv] = o;
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
+  __syncthreads();
+
+  // ---- stage 2: B = deq(S0) pn + window, fp16 (kernels.py:1483-1571); the window half by half ----
+  f16x4 bh[2][8];                                     // B packed, fp16 (tile layout, k = c for the MFMAs)
+  {
+    Tile4 t;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) t.a[g][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    store_half(sh, win, L, 0);
+    __syncthreads();
+    rebuild_half4(t, sh.op[0], sh.op[1]);
+    rebuild_half4(t, sh.op[0], sh.op[2]);
+    if (two) {
+      // the second half's rows are loaded only now: held across the first half's products they would push the
+      // code words (live from stage 1 to the end of the rebuild) out of the 128 registers
+      load_half<K_, V_>(win, st, slot, hv, L, 1);
+      __syncthreads();                                // every wave is past the first half's operands
+      store_half(sh, win, L, 1);
+      __syncthreads();
+      rebuild_half4(t, sh.op[0], sh.op[1]);
+      rebuild_half4(t, sh.op[0], sh.op[2]);
+    }
+    tile_add_words4(t, wds, sh.svr, sh.skl);
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) bh[g][nt] = pinned(to_h4(t.a[g][nt]));   // the fp16 rounding of B
+  }
+  __syncthreads();                                    // every wave is past the rebuild: the operand region is free
+  if (colt) {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) sh.r.uoT[a][cv] = f2h(sh.uoc[cv][a]);
+  } else {
+#pragma unroll
+    for (int a = 0; a < 4; ++a) sh.r.qoT[a][cv] = f2h(sh.qov[cv][a]);
+  }
+  __syncthreads();
+
+  // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
+  f32x4 p16[2];
+  p_step4(sh, bh, pn, R, p16);                        // P16 rows of this wave's channels (lanes < 16)
+  if (q == 0) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 16 * g + l16] = f2h(p16[g][r]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  {                                                   // Q^T partial over the wave's 32 channels
+    const f16x4 z4 = {};
+    f16x4 ap[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) ap[g] = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][32 * w + 16 * g + 4 * q] : z4;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      f32x4 d = mma16(ap[0], bh[0][nt], f32x4{0.f, 0.f, 0.f, 0.f});
+      d = mma16(ap[1], bh[1][nt], d);
+      if (q == 0) sh.r.qpart[w][16 * nt + l16] = d;
+    }
+  }
+  __syncthreads();
+  if (tid < VD) {                                     // waves 0 and 1: one row v per thread
+    // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels
+    const f16x8 z8 = {};
+    f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.r.uoT[l16][32 * ks + 8 * q] : z8;
+      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
+      macc = mma32(ao, bp, macc);
+    }
+    float M2[4][4];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    const int v = tid;
+    f32x4 s = sh.r.qpart[0][v];
+#pragma unroll
+    for (int w2 = 1; w2 < NW4; ++w2) s += sh.r.qpart[w2][v];
+    const f32x4 qo = sh.qov[v];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += pn * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
+    sh.qv[v] = s;
+  }
+  __syncthreads();
+  if (w == 0) {                                       // CholeskyQR2, fp16 Q (kernels.py:1778-1835)
+    __builtin_amdgcn_s_setprio(3);
+    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+    cholqr_pass(p0, p1);
+    cholqr_pass(p0, p1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = r < R ? hround(p0[r]) : 0.f;
+      p1[r] = r < R ? hround(p1[r]) : 0.f;
+      sh.qT[r][l] = f2h(p0[r]);
+      sh.qT[r][l + 64] = f2h(p1[r]);
+    }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+  f32x4 u16[2];
+  p_step4(sh, bh, pn, R, u16);                        // U16 = P step with Q16 (lanes < 16)
+
+  // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
+  Tile4 t;
+  {
+    const f16x4 z4 = {};
+    f16x4 auo[2], aun[2];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      auo[g] = q == 0 ? to_h4(sh.uoc[32 * w + 16 * g + l16]) : z4;                  // A[c][a] = U_old
+      aun[g] = q == 0 ? to_h4(-u16[g]) : z4;                                        // A[c][r] = -U16
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                              // B[a][v] = Q_old^T
+      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                               // B[r][v] = Q16^T
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        f32x4 e = from_h4(bh[g][nt]) * rpn;
+        e = mma16(auo[g], bqo, e);
+        e *= pn;
+        e = mma16(aun[g], bqn, e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.a[g][nt][i] = hround(e[i]);
+      }
+    }
+  }
+
+  // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
+  float rsk[2][4];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    float cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[g][nt][i]);
+      cs[i] = sum16(x);
+    }
+    // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
+    const int ic = l & 3;
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
+    const float sq = sqrtf(msum);
+    const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
+    const int cc = 32 * w + 16 * g + 4 * q + l16;
+    if (l16 < 4 && (K_ == KD || cc < K_)) Sk[cc] = fmaxf(sq, LQ_EPS);
+    rsk[g][0] = dpp<0x00>(rs);                        // quad_perm [i, i, i, i]: column i of the lane's quad
+    rsk[g][1] = dpp<0x55>(rs);
+    rsk[g][2] = dpp<0xaa>(rs);
+    rsk[g][3] = dpp<0xff>(rs);
+  }
+  // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    float m = 0.f;
+#pragma unroll
+    for (int g = 0; g < 2; ++g)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        t.a[g][nt][i] *= rsk[g][i];
+        m = fmaxf(m, fabsf(t.a[g][nt][i]));
+      }
+    sh.r.rmx[4 * w + q][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  if (tid < VD) {
+    float m = sh.r.rmx[0][tid];
+#pragma unroll
+    for (int k = 1; k < 4 * NW4; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
+    const float rmax = fmaxf(m, LQ_EPS);
+    if (V_ == VD || tid < V_) Sv[tid] = rmax;
+    sh.r.rq[tid] = qmax * (1.0f / rmax);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int v = 16 * nt + l16;
+    const float rq = sh.r.rq[v];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      uint32_t b[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[g][nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+      const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+      const int c = 32 * w + 16 * g + 4 * q;
+      if ((K_ == KD || c < K_) && (V_ == VD || v < V_))
+        *(uint32_t*)(Sq + v * K_ + c) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+  }
+  // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
+  if (q == 0) {
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int c = 32 * w + 16 * g + l16;
+      if (K_ == KD || c < K_)
+        for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16[g][r]);
+    }
+  }
+  if (tid < V_) {
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+  }
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+  __syncthreads();                                    // LDS reuse by the next head of this workgroup
+}
+
+}  // namespace lqf
+}  // namespace

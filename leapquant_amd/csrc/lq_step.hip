@@ -10,7 +10,7 @@
 //     the int8 tile, bf16 / fp16 MFMA for the window-key and factor dots), fed by 16-byte loads issued up front.
 //   * KDA (K = V = 128): two waves per value head, the same matrix-core dots, the per-channel gate folded into the
 //     key operands and the window's decayed keys formed by a backward scan split between the two waves.
-#include "lq_common.h"
+#include "lq_flush_core.h"
 
 namespace {
 
@@ -81,16 +81,34 @@ struct StepShared {
 // The per-head scalar work (norms, gate, beta, digits) runs in one wave per value head.  The window's u_j rows reach
 // LDS by direct global -> LDS loads.  <= 128 VGPRs and < 40 KiB LDS: four workgroups per CU, the whole B = 64 x H = 16
 // grid resident at once.
+// FL (fused flush, K = V = 128 and G = 2 only): after its step the workgroup flushes the heads whose window it has just
+// filled (or found full), with the four-wave flush of lq_flush_core.h over the same 256 threads -- one launch per decode
+// call instead of two.  The step's LDS and the flush's share the same bytes (both fit the 40 KiB that four workgroups
+// per CU allow).
 // ------------------------------------------------------------------------------------------------------------------
-template <int K_, int V_, int G, bool CONV>
+template <int K_, int V_, int G, bool FL>
+struct StepLds {
+  StepShared<K_, V_, G> st;
+};
+template <int K_, int V_, int G>
+struct StepLds<K_, V_, G, true> {
+  union {
+    StepShared<K_, V_, G> st;
+    lqf::FlushShared4 fl;
+  };
+};
+
+template <int K_, int V_, int G, bool CONV, bool FL>
 __global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
-void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist) {
+void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const float* Q0) {
+  static_assert(!FL || (K_ == 128 && V_ == 128 && G == 2), "fused flush: the four-wave layout, 128 x 128 heads");
   constexpr int KD = K_, VD = V_;
   constexpr int WPH = VD / 64;  // waves per value head
   constexpr int NE = KD / 64;   // channels per lane in the scalar work
   constexpr int KS32 = KD / 32, KS64 = KD / 64;   // k-steps of the 16x16x32 (bf16 / fp16) and 16x16x64 (int8) MFMAs
   constexpr bool NT = KD == 128;                  // non-temporal bulk loads (see ld_once)
-  __shared__ StepShared<K_, V_, G> sh;
+  __shared__ StepLds<K_, V_, G, FL> lds;
+  StepShared<K_, V_, G>& sh = lds.st;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
   const int hk = blockIdx.x - n * H;
@@ -383,11 +401,9 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist) {
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
   __syncthreads();              // ... and the other wave's, with the key and factor dots of every wave
   if (!live) {                  // a full window (a flush that did not cover this row): zero output, nothing written;
-    if (lt == 0) note_due(st.ctl, dlist, n * HV + hv);   // flag it again so that the flush after this step takes it
+    if (!FL && lt == 0) note_due(st.ctl, dlist, n * HV + hv);   // flag it again so that the flush takes it
     out[lt] = 0;
-    return;
-  }
-
+  } else {
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
   const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
   float a4 = 0.f, a5 = 0.f;
@@ -455,7 +471,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
-    if (h + 1 == L) note_due(st.ctl, dlist, n * HV + hv);   // this head is due: the flush that follows takes it
+    if (!FL && h + 1 == L) note_due(st.ctl, dlist, n * HV + hv);   // this head is due: the flush that follows takes it
   }
   if (wi == 0) {
 #pragma unroll
@@ -463,6 +479,24 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist) {
       const int c = lane + 64 * e;
       if (g == 0) ((bf16_t*)st.Kbuf)[(((long long)slot * H + hk) * L + h) * KD + c] = kapp[e];   // key append
       if (c < h) Wp[c] = wjv[e];
+    }
+  }
+  }  // live
+  if constexpr (FL) {
+    // the flush of this workgroup's heads whose window is now full (hcnt was L - 1 before the step, or already L):
+    // the fills are uniform loads, so every wave takes the same branch and reaches the same barriers
+    bool due[G], any = false;
+#pragma unroll
+    for (int g2 = 0; g2 < G; ++g2) {
+      due[g2] = hg[g2] >= L - 1;
+      any = any || due[g2];
+    }
+    if (any) {
+      __syncthreads();          // the step is done with the shared bytes, and its appends are visible to the workgroup
+      const float qm = code_range(st);
+#pragma unroll
+      for (int g2 = 0; g2 < G; ++g2)
+        if (due[g2]) lqf::flush_head4<128, 128>(lds.fl, st, Q0, slot, hk * G + g2, qm);
     }
   }
 }
@@ -846,9 +880,9 @@ template <int K_, int V_, bool CONV>
 static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
   dim3 grid((unsigned)(io->N * st->H));
   switch (st->HV / st->H) {
-    case 1: gdn_step_kernel<K_, V_, 1, CONV><<<grid, V_, 0, s>>>(*st, *io, cv, dlist); break;
-    case 2: gdn_step_kernel<K_, V_, 2, CONV><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist); break;
-    case 4: gdn_step_kernel<K_, V_, 4, CONV><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist); break;
+    case 1: gdn_step_kernel<K_, V_, 1, CONV, false><<<grid, V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 2: gdn_step_kernel<K_, V_, 2, CONV, false><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 4: gdn_step_kernel<K_, V_, 4, CONV, false><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
@@ -877,9 +911,7 @@ extern "C" int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* strea
   return lq_launch_step(st, io, 0, 0.f, nullptr, (hipStream_t)stream);
 }
 
-extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
-  int rc = lq_check_step(st, io);
-  if (rc) return rc;
+static int check_conv(const lq_state* st, const lq_conv* cv) {
   if (!cv || !cv->state || !cv->weight || cv->W != 4 || (cv->silu != 0 && cv->silu != 1) || cv->NS <= 0)
     return LQ_ERR_ARG;
   const long long C = 2ll * st->H * st->K + (long long)st->HV * st->V;
@@ -887,8 +919,36 @@ extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const 
   // the state taps of a slot must stay inside its slot_stride elements
   if ((C - 1) * cv->ch_stride + 2 * cv->tap_stride >= cv->slot_stride) return LQ_ERR_ARG;
   if (((uintptr_t)cv->weight & 7) != 0) return LQ_ERR_ARG;
+  return LQ_OK;
+}
+
+extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv, void* stream) {
+  int rc = lq_check_step(st, io);
+  if (rc) return rc;
+  if ((rc = check_conv(st, cv))) return rc;
   if (io->N == 0) return LQ_OK;
   return launch_gdn_dims<true>(st, io, *cv, nullptr, (hipStream_t)stream);
+}
+
+extern "C" int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0,
+                             void* stream) {
+  int rc = lq_check_step(st, io);
+  if (rc) return rc;
+  if (cv && (rc = check_conv(st, cv))) return rc;
+  const float qmax = st->qmax > 0.f ? st->qmax : LQ_QMAX;
+  if ((rc = lq_check_flush(st, Q0, io->idx, io->N, 0, qmax))) return rc;
+  if (io->N == 0) return LQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if (st->K == 128 && st->V == 128 && st->HV == 2 * st->H) {      // one launch: the step flushes its own due heads
+    const dim3 grid((unsigned)(io->N * st->H));
+    const lq_conv none = {};
+    if (cv) gdn_step_kernel<128, 128, 2, true, true><<<grid, 256, 0, s>>>(*st, *io, *cv, nullptr, Q0);
+    else gdn_step_kernel<128, 128, 2, false, true><<<grid, 256, 0, s>>>(*st, *io, none, nullptr, Q0);
+    return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
+  }
+  rc = cv ? launch_gdn_dims<true>(st, io, *cv, nullptr, s) : lq_launch_step(st, io, 0, 0.f, nullptr, s);
+  if (rc) return rc;
+  return lq_launch_flush(st, Q0, io->idx, io->N, 0, qmax, nullptr, s);
 }
 
 extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream) {

@@ -131,7 +131,8 @@ class LeapQuantState:
         return self._st
 
     def decode(self, ssm, mixed, a, b, A_log, dt_bias, idx, out):
-        """One decode token per row, then the end-of-window flush of the heads whose window became full.
+        """One decode token per row, then the end-of-window flush of the heads whose window became full (GDN: one
+        lq_gdn_decode call; KDA: the step, then the flush).
         a: GDN (N, HV) | KDA (N, HV, K) raw gate;  dt_bias: GDN (HV,) | KDA (HV*K,)."""
         A_log = self._as_f32(A_log)
         dt_bias = self._as_f32(dt_bias)
@@ -158,10 +159,11 @@ class LeapQuantState:
         if self.kda:
             _lib.check(L.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(self.glb), stream),
                        "lq_kda_step")
-        else:
-            _lib.check(L.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), stream), "lq_gdn_step")
-        _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx),
-                              N, 1 if self.kda else 0, ctypes.c_float(self.qmax), stream), "lq_flush")
+            _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 1, ctypes.c_float(self.qmax),
+                                  stream), "lq_flush")
+        else:                        # step + flush of the heads it fills (one launch for 128 x 128 heads, GQA 2)
+            _lib.check(L.lq_gdn_decode(ctypes.byref(st), ctypes.byref(io), None, KN._p(self.Q0), stream),
+                       "lq_gdn_decode")
 
     def decode_conv(self, ssm, x, conv_state, conv_weight, conv_bias, silu, a, b, A_log, dt_bias, idx, out):
         """GDN decode with the conv1d update fused into the step (lq_gdn_step_conv): x is the raw projection
@@ -199,10 +201,8 @@ class LeapQuantState:
         io = KN._step_io(x, a, b, A_log, dt_bias, idx, out, self.kstep_scale)
         cv = KN.conv_struct(conv_state, w, conv_bias, silu)
         stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
-        L = self._lib
-        _lib.check(L.lq_gdn_step_conv(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), stream), "lq_gdn_step_conv")
-        _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 0, ctypes.c_float(self.qmax), stream),
-                   "lq_flush")
+        _lib.check(self._lib.lq_gdn_decode(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), KN._p(self.Q0),
+                                           stream), "lq_gdn_decode")
 
     def _check_gate(self, a, N, KA):
         """The raw gate `a` is read as bf16, N x HV (GDN) or N x HV x K (KDA) values (kernels.py:86, 738)."""

@@ -176,6 +176,15 @@ class CheckingLib:
     def lq_kda_step(self, st, io, glb, stream):
         return self._step("lq_kda_step", st, io, True)
 
+    def lq_gdn_decode(self, st, io, cv, Q0, stream):
+        """The GDN step (conv fused when cv is set), then the flush of the rows of the call."""
+        cv = _arg(cv) if cv is not None else None
+        rc = self._step("lq_gdn_decode", st, io, False, cv)
+        if rc:
+            return rc
+        io = _arg(io)
+        return self._per_slot("lq_gdn_decode flush", st, ctypes.c_void_p(io.idx), io.N, False, False, Q0=Q0)
+
     def _per_slot(self, name, st, idx, N, kda, block, Q0=None, need_buf=True):
         st = _arg(st)
         self.calls.append(name)

@@ -51,9 +51,9 @@ def test_config4_plugin_calls_stay_in_bounds(checked, bf16_conv):
     with torch.no_grad():
         for _ in range(2):
             x = GS.run(stack, x)
-    step = "lq_gdn_step_conv" if bf16_conv else "lq_gdn_step"
     assert checked.calls.count("lq_quantize") == LAYERS
-    assert checked.calls.count(step) == 2 * LAYERS and checked.calls.count("lq_flush") == 2 * LAYERS
+    assert checked.calls.count("lq_gdn_decode") == 2 * LAYERS
+    assert checked.calls.count("lq_gdn_decode flush") == 2 * LAYERS
     # a mixed step on layer 0: 4 decode rows, prefill of slots 5..8 (the fp32 round trip around the engine's prefill)
     l = stack[0]
     md = FV.gdn_metadata(4, idx[:4], prefill_idx=idx[4:8], prefill_loc=torch.tensor([0, 2, 4, 6, 8]))
