@@ -13,10 +13,12 @@ Measurement:
     `warmup` report the calls actually run.  `achieved_gbps` divides the algorithmic bytes of those calls by their time.
   * `cpu_baseline`: the numpy oracle on config 0, its independent heads split over the host's cores (forked before the
     GPU is touched).
-  * roofline of the dominant kernel (the step): algorithmic bytes per launch (layout-independent minimum) over the
-    average launch duration, from HIP events around graph replays of step launches that rotate the same slot sets
-    (every window runs h = 0..63); traffic = the HBM bytes per launch that rocprofv3's FETCH_SIZE / WRITE_SIZE counters
-    read for this same command, calibrated on the 64 MiB copies it ends with.
+  * `roofline`: the timed region runs one kernel per call -- the GQA-2 step that also flushes the heads whose window it
+    fills (lq_gdn_decode) -- so its achieved rate is the algorithmic bytes of the timed calls (step bytes at each fill,
+    plus one all-due flush per set and window) over the timed region.  `step_roofline`: the step alone
+    (lq_gdn_step), algorithmic bytes per launch over the average launch duration, from HIP events around graph replays
+    of step launches over the same rotated sets (every window runs h = 0..63).  `traffic`: the HBM bytes per launch that
+    rocprofv3's FETCH_SIZE / WRITE_SIZE counters read for this same command, calibrated on the 64 MiB copies it ends with.
   * the same step on a dense bf16 state (`lq_dense_step`) as the baseline.
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 128] [--no-cpu]
 """
@@ -32,6 +34,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "int8 GDN/KDA decode-step µs + achieved HBM GB/s at B=64,H=32,d=128"
+DECODE_KERNEL = "gdn_step_kernel<128, 128, 2, false, true>"     # lq_gdn_decode at GQA 2: step + flush of its due heads
+STEP_KERNEL = "gdn_step_kernel<128, 128, 2, false, false>"      # the step alone (lq_gdn_step)
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -366,14 +370,14 @@ def config4_bench(torch, dev, stream, layers=24, B=64, reps=32):
             "tokens_per_s": round(B / (times["int8"] * 1e-6), 0)}
 
 
-def traffic_bytes():
-    """HBM bytes per step launch from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each scaled
-    by what the counter reads for the 64 MiB copies above (None when the summary is absent)."""
-    p = os.path.join(ROOT, "profiles", "gdn_step_B64_traffic.json")
+def traffic_bytes(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each
+    scaled by what the counter reads for the 64 MiB copies the bench ends with (None when the summary is absent)."""
+    p = os.path.join(ROOT, "profiles", "hbm_traffic.json")
     if not os.path.exists(p):
         return None
     with open(p) as f:
-        return json.load(f).get("hbm_bytes_per_launch")
+        return json.load(f).get(kernel, {}).get("hbm_bytes_per_launch")
 
 
 def _cpu_worker(heads, seed, calls, barrier, out):
@@ -562,6 +566,7 @@ def main():
     timed_bytes = timed_rot * NSET * (sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L))
                                       + flush_bytes(B, HV, H, K, V, R, L))
 
+    decode_gbps = timed_bytes / (ms_total * 1e-3) / 1e9
     progress("decode loop: %.3f us per call over %d calls (%d whole rotations of %d sets)"
              % (us_per_step, calls, timed_rot, NSET))
     # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
@@ -650,8 +655,12 @@ def main():
         _lib.check(_lib.lib().lq_gdn_step(ctypes.byref(sts), ctypes.byref(io_of(xconv, a, b, i % NSET)),
                                            ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "lq_gdn_step")
 
+    def fused_decode(i):                                          # what the plugin runs for a bf16 conv of width 4
+        x, a, b = pool[i % P]
+        lq.decode_conv(ssm, x, conv, cw, None, True, a, b, A_log, dt_bias, sets[i % NSET], out)
+
     conv_us = {}
-    for name, fn in (("fused", fused), ("unfused", unfused)):
+    for name, fn in (("fused", fused), ("unfused", unfused), ("decode", fused_decode)):
         gr = capture(fn, CH)
         lq.quantize(ssm, all_slots)                               # every window back to h = 0
         torch.cuda.synchronize()
@@ -694,19 +703,30 @@ def main():
                                "int8 state + fp32 scales, step + flush per call (the flush does work on one call in "
                                "64), whole windows of %d rotated slot sets" % NSET,
                    "batch": B, "value_heads": HV, "key_heads": H, "head_dim": K, "window": L, "rank": R},
-        "achieved_gbps": round(timed_bytes / (ms_total * 1e-3) / 1e9, 1),
-        "step_us": round(step_us, 3), "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
+        "achieved_gbps": round(decode_gbps, 1),
         "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
-        "speedup_vs_bf16_step": round(bf16_us / step_us, 3),
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(),
-                     "kernel": "gdn_step_kernel<128, 128, 2, false>", "bytes_per_launch": int(bytes_step)},
+        "speedup_vs_bf16_step": round(bf16_us / us_per_step, 3),
+        # the timed region is one kernel per decode call: the step that flushes the heads it fills
+        "roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(decode_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(DECODE_KERNEL),
+                     "kernel": DECODE_KERNEL, "bytes_per_launch": int(timed_bytes / calls),
+                     "us_per_launch": round(us_per_step, 3)},
+        # the step alone (no flush work), every window fill h = 0..63 over the same rotated sets
+        "step_us": round(step_us, 3), "speedup_vs_bf16_step_alone": round(bf16_us / step_us, 3),
+        "step_roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                          "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic_bytes(STEP_KERNEL),
+                          "kernel": STEP_KERNEL, "bytes_per_launch": int(bytes_step)},
+        # the standalone flush kernel (lq_flush: the KDA path, the other head shapes, the reference-API factories)
+        "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
     }
     res["conv_fused_config1"] = {
         "workload": "config 1 step with vLLM's causal_conv1d_update (width 4, SiLU, bf16 state [NS, C, 3]) fused in, "
                     "against the conv update kernel + step; rotated sets, h = 0..63",
         "fused_step_us": round(conv_us["fused"], 3), "conv_then_step_us": round(conv_us["unfused"], 3),
-        "plain_step_us": round(step_us, 3)}
+        "plain_step_us": round(step_us, 3),
+        "decode_conv_us": round(conv_us["decode"], 3),
+        "decode_conv_note": "LeapQuantState.decode_conv (lq_gdn_decode with the conv): conv + step + the flushes of "
+                            "the heads it fills, one launch per call, one whole window of every set"}
     res["kda_config2"] = kda
     res["flush_quantize_config3"] = fq
     res["head_dims_W16"] = hd
