@@ -53,12 +53,16 @@ __device__ __forceinline__ T ld_nt(const T* p) {
 }
 constexpr float KSPLIT = 64.0f;   // kn / qn scaled by 2^6 before the fp16 hi / lo split (keeps the lo part normal)
 
+// The MFMA B-operand tables (dig, bkq, hkq) are read as 16-byte fragments of up to six rows at once: their rows are
+// padded by 16 bytes so that those rows start in different LDS banks (unpadded, 128- or 256-byte rows all start in
+// the same bank).
+constexpr int DIGP = 16, OPP = 8;
 template <int K_, int V_, int G>
 struct StepShared {
   bf16_t ub[G][LMAX][V_];  // the window's u_j rows per value head (direct global -> LDS loads)
-  int8_t dig[G][6][K_];    // int8 GEMV B operand: k digits 0-2, q digits 0-2
-  bf16_t bkq[6][K_];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
-  f16_t hkq[4][K_];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
+  int8_t dig[G][6][K_ + DIGP];   // int8 GEMV B operand: k digits 0-2, q digits 0-2
+  bf16_t bkq[6][K_ + OPP];       // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
+  f16_t hkq[4][K_ + OPP];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
   float2 mq[G][V_];        // GEMV rows (k, q) in digit units
   float2 cwq[G][LMAX];     // (w_j dk_j, w_j dq_j) per value head: buffered entry j's coefficients in A4 / A5
   float2 duq[G][4];        // (dU_r, dQ_r) per value head, factor r
