@@ -89,8 +89,9 @@ int lq_abi_version(void);
 /* GDN decode step: one token per row; appends (k, u, w = 1) to the window and updates the gate products.
  * Replaces make_gdn_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ, idx, o)
  * (/root/reference/leapquant/kernels.py:27-692, launched at state.py:112-113).  Requires (K, V) = (128, 128), (64, 128)
- * or (64, 64) (kernels.py:62), 1 <= L <= 64, 1 <= R <= 4, HV % H == 0 and HV / H in {1, 2, 4}.  A head whose window is already full (hcnt >= L) is left
- * untouched and its output row is zero (the flush after every step keeps hcnt < L on entry). */
+ * or (64, 64) (kernels.py:62), 1 <= L <= 64, HV % H == 0 and HV / H in {1, 2, 4}, and 1 <= R <= 4 -- at (128, 128)
+ * 1 <= R <= 16, the reference's rank ablation (kernels.py:63-64, 457-469).  A head whose window is already full
+ * (hcnt >= L) is left untouched and its output row is zero (the flush after every step keeps hcnt < L on entry). */
 int lq_gdn_step(const lq_state* st, const lq_step_io* io, void* stream);
 
 /* lq_gdn_step with the conv1d update fused in (see lq_conv): io->mixed holds the raw projection.  No counterpart in the
@@ -109,8 +110,8 @@ int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, c
 /* KDA decode step (per-key-channel gate).  glb != 0: GLM's bounded gate glb * sigmoid(exp(A_log) (a + dt_bias));
  * glb == 0: Kimi's -exp(A_log) softplus(a + dt_bias).
  * Replaces make_kda_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ,
- * idx, o) (kernels.py:694-1075, launched at state.py:108-109).  Same limits as lq_gdn_step, with K = V = 128 only
- * (kernels.py:727). */
+ * idx, o) (kernels.py:694-1075, launched at state.py:108-109).  Same limits as lq_gdn_step, with K = V = 128 and
+ * R <= 4 only (kernels.py:727, 1036). */
 int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream);
 
 /* End-of-window flush of every (idx[n] > 0, hv) head whose window is full (hcnt == L): rebuild, one subspace
@@ -118,19 +119,21 @@ int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* strea
  * (127: INT8; 31: 6-bit in the same int8 container), window reset.  Due heads are found on the device.
  * Replaces make_flush(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx)
  * (kernels.py:1077-2033, launched at state.py:115-116).  Requires 1 <= L <= 64, 1 <= R <= 4 and (K, V) = (128, 128),
- * or for GDN (kda == 0) also (64, 128), (64, 64) (kernels.py:1089-1092). */
+ * or for GDN (kda == 0) also (64, 128), (64, 64) (kernels.py:1089-1092); GDN (128, 128) also 5 <= R <= 8, whose
+ * CholeskyQR drops a dependent column instead of flooring its pivot (kernels.py:1091, 1744-1772). */
 int lq_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, void* stream);
 
 /* Standalone quantize of the fp32 states of the slots idx[n] > 0 (read from the same ssm blocks the checkpoint then
  * overwrites), window reset (Wbuf = 0, Pbuf = 1, hcnt = 0).  qmax 127 (INT8) or 31 (6-bit).
  * Replaces make_quantize(...)(S0, Sq, Sk, Sv, UQ, Wbuf, Pbuf, hcnt, Q0, idx) (kernels.py:2126-2242, state.py:163-165).
- * Requires (K, V) = (128, 128), (64, 128) or (64, 64), 1 <= R <= 4. */
+ * Requires (K, V) = (128, 128), (64, 128) or (64, 64), 1 <= R <= 4; at (128, 128) 1 <= R <= 16 (every rank a step
+ * reads). */
 int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream);
 
 /* Prefill dequant (GDN): fp32 S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T written over the ssm blocks of the
  * slots idx[n] > 0, then window reset.  Replaces make_dequant(...)(S0, Sq, Sk, Sv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt,
  * UQ, idx) (kernels.py:2041-2123, state.py:152-154).  Requires (K, V) = (128, 128), (64, 128) or (64, 64),
- * 1 <= L <= 64, 1 <= R <= 4. */
+ * 1 <= L <= 64, 1 <= R <= 4; at (128, 128) 1 <= R <= 16. */
 int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream);
 
 /* Prefill dequant (KDA): fp32 S = (deq(Sq) + Q U^T) diag(exp(P)) + sum_{j<h} w_j u_j (K_j * D_j)^T, D_j the product of

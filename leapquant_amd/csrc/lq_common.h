@@ -10,6 +10,10 @@
 #define LQ_SOFTPLUS_THRESHOLD 20.0 // kernels.py:21
 #define LQ_PNMIN 1e-20f            // kernels.py:1078
 #define LQ_NORM_EPS 1e-6           // kernels.py:246-247
+// largest ranks R of GDN 128 x 128 heads: the step (and the quantize / dequant that build and read its checkpoints)
+// R <= 16, the flush R <= 8 (kernels.py:63, 1091); KDA and 64-dim heads R <= 4
+#define LQ_STEP_RMAX 16
+#define LQ_FLUSH_RMAX 8
 
 typedef uint16_t bf16_t;   // bfloat16 bits
 typedef uint16_t f16_t;    // IEEE half bits
@@ -89,6 +93,32 @@ __device__ __forceinline__ float xor32_max(float x) {
 // all-reduce over the wave
 __device__ __forceinline__ float sum64(float x) { return xor32_sum(xor16_sum(sum16(x))); }
 __device__ __forceinline__ float max64(float x) { return xor32_max(xor16_max(max16(x))); }
+
+// the same exchanges on fp64 values (both 32-bit halves moved by the same lane pattern)
+template <int CTRL>
+__device__ __forceinline__ double dppd(double x) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+  const unsigned lo = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, 0xf, 0xf, false);
+  const unsigned hi = (unsigned)__builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, 0xf, 0xf, false);
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double join_d(unsigned lo, unsigned hi) {
+  return __builtin_bit_cast(double, ((unsigned long long)hi << 32) | lo);
+}
+__device__ __forceinline__ double sum64d(double x) {
+  x += dppd<DPP_XOR1>(x);
+  x += dppd<DPP_XOR2>(x);
+  x += dppd<DPP_HALF_MIRROR>(x);
+  x += dppd<DPP_MIRROR>(x);
+  unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+  auto l16 = __builtin_amdgcn_permlane16_swap((unsigned)u, (unsigned)u, false, false);
+  auto h16 = __builtin_amdgcn_permlane16_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+  x = join_d(l16[0], h16[0]) + join_d(l16[1], h16[1]);
+  u = __builtin_bit_cast(unsigned long long, x);
+  auto l32 = __builtin_amdgcn_permlane32_swap((unsigned)u, (unsigned)u, false, false);
+  auto h32 = __builtin_amdgcn_permlane32_swap((unsigned)(u >> 32), (unsigned)(u >> 32), false, false);
+  return join_d(l32[0], h32[0]) + join_d(l32[1], h32[1]);
+}
 
 // ---- gates (scalar, per (row, head) or per channel); evaluated in fp64 and rounded once ----------------------------
 __device__ __forceinline__ double softplus20(double x) {

@@ -90,12 +90,12 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
   }
 }
 
-template <bool KDA, int K_ = KD, int V_ = VD>
+template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
-  __shared__ FlushShared sh;
-  auto head = [&](int slot, int hv) { flush_head<KDA, K_, V_>(sh, st, Q0, slot, hv, qmax); };
+  __shared__ FlushShared<RA> sh;
+  auto head = [&](int slot, int hv) { flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax); };
   if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan(sh.due, st, idx, N, head);
 }
@@ -126,10 +126,12 @@ struct QTile {
   f32x4 a[2][8];
 };
 
+template <int RA>
 struct QuantShared {
-  f32x4 qv[VD];
-  f32x4 pp[KD];
-  f32x4 qpart[QW][VD];
+  static constexpr int NB = RA / 4;  // blocks of four factor columns
+  f32x4 qv[NB][VD];
+  f32x4 pp[NB][KD];
+  f32x4 qpart[QW][VD];               // one block's per-wave partial rows at a time
   float rowmax[QW][VD];
   float sk[KD];
 };
@@ -194,11 +196,32 @@ __device__ __forceinline__ f32x4 sum_parts_q(const f32x4 (*part)[VD], int v) {
   return s;
 }
 
-template <bool KDA, int K_ = KD, int V_ = VD>
+// rows l, l + 64 of the NB blocks X[b] as plain arrays (wave 0's view of a 128 x RA factor) and back
+template <int RA>
+__device__ __forceinline__ void rows_get(const f32x4 (*X)[128], int l, float (&p0)[RA], float (&p1)[RA]) {
+#pragma unroll
+  for (int b = 0; b < RA / 4; ++b) {
+    const f32x4 x0 = X[b][l], x1 = X[b][l + 64];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) { p0[4 * b + i] = x0[i]; p1[4 * b + i] = x1[i]; }
+  }
+}
+template <int RA>
+__device__ __forceinline__ void rows_put(f32x4 (*X)[128], int l, const float (&p0)[RA], const float (&p1)[RA]) {
+#pragma unroll
+  for (int b = 0; b < RA / 4; ++b) {
+    X[b][l] = f32x4{p0[4 * b], p0[4 * b + 1], p0[4 * b + 2], p0[4 * b + 3]};
+    X[b][l + 64] = f32x4{p1[4 * b], p1[4 * b + 1], p1[4 * b + 2], p1[4 * b + 3]};
+  }
+}
+
+// RA: factor columns held (4, 8 or 16; R <= RA), as RA / 4 blocks of four that the reductions take one at a time
+template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
 __global__ __launch_bounds__(QT) __attribute__((amdgpu_waves_per_eu(4)))
 void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax, int iters) {
-  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
-  __shared__ QuantShared sh;
+  static_assert(!KDA || (K_ == KD && V_ == VD && RA == 4), "KDA heads are 128 x 128, R <= 4");
+  constexpr int NB = RA / 4;
+  __shared__ QuantShared<RA> sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
   const int slot = idx[n];
@@ -220,51 +243,69 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     }
   }
   if (tid < VD) {
-    f32x4 q0v;
-    for (int r = 0; r < 4; ++r) q0v[r] = (r < R && tid < V_) ? Q0[tid * R + r] : 0.f;
-    sh.qv[tid] = q0v;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      f32x4 q0v;
+      for (int i = 0; i < 4; ++i) q0v[i] = (4 * b + i < R && tid < V_) ? Q0[tid * R + 4 * b + i] : 0.f;
+      sh.qv[b][tid] = q0v;
+    }
   }
   __syncthreads();
   // P = S^T Q, MGS; Q = S P, MGS (`iters` rounds)
   for (int it = 0; it < iters; ++it) {
-    colred_q(t, sh.qv, [&](int cg, int i, f32x4 s) { if ((l & 15) == 0) sh.pp[32 * w + 16 * cg + 4 * q + i] = s; });
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+      colred_q(t, sh.qv[b], [&](int cg, int i, f32x4 s) { if ((l & 15) == 0) sh.pp[b][32 * w + 16 * cg + 4 * q + i] = s; });
     __syncthreads();
     if (w == 0) {
       __builtin_amdgcn_s_setprio(3);
-      f32x4 p0 = sh.pp[l], p1 = sh.pp[l + 64];
-      mgs(p0, p1, R);
-      sh.pp[l] = p0;
-      sh.pp[l + 64] = p1;
+      float p0[RA], p1[RA];
+      rows_get<RA>(sh.pp, l, p0, p1);
+      mgs_n<RA>(p0, p1, R);
+      rows_put<RA>(sh.pp, l, p0, p1);
       __builtin_amdgcn_s_setprio(0);
     }
     __syncthreads();
-    rowred_q(t, sh.pp, sh.qpart);
-    __syncthreads();
+    float p0[RA], p1[RA];                             // wave 0: the rows l, l + 64 of Q = S P, block by block
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      rowred_q(t, sh.pp[b], sh.qpart);
+      __syncthreads();
+      if (w == 0) {
+        const f32x4 s0 = sum_parts_q(sh.qpart, l), s1 = sum_parts_q(sh.qpart, l + 64);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) { p0[4 * b + i] = s0[i]; p1[4 * b + i] = s1[i]; }
+      }
+      if (b + 1 < NB) __syncthreads();                // wave 0 has read the partials before the next block's
+    }
     if (w == 0) {
       __builtin_amdgcn_s_setprio(3);
-      f32x4 p0 = sum_parts_q(sh.qpart, l), p1 = sum_parts_q(sh.qpart, l + 64);
-      mgs(p0, p1, R);
-      sh.qv[l] = p0;
-      sh.qv[l + 64] = p1;
+      mgs_n<RA>(p0, p1, R);
+      rows_put<RA>(sh.qv, l, p0, p1);
       __builtin_amdgcn_s_setprio(0);
     }
     __syncthreads();
   }
   // U = fp16(S^T Q) straight to LDS (sh.pp is not read again before the next barrier), Q16 = fp16(Q)
-  colred_q(t, sh.qv, [&](int cg, int i, f32x4 s) {
-    if ((l & 15) == 0) {
-      f32x4 u;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(s[r]) : 0.f;
-      sh.pp[32 * w + 16 * cg + 4 * q + i] = u;
-    }
-  });
+  for (int b = 0; b < NB; ++b)
+    colred_q(t, sh.qv[b], [&](int cg, int i, f32x4 s) {
+      if ((l & 15) == 0) {
+        f32x4 u;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) u[r] = 4 * b + r < R ? hround(s[r]) : 0.f;
+        sh.pp[b][32 * w + 16 * cg + 4 * q + i] = u;
+      }
+    });
   __syncthreads();                                    // every wave has read Q (sh.qv)
   if (tid < VD) {
-    f32x4 x = sh.qv[tid];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) x[r] = r < R ? hround(x[r]) : 0.f;
-    sh.qv[tid] = x;
+    for (int b = 0; b < NB; ++b) {
+      f32x4 x = sh.qv[b][tid];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) x[r] = 4 * b + r < R ? hround(x[r]) : 0.f;
+      sh.qv[b][tid] = x;
+    }
   }
   __syncthreads();
   // E = S - Q U^T (fp32), column scales
@@ -273,14 +314,19 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 32 * w + 16 * cg + 4 * q + i;
-      const f32x4 unc = sh.pp[c];
+      f32x4 unc[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) unc[b] = sh.pp[b][c];
       float s = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
-        const f32x4 qnv = sh.qv[16 * nt + (l & 15)];
         float e = t.a[cg][nt][i];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
+        for (int b = 0; b < NB; ++b) {
+          const f32x4 qnv = sh.qv[b][16 * nt + (l & 15)];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[b][r], e);
+        }
         t.a[cg][nt][i] = e;
         s += fabsf(e);
       }
@@ -337,12 +383,12 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   if (tid < KD) {
     if (K_ == KD || tid < K_) {
       Sk[tid] = sh.sk[tid];
-      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + tid] = f2h(sh.pp[tid][r]);
+      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + tid] = f2h(sh.pp[r >> 2][tid][r & 3]);
     }
   } else if (tid < KD + VD) {
     const int v = tid - KD;
     if (V_ == VD || v < V_)
-      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + v] = f2h(sh.qv[v][r]);
+      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + v] = f2h(sh.qv[r >> 2][v][r & 3]);
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (KDA) {
@@ -471,10 +517,22 @@ void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
 // prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place.  A head
 // of K_ x V_ < 128 x 128 runs zero-padded in the tile (see flush_head) and writes its own rows / columns only.
 // ------------------------------------------------------------------------------------------------------------------
-template <int K_ = KD, int V_ = VD>
+template <int RA>
+struct DeqShared {
+  static constexpr int NB = RA / 4;
+  bf16_t op[3][KD][OPS];       // window operands, as in the flush
+  float skl[KD];               // Sk
+  float svr[VD];               // Sv
+  float w[LPMAX];
+  f32x4 uoc[NB][KD];           // U rows [c][r], r >= R zero
+  f32x4 qov[NB][VD];           // Q rows [v][r]
+};
+
+template <int K_ = KD, int V_ = VD, int RA = 4>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
-  __shared__ FlushShared sh;
+  constexpr int NB = RA / 4;
+  __shared__ DeqShared<RA> sh;
   const int HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
   const int slot = idx[n];
@@ -495,26 +553,26 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   const bool cok = (K_ == KD && V_ == VD) || cv < nc;
   const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
   const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
-  float uqv[4];
+  float uqv[RA];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
+  for (int a = 0; a < RA; ++a) {
     const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
-    uqv[a] = cok ? x : 0.f;
+    uqv[a] = (cok && a < R) ? x : 0.f;
   }
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
   load_window<false, K_, V_>(win, st, slot, hv, h, LP);
   uint32_t wds[8];
   load_code_words<K_, V_>(wds, Sq);
-  f32x4 fac;
+  if (tid < KD + VD) {
+    if (tid < KD) sh.skl[cv] = scv;
+    else sh.svr[cv] = scv;
 #pragma unroll
-  for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
-  if (tid < KD) {
-    sh.skl[cv] = scv;
-    sh.uoc[cv] = fac;
-  } else if (tid < KD + VD) {
-    sh.svr[cv] = scv;
-    sh.qov[cv] = fac;
+    for (int b = 0; b < NB; ++b) {
+      const f32x4 fac = {uqv[4 * b], uqv[4 * b + 1], uqv[4 * b + 2], uqv[4 * b + 3]};
+      if (tid < KD) sh.uoc[b][cv] = fac;
+      else sh.qov[b][cv] = fac;
+    }
   }
   if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
   __syncthreads();
@@ -527,14 +585,19 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + (l & 15);
       const float rv = sh.svr[v];
-      const f32x4 qo = sh.qov[v];
+      f32x4 qo[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) qo[b] = sh.qov[b][v];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int c = c0 + i;
-        const f32x4 uo = sh.uoc[c];
         float x = (((float)(int)(int8_t)(wds[nt] >> (8 * i)) * inv) * sh.skl[c]) * rv;   // kernels.py:2107
 #pragma unroll
-        for (int a = 0; a < 4; ++a) x = fmaf(qo[a], uo[a], x);                         // kernels.py:2109-2111
+        for (int b = 0; b < NB; ++b) {
+          const f32x4 uo = sh.uoc[b][c];
+#pragma unroll
+          for (int a = 0; a < 4; ++a) x = fmaf(qo[b][a], uo[a], x);                    // kernels.py:2109-2111
+        }
         t.a[nt][i] = x * P;                                                             // kernels.py:2113
       }
     }
@@ -636,9 +699,11 @@ bool head_dims(const lq_state* st, bool kda) {
   return (st->K == KD && st->V == VD) || (!kda && st->K == 64 && (st->V == 128 || st->V == 64));
 }
 
-int check_block_state(const lq_state* st, bool need_buf, bool kda) {
+// rmax: the entry point's largest rank for GDN 128 x 128 heads (every other head: R <= 4)
+int check_block_state(const lq_state* st, bool need_buf, bool kda, int rmax) {
   if (!st || !st->ssm || !st->hcnt || !st->Wbuf || !st->Pbuf) return LQ_ERR_ARG;
-  if (!head_dims(st, kda) || st->L < 1 || st->L > LPMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (!head_dims(st, kda) || st->L < 1 || st->L > LPMAX || st->R < 1) return LQ_ERR_ARG;
+  if (st->R > ((!kda && st->K == KD && st->V == VD) ? rmax : 4)) return LQ_ERR_ARG;
   if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0) return LQ_ERR_ARG;
   if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3)) return LQ_ERR_ARG;
   if (((uintptr_t)st->ssm & 15) != 0) return LQ_ERR_ARG;
@@ -649,7 +714,7 @@ int check_block_state(const lq_state* st, bool need_buf, bool kda) {
 }  // namespace
 
 int lq_check_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax) {
-  int rc = check_block_state(st, true, kda != 0);
+  int rc = check_block_state(st, true, kda != 0, LQ_FLUSH_RMAX);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || (kda && !st->Gbuf)) return LQ_ERR_ARG;
   return LQ_OK;
@@ -662,6 +727,7 @@ int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, 
   const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
   const dim3 g4((unsigned)(total < 4 * num_cus() ? total : 4 * num_cus()));  // four-wave flush: four per CU
   if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if (st->K == KD && st->R > 4) flush_kernel<false, KD, VD, 8><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else if (st->K == KD) flush4_kernel<><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
@@ -675,20 +741,22 @@ extern "C" int lq_flush(const lq_state* st, const float* Q0, const int* idx, int
 }
 
 extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, false, false);
+  int rc = check_block_state(st, false, false, LQ_STEP_RMAX);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
   const dim3 g((unsigned)(N * st->HV));
   hipStream_t s = (hipStream_t)stream;
-  if (st->K == KD) quantize_kernel<false><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  if (st->K == KD && st->R > 8) quantize_kernel<false, KD, VD, 16><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else if (st->K == KD && st->R > 4) quantize_kernel<false, KD, VD, 8><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else if (st->K == KD) quantize_kernel<false><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   else if (st->V == VD) quantize_kernel<false, 64, 128><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   else quantize_kernel<false, 64, 64><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 
 extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, false, true);
+  int rc = check_block_state(st, false, true, 4);
   if (rc) return rc;
   if (N < 0 || (N > 0 && (!Q0 || !idx)) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
@@ -697,7 +765,7 @@ extern "C" int lq_kda_checkpoint(const lq_state* st, const float* Q0, const int*
 }
 
 extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, true, true);
+  int rc = check_block_state(st, true, true, 4);
   if (rc) return rc;
   if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
@@ -706,13 +774,15 @@ extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float q
 }
 
 extern "C" int lq_dequant(const lq_state* st, const int* idx, int N, float qmax, void* stream) {
-  int rc = check_block_state(st, true, false);
+  int rc = check_block_state(st, true, false, LQ_STEP_RMAX);
   if (rc) return rc;
   if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f)) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
   const dim3 g((unsigned)(N * st->HV));
   hipStream_t s = (hipStream_t)stream;
-  if (st->K == KD) dequant_kernel<><<<g, FT, 0, s>>>(*st, idx, qmax);
+  if (st->K == KD && st->R > 8) dequant_kernel<KD, VD, 16><<<g, FT, 0, s>>>(*st, idx, qmax);
+  else if (st->K == KD && st->R > 4) dequant_kernel<KD, VD, 8><<<g, FT, 0, s>>>(*st, idx, qmax);
+  else if (st->K == KD) dequant_kernel<><<<g, FT, 0, s>>>(*st, idx, qmax);
   else if (st->V == VD) dequant_kernel<64, 128><<<g, FT, 0, s>>>(*st, idx, qmax);
   else dequant_kernel<64, 64><<<g, FT, 0, s>>>(*st, idx, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;

@@ -51,25 +51,28 @@ struct Tile {
   f32x4 a[8];
 };
 
+// RA = factor columns held (4: R <= 4; 8: the R = 8 GDN flush, kernels.py:1091, 1123), as NB = RA / 4 blocks of four
+template <int RA = 4>
 struct FlushShared {
+  static constexpr int NB = RA / 4;
   union {
     bf16_t op[3][KD][OPS];     // rebuild operands [c or v][j]
     struct {                   // after the rebuild
-      f32x4 qpart[NW][VD];     // per-wave partial Q rows
+      f32x4 qpart[NW][NB][VD]; // per-wave partial Q rows
       float rmx[4 * NW][VD];   // per-(wave, lane group) row maxima of the scaled residual
       float rq[VD];            // qmax / row scale
-      f16_t ppT[4][KD];        // P16^T
+      f16_t ppT[RA][KD];       // P16^T
     } r;
   };
   float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
   float svr[VD];               // row factor of the dequant (Sv pn / qmax, KDA: Sv / qmax)
   float w[LPMAX];
-  f32x4 uoc[KD];               // old U rows [c][a] (KDA: fp16(U pc)), a >= R zero
-  f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
-  f16_t uoT[4][KD];            // the same, fp16 transposed (MFMA operands)
-  f16_t qoT[4][VD];
-  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
-  f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
+  f32x4 uoc[NB][KD];           // old U rows [c][a] (KDA: fp16(U pc)), a >= R zero
+  f32x4 qov[NB][VD];           // old Q rows [v][a], a >= R zero
+  f16_t uoT[RA][KD];           // the same, fp16 transposed (MFMA operands)
+  f16_t qoT[RA][VD];
+  f16_t qT[RA][VD];            // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f32x4 qv[NB][VD];            // Q rows: fp32 before CholeskyQR, then Q16
   unsigned long long due;      // persistent flush: due mask of the current candidate chunk
 };
 
@@ -188,6 +191,87 @@ __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
     }
   }
 }
+// the same on N columns held as plain arrays (rows l, l + 64 of a lane of wave 0), for ranks up to 16
+template <int N>
+__device__ __forceinline__ void mgs_n(float (&p0)[N], float (&p1)[N], int R) {
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    if (j < R) {
+#pragma unroll
+      for (int c = 0; c < j; ++c) {
+        const float sc = sum64u(fmaf(p0[c], p0[j], p1[c] * p1[j]));
+        p0[j] = p0[j] - sc * p0[c];
+        p1[j] = p1[j] - sc * p1[c];
+      }
+      const float nrm = sum64u(fmaf(p0[j], p0[j], p1[j] * p1[j]));
+      const float rs = rsqrt_rn(fmaxf(nrm, 1e-30f));
+      p0[j] *= rs;
+      p1[j] *= rs;
+    }
+  }
+}
+
+// CholeskyQR pass of the wider-rank flush (R = 8, kernels.py:1744-1772) on N columns: the same factorisation, but a
+// pivot that has lost all but 1e-6 of its Gram diagonal drops its column (1 / L_jj = 0) instead of being floored;
+// columns past R are zero and stay zero.  Gram, factor and substitution run in fp64: a column that depends on the
+// earlier ones leaves a pivot of ~1e-14 G_jj in fp64, but fp32 sums of 128 rows leave ~1e-6 G_jj of rounding -- the
+// drop threshold itself -- so in fp32 whether such a column is dropped would be up to the rounding.
+// lane l's fp64 value, uniform over the wave
+__device__ __forceinline__ double rl_d(double x, int l) {
+  const unsigned long long u = __builtin_bit_cast(unsigned long long, x);
+  return join_d((unsigned)__builtin_amdgcn_readlane((int)(unsigned)u, l),
+                (unsigned)__builtin_amdgcn_readlane((int)(unsigned)(u >> 32), l));
+}
+template <int N>
+__device__ __forceinline__ void cholqr_pass_drop(float (&p0)[N], float (&p1)[N]) {
+  static_assert(N * (N + 1) / 2 <= 64, "one triangle entry per lane");
+  const int lane = lane_id();
+  double a = 0.0;                                     // lane t: entry t of the packed lower triangle (Gram, then factor)
+#pragma unroll
+  for (int r = 0; r < N; ++r)
+#pragma unroll
+    for (int c = 0; c <= r; ++c) {
+      const double g = sum64d(fma((double)p0[r], (double)p0[c], (double)p1[r] * (double)p1[c]));
+      a = lane == r * (r + 1) / 2 + c ? g : a;
+    }
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int rj = j * (j + 1) / 2;
+#pragma unroll
+    for (int k = 0; k < j; ++k) {
+      const int rk = k * (k + 1) / 2;
+      double ac = rl_d(a, rj + k);
+#pragma unroll
+      for (int m = 0; m < k; ++m) ac -= rl_d(a, rj + m) * rl_d(a, rk + m);
+      ac *= rl_d(a, rk + k);                          // L_jk (the diagonal entries hold 1 / L_kk)
+      a = lane == rj + k ? ac : a;
+    }
+    const double gjj = rl_d(a, rj + j);
+    double ac = gjj;
+#pragma unroll
+    for (int m = 0; m < j; ++m) {
+      const double ljm = rl_d(a, rj + m);
+      ac -= ljm * ljm;
+    }
+    ac = ac > 1e-6 * gjj + 1e-30 ? 1.0 / sqrt(fmax(ac, 1e-30)) : 0.0;
+    a = lane == rj + j ? ac : a;
+  }
+#pragma unroll
+  for (int s = 0; s < 2; ++s) {
+    float (&p)[N] = s ? p1 : p0;
+    double x[N];
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int rj = j * (j + 1) / 2;
+      double ac = (double)p[j];
+#pragma unroll
+      for (int m = 0; m < j; ++m) ac -= x[m] * rl_d(a, rj + m);
+      x[j] = ac * rl_d(a, rj + j);
+    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) p[j] = (float)x[j];
+  }
+}
 
 // the 8 code words of the lane's tile entries (issued early; consumed by tile_add_words).  A head of K_ x V_ < 128 x
 // 128 sits zero-padded in the tile: entries past its rows / columns read as 0 (clamped addresses, no divergent load).
@@ -264,8 +348,8 @@ __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int 
 // Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write.  GDN: op0 =
 // K_j[c], op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 = raw K_j[c] / e_j[c] (turned
 // into the decayed key operands by kda_key_scan), op2 = u_j[v].  Rows j >= h carry zero values and, for KDA, decay 1.
-template <bool KDA>
-__device__ __forceinline__ void store_window(FlushShared& sh, const WinRegs& r, int h, int LP) {
+template <bool KDA, class SH>
+__device__ __forceinline__ void store_window(SH& sh, const WinRegs& r, int h, int LP) {
   const int ch = win_chunk(LP);
   if (ch >= 16) return;
   const int j0 = 2 * win_pair(LP), c8 = ch * 8;
@@ -373,57 +457,84 @@ __device__ __forceinline__ f32x4 sum_parts(const f32x4 (*part)[VD], int v) {
   return s;
 }
 
+// M[a][r] = sum_k X[k][a] Y[k][r] over 128 k for a, r < RA, from the fp16 transposed operands X^T, Y^T ([RA][128]): the
+// MFMA leaves M[a][r] in lane 16 (a >> 2) + r, element a & 3; every lane gets all RA x RA entries
+template <int RA>
+__device__ __forceinline__ void gram_t(const f16_t (*XT)[128], const f16_t (*YT)[128], float (&M)[RA][RA]) {
+  const int l = lane_id(), q = l >> 4, l16 = l & 15;
+  const bool rla = l16 < RA;
+  const f16x8 z8 = {};
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    const f16x8 ao = rla ? *(const f16x8*)&XT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 by = rla ? *(const f16x8*)&YT[l16][32 * ks + 8 * q] : z8;
+    macc = mma32(ao, by, macc);
+  }
+#pragma unroll
+  for (int a = 0; a < RA; ++a)
+#pragma unroll
+    for (int r = 0; r < RA; ++r) M[a][r] = rl(macc[a & 3], 16 * (a >> 2) + r);
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // flush (kernels.py:1077-2033): one due (slot, head)
 // ------------------------------------------------------------------------------------------------------------------
 // P = B^T Q + pn U_old (Q_old^T Q) for this wave's 16 key channels, fp16-rounded (kernels.py:1580-1700).  Q^T comes
 // from sh.qT; bt[nt] is the transposed packing of B (lane l: B[16 w + (l & 15)][16 nt + 4 (l >> 4) + i]).  Lanes
-// l < 16 return P[16 w + l][0..3] (zero for r >= R); the other lanes return zeros.
-__device__ __forceinline__ f32x4 p_step(const FlushShared& sh, const f16x4 bt[8], float pn, int R) {
+// l < 16 RA / 4 return P[16 w + (l & 15)][4 (l >> 4) + i] (zero for columns >= R); the other lanes return zeros.
+template <int RA>
+__device__ __forceinline__ f32x4 p_step(const FlushShared<RA>& sh, const f16x4 bt[8], float pn, int R) {
+  constexpr int NB = RA / 4;
   const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
-  const bool rl4 = l16 < 4;
-  const f16x8 z8 = {};
+  const bool rla = l16 < RA;
   const f16x4 z4 = {};
-  // M[a][r] = sum_v Q_old[v][a] Q[v][r]: lanes l < 4 hold column r = l
-  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    const f16x8 ao = rl4 ? *(const f16x8*)&sh.qoT[l16][32 * ks + 8 * q] : z8;
-    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
-    macc = mma32(ao, bq, macc);
-  }
+  float M[RA][RA];                                    // Q_old^T Q
+  gram_t<RA>(sh.qoT, sh.qT, M);
   // P^T[r][c] = sum_v Q^T[r][v] B[c][v]  (k = v from the transposed packing)
   f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
-    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+    const f16x4 aq = rla ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
     pacc = mma16(aq, bt[nt], pacc);
   }
-  float M[4][4];
+  float uo[RA];
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int b = 0; b < NB; ++b) {
+    const f32x4 x = sh.uoc[b][16 * w + l16];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
-  const f32x4 uo = sh.uoc[16 * w + l16];
+    for (int i = 0; i < 4; ++i) uo[4 * b + i] = x[i];
+  }
   f32x4 p;
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
-    p[r] = (q == 0 && r < R) ? hround(pacc[r] + pn * corr) : 0.f;
+  for (int i = 0; i < 4; ++i) {
+    float corr = 0.f;
+#pragma unroll
+    for (int a = 0; a < RA; ++a) {
+      float m = M[a][i];                              // column r = 4 q + i of this lane
+#pragma unroll
+      for (int b = 1; b < NB; ++b) m = q == b ? M[a][4 * b + i] : m;
+      corr = a == 0 ? uo[0] * m : corr + uo[a] * m;
+    }
+    p[i] = (q < NB && 4 * q + i < R) ? hround(pacc[i] + pn * corr) : 0.f;
   }
   return p;
 }
 
 // A GDN head of K_ x V_ < 128 x 128 (kernels.py:1089: (64, 128), (64, 64)) runs zero-padded in the 128 x 128 tile:
 // its loads read zeros past its rows / columns, every product and Gram sum then only adds exact zeros, the column
-// means divide by V_, and the stores write its own rows / columns only.
-template <bool KDA, int K_ = KD, int V_ = VD>
-__device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+// means divide by V_, and the stores write its own rows / columns only.  RA = 8 (GDN 128 x 128, R = 8): the factor
+// products carry eight columns (lanes l < 32 of each MFMA) and CholeskyQR drops dependent columns (kernels.py:1744-1772).
+template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
+__device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                            float qmax) {
   static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
+  static_assert(RA == 4 || (RA == 8 && !KDA && K_ == KD && V_ == VD), "R = 8: GDN 128 x 128 heads");
+  constexpr int NB = RA / 4;
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
+  const int qb = q < NB ? q : NB - 1;                 // this lane's factor block in the MFMA operands (lanes < 16 NB)
   char* base = block_base(st, slot, hv);
   int8_t* Sq = (int8_t*)base;
   float* Sk = (float*)(base + V_ * K_);
@@ -444,9 +555,9 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   const int cvc = (K_ == KD && V_ == VD) ? cv : min(cv, nc - 1);
   const int vq = V_ == VD ? cv : min(cv, V_ - 1);
   const float scv = cok ? (colt ? Sk[cvc] : Sv[cvc]) : 0.f;
-  float uqv[4], q0v[4];
+  float uqv[RA], q0v[RA];
 #pragma unroll
-  for (int a = 0; a < 4; ++a) {
+  for (int a = 0; a < RA; ++a) {
     const float x = h2f(UQ[min(a, R - 1) * (K_ + V_) + (colt ? 0 : K_) + cvc]);
     uqv[a] = cok ? x : 0.f;
     const float y = Q0[vq * R + min(a, R - 1)];
@@ -464,25 +575,33 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
     float pcv = 1.f;
     if (KDA) pcv = expf(pbc);                                                          // kernels.py:1451
     sh.skl[c] = KDA ? scv * pcv : scv;                                                // kernels.py:1519
-    f32x4 u;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      u[a] = a < R ? uqv[a] : 0.f;
-      if (KDA) u[a] = hround(u[a] * pcv);                                             // kernels.py:1464-1465
-      sh.uoT[a][c] = f2h(u[a]);
+    for (int b = 0; b < NB; ++b) {
+      f32x4 u;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int a = 4 * b + i;
+        u[i] = a < R ? uqv[a] : 0.f;
+        if (KDA) u[i] = hround(u[i] * pcv);                                           // kernels.py:1464-1465
+        sh.uoT[a][c] = f2h(u[i]);
+      }
+      sh.uoc[b][c] = u;
     }
-    sh.uoc[c] = u;
   } else if (tid < KD + VD) {
     const int v = cv;
     sh.svr[v] = KDA ? scv * (1.0f / qmax) : scv * (pn / qmax);                       // kernels.py:1468, 1483
-    f32x4 o;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      o[a] = a < R ? uqv[a] : 0.f;
-      sh.qoT[a][v] = f2h(o[a]);
-      sh.qT[a][v] = f2h(a < R ? hround(q0v[a]) : 0.f);                                // kernels.py:1573-1577
+    for (int b = 0; b < NB; ++b) {
+      f32x4 o;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int a = 4 * b + i;
+        o[i] = a < R ? uqv[a] : 0.f;
+        sh.qoT[a][v] = f2h(o[i]);
+        sh.qT[a][v] = f2h(a < R ? hround(q0v[a]) : 0.f);                              // kernels.py:1573-1577
+      }
+      sh.qov[b][v] = o;
     }
-    sh.qov[v] = o;
   }
   if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
   __syncthreads();
@@ -518,46 +637,51 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   }
 
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
-  const f32x4 p16 = p_step(sh, bt, pn, R);            // P16 rows of this wave (lanes < 16)
+  const f32x4 p16 = p_step<RA>(sh, bt, pn, R);        // P16 rows of this wave (lanes < 16 NB)
   __syncthreads();                                    // every wave is past the rebuild: the op region is free
   // Q = B P16 + pn Q_old (U_old^T P16): per-wave partials of B P16 over the wave's 16 channels, summed below
-  if (q == 0) {
+  if (q < NB) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) sh.r.ppT[r][16 * w + l16] = f2h(p16[r]);
+    for (int i = 0; i < 4; ++i) sh.r.ppT[4 * q + i][16 * w + l16] = f2h(p16[i]);
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   {
     const f16x4 z4 = {};
-    const f16x4 ap = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][16 * w + 4 * q] : z4;   // A[r][c] = P16^T
+    const f16x4 ap = l16 < RA ? *(const f16x4*)&sh.r.ppT[l16][16 * w + 4 * q] : z4;   // A[r][c] = P16^T
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
-      const f32x4 d = mma16(ap, bh[nt], f32x4{0.f, 0.f, 0.f, 0.f});                 // Q^T[r][16 nt + l]
-      if (q == 0) sh.r.qpart[w][16 * nt + l16] = d;
+      const f32x4 d = mma16(ap, bh[nt], f32x4{0.f, 0.f, 0.f, 0.f});                 // Q^T[4 q + i][16 nt + l]
+      if (q < NB) sh.r.qpart[w][qb][16 * nt + l16] = d;
     }
   }
   __syncthreads();
   if (tid < VD) {                                     // waves 0 and 1: one row v per thread
     // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels (every column of P16 is in ppT now)
-    const f16x8 z8 = {};
-    f32x4 macc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.uoT[l16][32 * ks + 8 * q] : z8;
-      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
-      macc = mma32(ao, bp, macc);
-    }
-    float M2[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    float M2[RA][RA];
+    gram_t<RA>(sh.uoT, sh.r.ppT, M2);
     const int v = tid;
-    f32x4 s = sum_parts(sh.r.qpart, v);
-    const f32x4 qo = sh.qov[v];
+    float qo[RA];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] += pn * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
-    sh.qv[v] = s;
+    for (int b = 0; b < NB; ++b) {
+      const f32x4 x = sh.qov[b][v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qo[4 * b + i] = x[i];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      f32x4 s = sh.r.qpart[0][b][v];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) s += sh.r.qpart[w2][b][v];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float corr = qo[0] * M2[0][4 * b + i];
+#pragma unroll
+        for (int a = 1; a < RA; ++a) corr += qo[a] * M2[a][4 * b + i];
+        s[i] += pn * corr;
+      }
+      sh.qv[b][v] = s;
+    }
   }
   __syncthreads();
   // CholeskyQR2 (wave 0), fp16 Q.  The serial phases of one wave run at raised wave priority: the CU's other workgroup
@@ -565,36 +689,65 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
   // quantize 222 -> 214 us with the same in its MGS phases)
   if (w == 0) {
     __builtin_amdgcn_s_setprio(3);
-    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+    if constexpr (RA == 4) {
+      f32x4 p0 = sh.qv[0][l], p1 = sh.qv[0][l + 64];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
-    cholqr_pass(p0, p1);
-    cholqr_pass(p0, p1);
+      for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+      cholqr_pass(p0, p1);
+      cholqr_pass(p0, p1);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      p0[r] = r < R ? hround(p0[r]) : 0.f;
-      p1[r] = r < R ? hround(p1[r]) : 0.f;
-      sh.qT[r][l] = f2h(p0[r]);
-      sh.qT[r][l + 64] = f2h(p1[r]);
+      for (int r = 0; r < 4; ++r) {
+        p0[r] = r < R ? hround(p0[r]) : 0.f;
+        p1[r] = r < R ? hround(p1[r]) : 0.f;
+        sh.qT[r][l] = f2h(p0[r]);
+        sh.qT[r][l + 64] = f2h(p1[r]);
+      }
+      sh.qv[0][l] = p0;
+      sh.qv[0][l + 64] = p1;
+    } else {
+      float p0[RA], p1[RA];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const f32x4 x0 = sh.qv[b][l], x1 = sh.qv[b][l + 64];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p0[4 * b + i] = 4 * b + i < R ? x0[i] : 0.f;
+          p1[4 * b + i] = 4 * b + i < R ? x1[i] : 0.f;
+        }
+      }
+      cholqr_pass_drop<RA>(p0, p1);
+      cholqr_pass_drop<RA>(p0, p1);
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        f32x4 y0, y1;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * b + i;
+          y0[i] = r < R ? hround(p0[r]) : 0.f;
+          y1[i] = r < R ? hround(p1[r]) : 0.f;
+          sh.qT[r][l] = f2h(y0[i]);
+          sh.qT[r][l + 64] = f2h(y1[i]);
+        }
+        sh.qv[b][l] = y0;
+        sh.qv[b][l + 64] = y1;
+      }
     }
-    sh.qv[l] = p0;
-    sh.qv[l + 64] = p1;
     __builtin_amdgcn_s_setprio(0);
   }
   __syncthreads();
-  const f32x4 u16 = p_step(sh, bt, pn, R);            // U16 = P step with Q16 (lanes < 16: rows 16 w + l)
+  const f32x4 u16 = p_step<RA>(sh, bt, pn, R);        // U16 = P step with Q16 (lanes < 16 NB: rows 16 w + l)
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
   Tile t;
   {
     const f16x4 z4 = {};
-    const f16x4 auo = q == 0 ? to_h4(sh.uoc[16 * w + l16]) : z4;                     // A[c][a] = U_old
-    const f16x4 aun = q == 0 ? to_h4(-u16) : z4;                                     // A[c][r] = -U16
+    const f16x4 auo = q < NB ? to_h4(sh.uoc[qb][16 * w + l16]) : z4;                // A[c][a] = U_old
+    const f16x4 aun = q < NB ? to_h4(-u16) : z4;                                     // A[c][r] = -U16
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + l16;
-      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                               // B[a][v] = Q_old^T
-      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                                // B[r][v] = Q16^T
+      const f16x4 bqo = q < NB ? to_h4(sh.qov[qb][v]) : z4;                           // B[a][v] = Q_old^T
+      const f16x4 bqn = q < NB ? to_h4(sh.qv[qb][v]) : z4;                            // B[r][v] = Q16^T
       f32x4 e = from_h4(bh[nt]);
       if (!KDA) e *= rpn;
       e = mma16(auo, bqo, e);
@@ -660,11 +813,13 @@ __device__ void flush_head(FlushShared& sh, const lq_state& st, const float* __r
       *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
-  if (q == 0 && (K_ == KD || 16 * w + l16 < K_)) {
-    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + 16 * w + l16] = f2h(u16[r]);
+  if (q < NB && (K_ == KD || 16 * w + l16 < K_)) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * q + i < R) UQ[(4 * q + i) * (K_ + V_) + 16 * w + l16] = f2h(u16[i]);
   }
   if (tid < V_) {
-    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[r >> 2][tid][r & 3]);
   }
   if (KDA) {
     if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;

@@ -42,7 +42,7 @@ extern "C" int lq_decode_noalloc(const lq_state* st, const lq_step_io* io, const
   int rc = lq_check_step(st, io);
   if (rc) return rc;
   if (kda != 0 && kda != 1) return LQ_ERR_ARG;
-  if (kda && (!st->Gbuf || st->K != 128 || st->V != 128)) return LQ_ERR_ARG;
+  if (kda && (!st->Gbuf || st->K != 128 || st->V != 128 || st->R > 4)) return LQ_ERR_ARG;
   const float qmax = st->qmax > 0.f ? st->qmax : LQ_QMAX;
   rc = lq_check_flush(st, Q0, io->idx, io->N, kda, qmax);
   if (rc) return rc;

@@ -57,7 +57,7 @@ constexpr float KSPLIT = 64.0f;   // kn / qn scaled by 2^6 before the fp16 hi / 
 // padded by 16 bytes so that those rows start in different LDS banks (unpadded, 128- or 256-byte rows all start in
 // the same bank).
 constexpr int DIGP = 16, OPP = 8;
-template <int K_, int V_, int G>
+template <int K_, int V_, int G, int RM>
 struct StepShared {
   bf16_t ub[G][LMAX][V_];  // the window's u_j rows per value head (direct global -> LDS loads)
   int8_t dig[G][6][K_ + DIGP];   // int8 GEMV B operand: k digits 0-2, q digits 0-2
@@ -65,7 +65,7 @@ struct StepShared {
   f16_t hkq[4][K_ + OPP];        // factor-dot B operand: fp16 hi / lo of 64 kn, then of 64 qn
   float2 mq[G][V_];        // GEMV rows (k, q) in digit units
   float2 cwq[G][LMAX];     // (w_j dk_j, w_j dq_j) per value head: buffered entry j's coefficients in A4 / A5
-  float2 duq[G][4];        // (dU_r, dQ_r) per value head, factor r
+  float2 duq[G][RM];       // (dU_r, dQ_r) per value head, factor r
   float w[G][LMAX];        // gated entry weights w_j per value head
   float sc[G][8];          // per value head: alpha, beta, kappa, kmax, qmax
 };
@@ -90,29 +90,33 @@ struct StepShared {
 // call instead of two.  The step's LDS and the flush's share the same bytes (both fit the 40 KiB that four workgroups
 // per CU allow).
 // ------------------------------------------------------------------------------------------------------------------
-template <int K_, int V_, int G, bool FL>
+template <int K_, int V_, int G, bool FL, int RM>
 struct StepLds {
-  StepShared<K_, V_, G> st;
+  StepShared<K_, V_, G, RM> st;
 };
-template <int K_, int V_, int G>
-struct StepLds<K_, V_, G, true> {
+template <int K_, int V_, int G, int RM>
+struct StepLds<K_, V_, G, true, RM> {
   union {
-    StepShared<K_, V_, G> st;
+    StepShared<K_, V_, G, RM> st;
     lqf::FlushShared4 fl;
   };
 };
 
-template <int K_, int V_, int G, bool CONV, bool FL>
+// RM: factors held per head.  4 (R <= 4): the G R <= 16 factor rows of the workgroup's heads are one MFMA tile, taken
+// by the last wave.  16 (the rank ablation R <= 16, K = V = 128; kernels.py:63, 457-469): up to G tiles, tile g taken
+// by the second wave of head g.
+template <int K_, int V_, int G, bool CONV, bool FL, int RM = 4>
 __global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
 void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const float* Q0) {
   static_assert(!FL || (K_ == 128 && V_ == 128 && G == 2), "fused flush: the four-wave layout, 128 x 128 heads");
+  static_assert(RM == 4 || (RM == 16 && K_ == 128 && V_ == 128 && !FL), "ranks above 4: 128 x 128 heads, no fused flush");
   constexpr int KD = K_, VD = V_;
   constexpr int WPH = VD / 64;  // waves per value head
   constexpr int NE = KD / 64;   // channels per lane in the scalar work
   constexpr int KS32 = KD / 32, KS64 = KD / 64;   // k-steps of the 16x16x32 (bf16 / fp16) and 16x16x64 (int8) MFMAs
   constexpr bool NT = KD == 128;                  // non-temporal bulk loads (see ld_once)
-  __shared__ StepLds<K_, V_, G, FL> lds;
-  StepShared<K_, V_, G>& sh = lds.st;
+  __shared__ StepLds<K_, V_, G, FL, RM> lds;
+  StepShared<K_, V_, G, RM>& sh = lds.st;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int n = blockIdx.x / H;
   const int hk = blockIdx.x - n * H;
@@ -161,11 +165,12 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const bf16_t araw = ((const bf16_t*)io.a)[(long long)n * HV + hv];
   const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
   const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
-  // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA (last wave)
+  // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA, tile ft of them
   f16x8 ufr[KS32];
-  const bool fwave = wv == WPH * G - 1;
+  const int ft = RM == 4 ? 0 : g;
+  const bool fwave = RM == 4 ? wv == WPH * G - 1 : (wi == WPH - 1 && 16 * g < G * R);
   {
-    const int m = n16 < G * R ? n16 : 0, g2 = m / R, r = m - g2 * R;
+    const int m = 16 * ft + n16 < G * R ? 16 * ft + n16 : 0, g2 = m / R, r = m - g2 * R;
     const f16_t* U = (const f16_t*)(block_base(st, slot, hk * G + g2) + VD * KD + 4 * (KD + VD)) + r * (KD + VD);
 #pragma unroll
     for (int ks = 0; ks < KS32; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
@@ -174,9 +179,9 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   if (CONV) vtap = conv_taps(cv, mrow, cvb, 2 * H * KD + hv * VD + lt);
   else vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
-  float qt[4];                  // Q^T[r][lt]
+  float qt[RM];                 // Q^T[r][lt]
 #pragma unroll
-  for (int r = 0; r < 4; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
+  for (int r = 0; r < RM; ++r) qt[r] = h2f(UQp[min(r, R - 1) * (KD + VD) + KD + lt]);
   const float P = st.Pbuf[sh_];
   // Window fills of the G value heads: uniform loads, served by the scalar data cache.  A vector load here would queue
   // behind the bulk loads the CU's other workgroups have issued, and every later load of this workgroup waits for it.
@@ -397,7 +402,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const float s = (acc[i] + dpp<DPP_XOR1>(acc[i])) * (1.0f / KSPLIT);               // hi + lo (lanes 0 / 2)
-      const int m = 4 * q4 + i;
+      const int m = 16 * ft + 4 * q4 + i;
       if ((n16 == 0 || n16 == 2) && m < G * R) ((float*)&sh.duq[m / R][m % R])[n16 >> 1] = s;
     }
   }
@@ -433,10 +438,13 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
     a5 = fmaf(ub, c.y, a5);
   }
   float a6 = 0.f, a7 = 0.f;
-  for (int r = 0; r < R; ++r) {
-    const float2 d = sh.duq[g][r];
-    a6 = fmaf(qt[r], d.x, a6);
-    a7 = fmaf(qt[r], d.y, a7);
+#pragma unroll
+  for (int r = 0; r < RM; ++r) {
+    if (r < R) {
+      const float2 d = sh.duq[g][r];
+      a6 = fmaf(qt[r], d.x, a6);
+      a7 = fmaf(qt[r], d.y, a7);
+    }
   }
   // ---- int8 GEMV on the matrix cores (the tile is the last data to arrive).  B columns: 0 / 4 / 8 = k digits 0 / 1 / 2, 1 / 5 / 9 = q digits, others 0 ----
   {
@@ -868,7 +876,8 @@ static bool gdn_dims(int K, int V) { return (K == 128 && V == 128) || (K == 64 &
 
 int lq_check_step(const lq_state* st, const lq_step_io* io) {
   if (!st || !io) return LQ_ERR_ARG;
-  if (!gdn_dims(st->K, st->V) || st->L < 1 || st->L > LMAX || st->R < 1 || st->R > 4) return LQ_ERR_ARG;
+  if (!gdn_dims(st->K, st->V) || st->L < 1 || st->L > LMAX || st->R < 1) return LQ_ERR_ARG;
+  if (st->R > (st->K == 128 && st->V == 128 ? LQ_STEP_RMAX : 4)) return LQ_ERR_ARG;   // kernels.py:63-64
   if (st->H <= 0 || st->HV <= 0 || st->HV % st->H != 0 || st->NS <= 0 || io->N < 0) return LQ_ERR_ARG;
   if (!st->ssm || !st->Kbuf || !st->Ubuf || !st->Wbuf || !st->Pbuf || !st->hcnt) return LQ_ERR_ARG;
   // 16-byte loads of the int8 rows and of the scale / factor block need a 16-byte aligned block start
@@ -880,13 +889,13 @@ int lq_check_step(const lq_state* st, const lq_step_io* io) {
   return LQ_OK;
 }
 
-template <int K_, int V_, bool CONV>
+template <int K_, int V_, bool CONV, int RM = 4>
 static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
   dim3 grid((unsigned)(io->N * st->H));
   switch (st->HV / st->H) {
-    case 1: gdn_step_kernel<K_, V_, 1, CONV, false><<<grid, V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
-    case 2: gdn_step_kernel<K_, V_, 2, CONV, false><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
-    case 4: gdn_step_kernel<K_, V_, 4, CONV, false><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 1: gdn_step_kernel<K_, V_, 1, CONV, false, RM><<<grid, V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 2: gdn_step_kernel<K_, V_, 2, CONV, false, RM><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 4: gdn_step_kernel<K_, V_, 4, CONV, false, RM><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
@@ -894,6 +903,7 @@ static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& c
 
 template <bool CONV>
 static int launch_gdn_dims(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
+  if (st->K == 128 && st->R > 4) return launch_gdn<128, 128, CONV, LQ_STEP_RMAX>(st, io, cv, dlist, s);
   if (st->K == 128) return launch_gdn<128, 128, CONV>(st, io, cv, dlist, s);
   return st->V == 128 ? launch_gdn<64, 128, CONV>(st, io, cv, dlist, s) : launch_gdn<64, 64, CONV>(st, io, cv, dlist, s);
 }
@@ -905,6 +915,7 @@ int lq_launch_step(const lq_state* st, const lq_step_io* io, int kda, float glb,
     const lq_conv none = {};
     return launch_gdn_dims<false>(st, io, none, dlist, s);
   }
+  if (st->R > 4) return LQ_ERR_ARG;           // the KDA step holds four factors (kernels.py:1036)
   kda_step_kernel<<<dim3((unsigned)(io->N * st->HV)), 128, 0, s>>>(*st, *io, glb, dlist);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
@@ -943,7 +954,7 @@ extern "C" int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_
   if ((rc = lq_check_flush(st, Q0, io->idx, io->N, 0, qmax))) return rc;
   if (io->N == 0) return LQ_OK;
   hipStream_t s = (hipStream_t)stream;
-  if (st->K == 128 && st->V == 128 && st->HV == 2 * st->H) {      // one launch: the step flushes its own due heads
+  if (st->K == 128 && st->V == 128 && st->HV == 2 * st->H && st->R <= 4) {   // one launch: the step flushes its own due heads
     const dim3 grid((unsigned)(io->N * st->H));
     const lq_conv none = {};
     if (cv) gdn_step_kernel<128, 128, 2, true, true><<<grid, 256, 0, s>>>(*st, *io, *cv, nullptr, Q0);
@@ -958,7 +969,7 @@ extern "C" int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_
 extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream) {
   int rc = lq_check_step(st, io);
   if (rc) return rc;
-  if (!st->Gbuf || st->K != KD || st->V != VD) return LQ_ERR_ARG;
+  if (!st->Gbuf || st->K != KD || st->V != VD || st->R > 4) return LQ_ERR_ARG;
   return lq_launch_step(st, io, 1, glb, nullptr, (hipStream_t)stream);
 }
 

@@ -11,6 +11,9 @@ Deliberate differences (documented in the package's design notes):
   * The NVIDIA schedule knobs (SMS, NSTAGE, NSTAGEQ, NCG, NNW, MAXIT, PAD, MMT, NTP, RSG, threads, BV) are accepted
     and ignored: the HIP kernels have one schedule for gfx950.
   * The window may be up to 64 entries (the reference's kernels stop at 16 / 32).
+  * Ranks as the reference's asserts allow (kernels.py:63-64, 1091): R <= 4, plus R in {8, 12, 16} for the GDN step
+    and R = 8 for the GDN flush at (K, V) = (128, 128); make_quantize / make_dequant take any R a step can read
+    (the reference's quantize has no bound of its own beyond the slot fit).
   * make_gdn_step / make_kda_step / make_flush / make_quantize / make_dequant take a code range `qmax` (127: INT8,
     default; 31: 6-bit codes in the same int8 container).
 """
@@ -57,11 +60,17 @@ def _need(t, dtype, shape, name):
 GDN_DIMS = ((128, 128), (64, 128), (64, 64))        # kernels.py:62, 1089 (KDA: 128 x 128 only, 727)
 
 
-def _check_dims(K, V, L, R, kda=False):
+def _check_dims(K, V, L, R, kda=False, rank="step"):
+    """Static shape checks.  `rank`: whose rank rule applies -- "step" (kernels.py:63-64: R <= 4, or R in {8, 12, 16}
+    at 128 x 128), "flush" (kernels.py:1091: R <= 4, or R = 8 for GDN 128 x 128) or "checkpoint" (quantize / dequant:
+    any rank a step reads).  KDA keeps R <= 4 throughout (its step holds four factors, kernels.py:1036)."""
     dims = ((128, 128),) if kda else GDN_DIMS
     assert (K, V) in dims, "liblq: head dims (K, V) in %s, got (%d, %d)" % (dims, K, V)
     assert 1 <= L <= LMAX, "liblq: window 1 <= L <= %d, got %d" % (LMAX, L)
-    assert 1 <= R <= 4, "liblq: rank 1 <= R <= 4, got %d" % R
+    wide = (K, V) == (128, 128) and not kda
+    ok = {"step": wide and R % 4 == 0 and R <= 16, "flush": wide and R == 8, "checkpoint": wide and R <= 16}[rank]
+    assert R >= 1 and (R <= 4 or ok), \
+        "liblq: rank R = %d not supported here (%s, (K, V) = (%d, %d)%s)" % (R, rank, K, V, ", KDA" if kda else "")
     assert V * K // 4 + K + V + R * (K + V) // 2 <= V * K, "checkpoint must fit inside the fp32 slot"
 
 
@@ -171,7 +180,7 @@ def make_flush(NS, HV, K, V, L, SS, R=4, ITERS=1, SMS=None, NCG=3, MAXIT=128, PA
     """End-of-window flush (kernels.py:1077-2033).  Returns
     flush(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx).  Due heads (hcnt == L) are found on
     the device; ITERS = 1 and PNMIN = 1e-20 as in the reference's use (state.py:79)."""
-    _check_dims(K, V, L, R, kda=KDA)
+    _check_dims(K, V, L, R, kda=KDA, rank="flush")
     assert ITERS == 1, "liblq: one subspace iteration per flush (ITERS = 1)"
     assert PNMIN == 1e-20
     L_ = _lib.lib()
@@ -201,7 +210,7 @@ def make_dequant(NS, HV, K, V, L, SS, BV=32, threads=128, kda=False, buf_dtype=F
     """Prefill round trip, part 1 (kernels.py:2041-2123): fp32 S[slot] <- decay deq(S0) + window, then window reset.
     Returns dequant(S0, Sq, Sk, Sv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, UQ, idx).  GDN with bf16 buffers only (the
     reference's KDA branch is never called: state.py:80-82)."""
-    _check_dims(K, V, L, max(R, 1))
+    _check_dims(K, V, L, max(R, 1), rank="checkpoint")
     assert not kda and buf_dtype == BF16 and R >= 1, "liblq: GDN dequant with bf16 buffers and R >= 1"
     L_ = _lib.lib()
 
@@ -221,7 +230,7 @@ def make_dequant(NS, HV, K, V, L, SS, BV=32, threads=128, kda=False, buf_dtype=F
 def make_quantize(NS, HV, K, V, L, SS, R=4, ITERS=1, threads=128, qmax=QMAX):
     """Prefill round trip, part 2 (kernels.py:2126-2242): 8-bit checkpoint of the fp32 states of the listed slots,
     then window reset.  Returns quantize(S0, Sq, Sk, Sv, UQ, Wbuf, Pbuf, hcnt, Q0, idx)."""
-    _check_dims(K, V, L, R)
+    _check_dims(K, V, L, R, rank="checkpoint")
     assert ITERS == 1, "liblq: ITERS = 1"
     L_ = _lib.lib()
 

@@ -332,9 +332,12 @@ def kda_step(st, mixed, a, b, A_log, dt_bias, idx, glb=0.0, scale=None, qmax=QMA
 # CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835), float64
 # ----------------------------------------------------------------------------------------------------------------
 def cholqr_pass(pr):
-    """pr: [D,V,R] (R <= 4 used; zero columns beyond R).  Returns pr L^{-T} with the relative pivot floor
-    d_j -> max(d_j, 1e-6 G_jj) (j >= 1) and the absolute floor 1e-30 before every rsqrt."""
+    """pr: [D,V,R].  Returns pr L^{-T}.  R <= 4 (kernels.py:1781-1835): relative pivot floor d_j -> max(d_j, 1e-6 G_jj)
+    (j >= 1) and the absolute floor 1e-30 before every rsqrt.  R > 4 (the R = 8 flush, kernels.py:1744-1772): a pivot
+    with d_j <= 1e-6 G_jj + 1e-30 drops its column (1 / L_jj = 0) instead."""
     D, V, R = pr.shape
+    if R > 4:
+        return _cholqr_pass_drop(pr)
     Gm = np.einsum("dvr,dvs->drs", pr, pr)
     ll = {}
     out = pr.copy()
@@ -355,6 +358,26 @@ def cholqr_pass(pr):
         for m_ in range(j):
             acc -= out[:, :, m_] * ll[(j, m_)][:, None]
         out[:, :, j] = acc * ll[(j, j)][:, None]
+    return out
+
+
+def _cholqr_pass_drop(pr):
+    """The R > 4 CholeskyQR pass: Cholesky of the Gram matrix column by column; column j is kept when its remaining
+    pivot exceeds 1e-6 G_jj + 1e-30 and scaled by its reciprocal square root, else zeroed together with its entries
+    in L (kernels.py:1758-1767)."""
+    D, V, R = pr.shape
+    Gm = np.einsum("dvr,dvs->drs", pr, pr)
+    ll = np.zeros((D, R, R))
+    for j in range(R):
+        for kk in range(j):
+            ll[:, j, kk] = (Gm[:, j, kk] - (ll[:, j, :kk] * ll[:, kk, :kk]).sum(-1)) * ll[:, kk, kk]
+        acc = Gm[:, j, j] - (ll[:, j, :j] ** 2).sum(-1)
+        keep = acc > 1e-6 * Gm[:, j, j] + 1e-30
+        ll[:, j, j] = np.where(keep, 1.0 / np.sqrt(np.maximum(acc, 1e-30)), 0.0)
+    out = pr.copy()
+    for j in range(R):
+        acc = out[:, :, j] - np.einsum("dvm,dm->dv", out[:, :, :j], ll[:, j, :j])
+        out[:, :, j] = acc * ll[:, j, j][:, None]
     return out
 
 
@@ -382,9 +405,10 @@ def due_pairs(st, idx):
     return out
 
 
-def flush(st, Q0, idx, qmax=QMAX, return_debug=False):
+def flush(st, Q0, idx, qmax=QMAX, return_debug=False, b_hook=None):
     """Flush every due (slot, head) in place: rebuild B, one subspace iteration from Q0 with CholeskyQR2, new fp16
-    factors, smoothed residual, INT8 (or qmax) codes, window reset."""
+    factors, smoothed residual, INT8 (or qmax) codes, window reset.  b_hook (tests only): a function applied to the
+    rebuilt fp16 B [D,V,K] before the subspace step, to measure how the outputs respond to a change of B."""
     NS, HV, H, K, V, L, R = _dims(st)
     G = HV // H
     kda = st["kda"]
@@ -432,6 +456,8 @@ def flush(st, Q0, idx, qmax=QMAX, return_debug=False):
         rpn = None
     deq = r32(r32(code * svr[:, :, None]) * skl[:, None, :])                                     # kernels.py:1534-1535
     B = fp16(deq.astype(np.float64) + ring).astype(np.float64)                                  # kernels.py:1564-1571
+    if b_hook is not None:
+        B = b_hook(B)
     Q16 = np.broadcast_to(fp16(Q0).astype(np.float64), (len(pairs),) + Q0.shape).copy()         # kernels.py:1573-1577
     p = pn64[:, None, None]
 

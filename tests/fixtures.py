@@ -48,6 +48,31 @@ def make_state(rng, NS, HV, H, K=128, V=128, L=16, R=4, kda=False, sigma=0.02, q
     return st, S, Q0
 
 
+def oracle_steps(rng, st, steps, NS, HV, H, flush_Q0=None):
+    """GDN oracle decode steps on random subsets of the slots 1..NS-1, each followed by the flush when flush_Q0 is
+    given (every slot then ends at its own window fill)."""
+    A_log, dt_bias = gate_params(HV)
+    for _ in range(steps):
+        sl = rng.permutation(np.arange(1, NS))[: rng.integers(1, NS)]
+        mixed, a, b = make_inputs(rng, len(sl), HV, H)
+        O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
+        if flush_Q0 is not None:
+            O.flush(st, flush_Q0, sl)
+
+
+def due_flush_case(rng, L, R=4, NS=6, HV=4, H=2):
+    """(state, Q0): a GDN state at rank R after L + 5 steps-and-flushes, then slots 1 and 3 stepped to a full window
+    (due), the other slots partial."""
+    st, _, Q0 = make_state(rng, NS, HV, H, L=L, R=R)
+    oracle_steps(rng, st, L + 5, NS, HV, H, flush_Q0=Q0)
+    A_log, dt_bias = gate_params(HV)
+    for s in (1, 3):
+        while st["hcnt"][s, 0] < L:
+            mixed, a, b = make_inputs(rng, 1, HV, H)
+            O.gdn_step(st, mixed, a, b, A_log, dt_bias, np.array([s]))
+    return st, Q0
+
+
 def make_trajectory(kda=False, L=16, steps=35, seed=0, NS=4, HV=2, H=None, K=128, V=128, R=4):
     """Runs `steps` oracle decode steps (each followed by the flush) on a small state; returns a dict of arrays."""
     H = (2 if kda else 1) if H is None else H

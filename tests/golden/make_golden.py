@@ -19,7 +19,7 @@ sys.path.insert(0, os.path.join(HERE, "..", ".."))
 
 def write_q0():
     import torch
-    for V, R in ((128, 4), (128, 1), (128, 2), (64, 4)):
+    for V, R in ((128, 4), (128, 1), (128, 2), (64, 4), (128, 8), (128, 12), (128, 16)):
         q0 = torch.randn(V, R, generator=torch.Generator().manual_seed(0)).numpy().astype(np.float32)
         np.save(os.path.join(HERE, "q0_%dx%d.npy" % (V, R)), q0)
 

@@ -2,9 +2,34 @@
 import numpy as np
 import torch
 
-from leapquant_amd.state import LeapQuantState
+from leapquant_amd.state import LeapQuantState, state_views
 
 DEV = "cuda:0"
+
+
+class RawGdnState:
+    """The GDN buffers LeapQuantState allocates (state.py:61-70), loaded from an oracle state, without its kernel set:
+    the rank ablation R = 12, 16 has a step, quantize and dequant but no flush (kernels.py:63, 1091), so a
+    LeapQuantState -- which builds all four, as the reference's does -- refuses it.  Quacks like one for load_state /
+    from_gpu."""
+    kda = False
+
+    def __init__(self, st):
+        NS, HV, V, K = st["Sq"].shape
+        self.NS, self.HV, self.K, self.V = NS, HV, K, V
+        self.H, self.L, self.R = st["Kbuf"].shape[1], st["Wbuf"].shape[-1], st["UQ"].shape[2]
+        self.ssm = torch.zeros(NS, HV, V, K, device=DEV)
+        self.SS = self.ssm.stride(0)
+        self.Kbuf = torch.zeros(NS, self.H, self.L, K, dtype=torch.bfloat16, device=DEV)
+        self.Ubuf = torch.zeros(NS, HV, self.L, V, dtype=torch.bfloat16, device=DEV)
+        self.Wbuf = torch.zeros(NS, HV, self.L, device=DEV)
+        self.Pbuf = torch.ones(NS, HV, 1, device=DEV)
+        self.hcnt = torch.zeros(NS, HV, dtype=torch.int32, device=DEV)
+        self.Gbuf = None
+        load_state(self, self.ssm, st)
+
+    def views(self, ssm):
+        return state_views(ssm, self.R)
 
 
 def to_gpu(st, H=None, qmax=127.0, glb=0.0):

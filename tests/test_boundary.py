@@ -60,7 +60,7 @@ def _io(**kw):
     return _lib.LqStepIO(**d)
 
 
-BAD_STATES = [dict(K=96), dict(V=64), dict(K=32, V=32), dict(L=0), dict(L=65), dict(R=0), dict(R=5), dict(H=0), dict(HV=3),
+BAD_STATES = [dict(K=96), dict(V=64), dict(K=32, V=32), dict(L=0), dict(L=65), dict(R=0), dict(R=17), dict(H=0), dict(HV=3),
               dict(NS=0), dict(slot_stride=100), dict(slot_stride=4 * 128 * 128 + 1), dict(ssm=8), dict(ssm=None),
               dict(hcnt=None), dict(Wbuf=None)]
 BAD_STEP_STATES = [dict(qmax=0.5), dict(qmax=128.0), dict(qmax=-31.0), dict(qmax=float("nan"))]
@@ -93,6 +93,47 @@ def test_entry_points_reject_bad_state(lib, bad):
                                z) == -1
         assert lib.lq_kda_checkpoint(ctypes.byref(st), ctypes.c_void_p(16), ctypes.c_void_p(16), 0,
                                      ctypes.c_float(127.0), z) == -1
+
+
+def test_rank_limits(lib):
+    """Ranks above 4 (kernels.py:63-64, 1091): GDN 128 x 128 steps take R <= 16, its flush R <= 8, quantize / dequant
+    R <= 16; KDA and the 64-dim heads stay at R <= 4.  The factories keep the reference's own sets (step R in
+    {8, 12, 16}, flush R = 8)."""
+    z, p = ctypes.c_void_p(0), ctypes.c_void_p(16)
+    io = _io()
+    for R in (5, 8, 12, 16):
+        st = _state(R=R)
+        assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == 0
+        assert lib.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(0.0), z) == -1
+        assert lib.lq_flush(ctypes.byref(st), p, p, 0, 0, ctypes.c_float(127.0), z) == (0 if R <= 8 else -1)
+        assert lib.lq_flush(ctypes.byref(st), p, p, 0, 1, ctypes.c_float(127.0), z) == -1
+        assert lib.lq_gdn_decode(ctypes.byref(st), ctypes.byref(io), None, p, z) == (0 if R <= 8 else -1)
+        assert lib.lq_quantize(ctypes.byref(st), p, p, 0, ctypes.c_float(127.0), z) == 0
+        assert lib.lq_dequant(ctypes.byref(st), p, 0, ctypes.c_float(127.0), z) == 0
+        assert lib.lq_kda_dequant(ctypes.byref(st), p, 0, ctypes.c_float(127.0), z) == -1
+        assert lib.lq_kda_checkpoint(ctypes.byref(st), p, p, 0, ctypes.c_float(127.0), z) == -1
+        for K, V in ((64, 128), (64, 64)):
+            st = _state(R=R, K=K, V=V)
+            assert lib.lq_gdn_step(ctypes.byref(st), ctypes.byref(io), z) == -1
+            assert lib.lq_flush(ctypes.byref(st), p, p, 0, 0, ctypes.c_float(127.0), z) == -1
+            assert lib.lq_quantize(ctypes.byref(st), p, p, 0, ctypes.c_float(127.0), z) == -1
+    from leapquant_amd import kernels as KN
+    SS = 32 * 128 * 128
+    for R in (1, 4, 8, 12, 16):
+        KN.make_gdn_step(4, 32, 16, 128, 128, 16, SS, R=R)
+        KN.make_quantize(4, 32, 128, 128, 16, SS, R=R)
+        KN.make_dequant(4, 32, 128, 128, 16, SS, buf_dtype=KN.BF16, R=R)
+    KN.make_flush(4, 32, 128, 128, 16, SS, R=8)
+    for bad in (dict(R=6), dict(R=20), dict(R=8, K=64, SS=32 * 64 * 128)):
+        kw = dict(K=128, SS=SS)
+        kw.update(bad)
+        with pytest.raises(AssertionError):
+            KN.make_gdn_step(4, 32, 16, kw["K"], 128, 16, kw["SS"], R=kw["R"])
+    for bad in (dict(R=12), dict(R=6), dict(R=8, KDA=True)):
+        with pytest.raises(AssertionError):
+            KN.make_flush(4, 32, 128, 128, 16, SS, **bad)
+    with pytest.raises(AssertionError):
+        KN.make_kda_step(4, 32, 32, 128, 128, 16, SS, R=8)
 
 
 @pytest.mark.parametrize("K,V", [(64, 128), (64, 64)])

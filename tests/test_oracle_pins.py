@@ -15,15 +15,18 @@ import numpy as np
 import pytest
 
 from oracle import lq_oracle as O
-from tests.fixtures import from_bits, gate_params, make_inputs, make_state, state_from_npz
+from tests.fixtures import due_flush_case, from_bits, gate_params, make_inputs, make_state, state_from_npz
 
 K = V = 128
 GOLD = os.path.join(os.path.dirname(__file__), "golden")
 # head dims (K, V): GDN (128, 128), (64, 128), (64, 64) (kernels.py:62, 1089); KDA 128 x 128 (kernels.py:727)
 GDN_DIMS = [(128, 128), (64, 128), (64, 64)]
 STEP_CASES = [(False, d) for d in GDN_DIMS] + [(True, (128, 128))]
-# (kda, dims, glb): KDA also with GLM's bounded gate (kernels.py:702-712)
-TRAJ_CASES = [(False, d, 0.0) for d in GDN_DIMS] + [(True, (128, 128), 0.0), (True, (128, 128), -5.0)]
+# (kda, dims, glb, R): KDA also with GLM's bounded gate (kernels.py:702-712); the GDN rank ablation R = 16 (kernels.py:63)
+TRAJ_CASES = [(False, d, 0.0, 4) for d in GDN_DIMS] + [(True, (128, 128), 0.0, 4), (True, (128, 128), -5.0, 4),
+                                                        (False, (128, 128), 0.0, 16)]
+# (kda, dims, R): the flush's ranks, R = 8 for GDN 128 x 128 (kernels.py:1091)
+FLUSH_CASES = [(k, d, 4) for k, d in STEP_CASES] + [(False, (128, 128), 8)]
 
 
 def _qk_from_mixed(mixed, H, HV, K=K, V=V):
@@ -41,15 +44,15 @@ def _sign_fixed_qr(X):
 
 
 # ------------------------------------------------------------------------------------------------ steps vs dense rule
-@pytest.mark.parametrize("kda,dims,glb", TRAJ_CASES)
+@pytest.mark.parametrize("kda,dims,glb,R", TRAJ_CASES)
 @pytest.mark.parametrize("HV,H", [(2, 1), (2, 2), (4, 2)])
-def test_step_trajectory_matches_dense_rule(kda, dims, glb, HV, H):
+def test_step_trajectory_matches_dense_rule(kda, dims, glb, R, HV, H):
     """Evolve a dense float64 state with the textbook rule beside the oracle's checkpoint + window representation
     (no flush: L = 64 > steps); the materialised oracle state and the outputs must track it."""
     K, V = dims
-    rng = np.random.default_rng(11 + HV + 10 * H + 100 * kda + K + V)
+    rng = np.random.default_rng(11 + HV + 10 * H + 100 * kda + K + V + R)
     NS, L = 3, 64
-    st, _, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=L, kda=kda)
+    st, _, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=L, R=R, kda=kda)
     idx = np.array([2, 1, 0])
     A_log, dt_bias = gate_params(HV, K, kda)
     A_log[:] = rng.uniform(-1.0, 0.5, HV)               # exercise A_log / dt_bias too
@@ -231,12 +234,69 @@ def test_flush_of_a_rank_deficient_state():
     assert np.all(np.abs(after - S) <= bound)
 
 
-def _rank2_state(L=16, seed=71):
+def test_cholqr_drop_rule_against_qr():
+    """The R = 8 CholeskyQR (kernels.py:1744-1772), two passes: a full-rank block ends as numpy's QR with a positive
+    diagonal; a block whose columns 3 and 6 repeat earlier directions ends with exactly those columns zero and the
+    others equal to the QR of the independent columns (the R <= 4 rule would floor the pivot instead)."""
+    rng = np.random.default_rng(3)
+    X = rng.standard_normal((2, 128, 8))
+    X[1, :, 3] = X[1, :, 0] - 2 * X[1, :, 1]
+    X[1, :, 6] = 0.5 * X[1, :, 2]
+    Y = O.cholqr_pass(O.cholqr_pass(X))
+    assert np.abs(Y[0] - _sign_fixed_qr(X[0])).max() < 1e-10
+    keep = [0, 1, 2, 4, 5, 7]
+    assert np.all(Y[1][:, [3, 6]] == 0.0)
+    assert np.abs(Y[1][:, keep] - _sign_fixed_qr(X[1][:, keep])).max() < 1e-8
+    # the floor of the R <= 4 pass keeps a dependent column alive (scaled noise) instead of dropping it
+    Z = X[1][:, :4]
+    assert np.any(O.cholqr_pass(Z[None])[0][:, 3] != 0.0)
+
+
+def test_flush_r8_code_sensitivity():
+    """Sets the R = 8 flush's GPU code bar (0.5 %).  A change of ONE fp16 ulp in one entry of each head's rebuilt B --
+    the size by which two correct fp32 window rebuilds differ -- moves > 0.1 % of the R = 8 codes (by one LSB each), but
+    well under 0.1 % at R = 4: the fp16 rounding of Q after an orthogonalisation with condition numbers of 10-20 turns
+    differences of ~1e-6 into rounding flips of whole factor columns."""
+    def bump(B):
+        B = B.copy()
+        for d in range(B.shape[0]):
+            B[d, 3, 5] = float(np.nextafter(np.float16(B[d, 3, 5]), np.float16(np.inf)))
+        return B
+    moved = {}
+    for R in (4, 8):
+        st, Q0 = due_flush_case(np.random.default_rng(864), 64, R=R)
+        a, b = O.copy_state(st), O.copy_state(st)
+        idx = np.array([1, 3])
+        O.flush(a, Q0, idx)
+        O.flush(b, Q0, idx, b_hook=bump)
+        d = np.abs(a["Sq"][[1, 3]].astype(np.int32) - b["Sq"][[1, 3]].astype(np.int32))
+        assert d.max() == 1
+        moved[R] = (d > 0).mean()
+    assert moved[8] > 1e-3 > moved[4], moved
+
+
+def test_flush_r8_of_a_rank_deficient_state():
+    """R = 8 on the rank-2 state: CholeskyQR drops factors 3..8 (their pivots vanish), so those Q and U columns are
+    exactly zero, the first two span the state's columns, and the logical state survives within its bound."""
+    st, Q0, S = _rank2_state(R=8)
+    dbg = O.flush(st, Q0, np.array([1]), return_debug=True)
+    for key in ("Sq", "Sk", "Sv", "UQ"):
+        assert np.all(np.isfinite(st[key][1].astype(np.float64))), key
+    assert np.all(dbg["Q16"][0][:, 2:] == 0.0) and np.all(dbg["U16"][0][:, 2:] == 0.0)
+    X = S @ (S.T @ O.fp16(Q0).astype(np.float64))
+    assert np.abs(dbg["Q16"][0][:, :2] - _sign_fixed_qr(X)[:, :2]).max() < 2e-3
+    after = O.materialize(st)[1, 0]
+    sk, sv = st["Sk"][1, 0].astype(np.float64), st["Sv"][1, 0].astype(np.float64)
+    bound = 0.5 * sk[None, :] * sv[:, None] / 127.0 + 2 ** -9 * np.abs(S).max()
+    assert np.all(np.abs(after - S) <= bound)
+
+
+def _rank2_state(L=16, seed=71, R=4):
     """(state, Q0, S): slot 1, head 0 holds the rank-2 logical state S = sum_j w_j u_j k_j^T with k_j in {ka, kb}, an
     all-zero checkpoint and a full window (hcnt = L), so the next flush takes it."""
     rng = np.random.default_rng(seed)
-    st = O.new_state(2, 1, 1, L=L)
-    Q0 = O.make_q0(128, 4)
+    st = O.new_state(2, 1, 1, L=L, R=R)
+    Q0 = O.make_q0(128, R)
     st["Sk"][:] = 1.0
     st["Sv"][:] = 1.0
     kk = rng.standard_normal((2, 128))
@@ -252,13 +312,13 @@ def _rank2_state(L=16, seed=71):
 
 
 # ------------------------------------------------------------------------------------------------ flush
-@pytest.mark.parametrize("kda,dims", STEP_CASES)
+@pytest.mark.parametrize("kda,dims,R", FLUSH_CASES)
 @pytest.mark.parametrize("L", [16, 64])
-def test_flush_against_qr_and_bounds(kda, dims, L):
+def test_flush_against_qr_and_bounds(kda, dims, R, L):
     K, V = dims
-    rng = np.random.default_rng(5 + L + 7 * kda + K + V)
+    rng = np.random.default_rng(5 + L + 7 * kda + K + V + R)
     HV, H = 2, (2 if kda else 1)
-    st, _, Q0 = make_state(rng, 3, HV, H, K=K, V=V, L=L, kda=kda)
+    st, _, Q0 = make_state(rng, 3, HV, H, K=K, V=V, L=L, R=R, kda=kda)
     A_log, dt_bias = gate_params(HV, K, kda)
     idx = np.array([1, 2])
     for t in range(L):
@@ -280,7 +340,7 @@ def test_flush_against_qr_and_bounds(kda, dims, L):
         Qref = _sign_fixed_qr(S @ (S.T @ Q16q0))
         Q16 = dbg["Q16"][i]
         assert np.abs(Q16 - Qref).max() < 2e-2, np.abs(Q16 - Qref).max()
-        assert np.abs(Q16.T @ Q16 - np.eye(4)).max() < 4e-3
+        assert np.abs(Q16.T @ Q16 - np.eye(R)).max() < 4e-3
         # U = S^T Q (fp16)
         Uref = S.T @ Q16
         assert np.abs(dbg["U16"][i] - Uref).max() < 2e-3 * np.abs(Uref).max() + 1e-4
@@ -325,16 +385,18 @@ def test_flush_fully_decayed_and_idle_heads():
 
 
 # ------------------------------------------------------------------------------------------------ quantize / lowrank
-@pytest.mark.parametrize("qmax", [127.0, 31.0])
-@pytest.mark.parametrize("heavy", [False, True])
-@pytest.mark.parametrize("dims", GDN_DIMS)
-def test_quantize_against_qr_and_bounds(qmax, heavy, dims):
+QUANT_CASES = [(q, h, d, 4) for q in (127.0, 31.0) for h in (False, True) for d in GDN_DIMS] + \
+    [(127.0, False, (128, 128), 8), (127.0, True, (128, 128), 16)]          # ranks a step can read (kernels.py:63)
+
+
+@pytest.mark.parametrize("qmax,heavy,dims,R", QUANT_CASES)
+def test_quantize_against_qr_and_bounds(qmax, heavy, dims, R):
     K, V = dims
-    rng = np.random.default_rng(21 + int(qmax) + heavy + K + V)
+    rng = np.random.default_rng(21 + int(qmax) + heavy + K + V + R)
     D = 3
     S = (0.02 * (rng.standard_t(3, (D, V, K)) if heavy else rng.standard_normal((D, V, K)))).astype(np.float32)
     S[1] += np.outer(rng.standard_normal(V), rng.standard_normal(K)).astype(np.float32) * 0.05   # a dominant direction
-    Q0 = O.make_q0(V, 4)
+    Q0 = O.make_q0(V, R)
     codes, sk, sv, UQ = O.quantize_dense(S, Q0, qmax=qmax)
     for d in range(D):
         S64 = S[d].astype(np.float64)
