@@ -34,8 +34,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "int8 GDN/KDA decode-step µs + achieved HBM GB/s at B=64,H=32,d=128"
-DECODE_KERNEL = "gdn_step_kernel<128, 128, 2, false, true>"     # lq_gdn_decode at GQA 2: step + flush of its due heads
-STEP_KERNEL = "gdn_step_kernel<128, 128, 2, false, false>"      # the step alone (lq_gdn_step)
+DECODE_KERNEL = "gdn_step_kernel<128, 128, 2, false, true, 4>"  # lq_gdn_decode at GQA 2: step + flush of its due heads
+STEP_KERNEL = "gdn_step_kernel<128, 128, 2, false, false, 4>"   # the step alone (lq_gdn_step)
 HBM_PEAK_GBPS = 8000.0
 
 
@@ -370,6 +370,59 @@ def config4_bench(torch, dev, stream, layers=24, B=64, reps=32):
             "tokens_per_s": round(B / (times["int8"] * 1e-6), 0)}
 
 
+def loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture):
+    """What the memory system delivers to a pure streaming read of the step's own byte pattern, over the same rotated
+    slot sets: leapquant_amd/_build/liblq_probe.so reads, per (row, value head) block of 64 KiB, the checkpoint bytes
+    the step reads (codes, scales, factors: the first 17408 + 4 (K + V) R bytes), two blocks per 256-thread workgroup
+    as the step's workgroups take them; the same bytes contiguous; and whole 64 KiB blocks -- each with plain and with
+    non-temporal 16-byte loads, in graphs of 64 launches (set i % NSET).  Also the fixed cost of a launch in a graph (one
+    empty workgroup)."""
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(ROOT, "leapquant_amd", "_build", "liblq_probe.so"))
+    probe.lq_probe_read.restype = ctypes.c_int
+    probe.lq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    blk = ssm.stride(1) * 4                                       # bytes per (slot, head) block
+    nblk = B * HV
+    ck = 128 * 128 + 4 * (128 + 128) + 2 * R * (128 + 128)       # codes, Sk | Sv, UQ: 19456 bytes at R = 4
+    sink = torch.empty(nblk * 256, dtype=torch.int32, device=dev)
+    base = [ssm.data_ptr() + (1 + B * k) * HV * blk for k in range(NSET)]
+
+    def run(stride, nbytes, nb, nt):
+        def launch(i):
+            rc = probe.lq_probe_read(ctypes.c_void_p(base[i % NSET]), stride, nbytes, nb, 2, nt,
+                                     ctypes.c_void_p(sink.data_ptr()),
+                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                raise RuntimeError("lq_probe_read failed (%d)" % rc)
+        gr = capture(launch, 64)
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = NSET // 2 if NSET >= 2 else 1
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(reps):
+                gr.replay()
+            e1.record(stream)
+        e1.synchronize()
+        return e0.elapsed_time(e1) * 1e3 / (64 * reps)
+
+    out = {"workload": "pure streaming reads over config 1's rotated slot sets (%d sets): per (row, value head) "
+                       "block of %d bytes, two blocks per 256-thread workgroup" % (NSET, blk)}
+    for name, stride, nbytes in (("checkpoint", blk, ck), ("contiguous", ck, ck), ("full_block", blk, blk)):
+        nbytes_launch = nblk * nbytes
+        for nt, tag in ((1, "nt"), (0, "plain")):
+            us = run(stride, nbytes, nblk, nt)
+            out["%s_%s_us" % (name, tag)] = round(us, 3)
+            out["%s_%s_gbps" % (name, tag)] = round(nbytes_launch / (us * 1e-6) / 1e9, 1)
+        out["%s_bytes_per_launch" % name] = nbytes_launch
+    out["empty_launch_us"] = round(run(blk, 16, 0, 0), 3)
+    out["note"] = ("checkpoint = the step's read of the cache (%d of every %d bytes); contiguous = the same bytes "
+                   "without gaps; full_block = every byte of the fp32 cache" % (ck, blk))
+    return out
+
+
 def traffic_bytes(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each
     scaled by what the counter reads for the 64 MiB copies the bench ends with (None when the summary is absent)."""
@@ -685,6 +738,8 @@ def main():
     del src, dst
 
     progress("bf16 baseline, fused conv, calibration copies")
+    ceiling = loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture)
+    progress("loader ceiling")
     kda = kda_bench(torch, dev, stream, capture)
     progress("KDA config 2")
     fq = flush_quantize_bench(torch, dev, stream)
@@ -727,6 +782,7 @@ def main():
         "decode_conv_us": round(conv_us["decode"], 3),
         "decode_conv_note": "LeapQuantState.decode_conv (lq_gdn_decode with the conv): conv + step + the flushes of "
                             "the heads it fills, one launch per call, one whole window of every set"}
+    res["loader_ceiling"] = ceiling
     res["kda_config2"] = kda
     res["flush_quantize_config3"] = fq
     res["head_dims_W16"] = hd

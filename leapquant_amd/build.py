@@ -1,6 +1,7 @@
-"""Builds liblq.so (the HIP kernels + C ABI of include/lq.h) in-tree for gfx950.
+"""Builds liblq.so (the HIP kernels + C ABI of include/lq.h) in-tree for gfx950, and liblq_probe.so (a streaming-read
+probe that bench.py times as the memory system's ceiling; not part of the API).
 
-    python -m leapquant_amd.build          # -> leapquant_amd/_build/liblq.so
+    python -m leapquant_amd.build          # -> leapquant_amd/_build/liblq.so, liblq_probe.so
 
 hipcc cross-compiles without a GPU.  Every HIP file gets `-Xclang -target-feature -Xclang -packed-fp32-ops` (no
 packed FP32 instructions in the device code).
@@ -14,6 +15,8 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "liblq.so")
 SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dense.hip", "lq_noalloc.hip")
+PROBE_LIB = os.path.join(OUT, "liblq_probe.so")
+PROBE_SOURCES = ("lq_probe.hip",)
 ARCH = os.environ.get("LQ_OFFLOAD_ARCH", "gfx950")
 
 
@@ -24,13 +27,9 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
-def build(verbose=False):
-    os.makedirs(OUT, exist_ok=True)
-    cc = hipcc()
-    flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-inline-asm",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+def _compile_link(cc, flags, sources, lib, verbose):
     objs = []
-    for s in SOURCES:
+    for s in sources:
         src = os.path.join(CSRC, s)
         obj = os.path.join(OUT, s.replace(".hip", ".o"))
         cmd = [cc] + flags + ["-c", src, "-o", obj]
@@ -42,12 +41,21 @@ def build(verbose=False):
             if err.strip():
                 print(err)
         objs.append(obj)
-    tmp = LIB + ".tmp"
+    tmp = lib + ".tmp"
     cmd = [cc, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError("link failed:\n%s" % r.stderr)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib)
+
+
+def build(verbose=False):
+    os.makedirs(OUT, exist_ok=True)
+    cc = hipcc()
+    flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-inline-asm",
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    _compile_link(cc, flags, SOURCES, LIB, verbose)
+    _compile_link(cc, flags, PROBE_SOURCES, PROBE_LIB, verbose)
     return LIB
 
 
