@@ -14,19 +14,29 @@ namespace {
 
 using namespace lqf;
 
-// Persistent flush: workgroup b checks the candidates p = b + gridDim.x k (row n = p / HV, head p % HV) 64 at a time
-// (wave 0, one per lane), and processes the due ones (slot > 0, hcnt == L; kernels.py:1200) one after another.
+// Persistent flush: workgroup b checks the candidate units p = b + gridDim.x k (row n = p / (HV / U), heads
+// U (p % (HV / U)) .. + U - 1; U = 1 but for the paired 64-dim heads) 64 at a time (wave 0, one per lane), and
+// processes the due ones (slot > 0, hcnt == L for some head of the unit; kernels.py:1200) one after another.
 // With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
 // otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
 // With a due list (dlist, lq_decode_noalloc) the flush takes exactly the listed heads instead: workgroup b the entries
 // b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, so
 // an entry left by an interrupted call is skipped; the last workgroup to finish empties the list.
-// `head(slot, hv)` flushes one head with the whole workgroup; `due` is a word of the workgroup's shared memory.
-template <class Head>
+// `head(slot, hv0, mask)` flushes the due heads hv0 + h (bit h of mask) of one unit with the whole workgroup; `due` is
+// a word of the workgroup's shared memory.
+template <int U>
+__device__ __forceinline__ unsigned unit_mask(const lq_state& st, int slot, int hv0) {
+  unsigned m = 0;
+#pragma unroll
+  for (int h = 0; h < U; ++h) m |= (st.hcnt[(long long)slot * st.HV + hv0 + h] == st.L ? 1u : 0u) << h;
+  return m;
+}
+
+template <int U = 1, class Head>
 __device__ void flush_scan(unsigned long long& due, const lq_state& st, const int* __restrict__ idx, int N,
                            Head head) {
-  const int HV = st.HV, L = st.L;
-  const int total = N * HV;
+  const int NU = st.HV / U;                           // units per row
+  const int total = N * NU;
   const int stride = gridDim.x;
   if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
   for (int base = blockIdx.x; base < total; base += 64 * stride) {
@@ -34,9 +44,9 @@ __device__ void flush_scan(unsigned long long& due, const lq_state& st, const in
       const int p = base + stride * (int)threadIdx.x;
       bool d = false;
       if (p < total) {
-        const int n = p / HV, hv = p - n * HV;
+        const int n = p / NU, u = p - n * NU;
         const int slot = idx[n];
-        d = slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L;
+        d = slot > 0 && slot < st.NS && unit_mask<U>(st, slot, u * U) != 0;
       }
       const unsigned long long m = __ballot(d);
       if (threadIdx.x == 0) due = m;
@@ -48,8 +58,9 @@ __device__ void flush_scan(unsigned long long& due, const lq_state& st, const in
       const int b = __ffsll((long long)m) - 1;
       m &= m - 1;
       const int p = base + stride * b;
-      const int n = p / HV, hv = p - n * HV;
-      head(idx[n], hv);
+      const int n = p / NU, u = p - n * NU;
+      const int slot = idx[n];
+      head(slot, u * U, unit_mask<U>(st, slot, u * U));
     }
   }
   if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
@@ -61,7 +72,9 @@ __device__ void flush_scan(unsigned long long& due, const lq_state& st, const in
   }
 }
 
-template <class Head>
+// listed heads: a unit of U heads is flushed with the listed head alone in its mask (the unit's other head, when
+// listed too, is another entry, flushed by its own workgroup: the flush of a unit never reads a head outside its mask)
+template <int U = 1, class Head>
 __device__ void flush_listed(unsigned long long& due, const lq_state& st, const int* __restrict__ idx, int N,
                              int* dlist, Head head) {
   const int HV = st.HV, L = st.L;
@@ -80,7 +93,10 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
     __syncthreads();
     const long long take = (long long)due;
     __syncthreads();
-    if (take >= 0) head((int)(take / HV), (int)(take % HV));
+    if (take >= 0) {
+      const int slot = (int)(take / HV), hv = (int)(take % HV);
+      head(slot, hv - hv % U, 1u << (hv % U));
+    }
   }
   __syncthreads();
   if (threadIdx.x == 0 && __hip_atomic_fetch_add(dlist + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
@@ -95,7 +111,7 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
   __shared__ FlushShared<RA> sh;
-  auto head = [&](int slot, int hv) { flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax); };
+  auto head = [&](int slot, int hv, unsigned) { flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax); };
   if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan(sh.due, st, idx, N, head);
 }
@@ -105,9 +121,504 @@ __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush4_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                    int* dlist) {
   __shared__ FlushShared4 sh;
-  auto head = [&](int slot, int hv) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax); };
+  auto head = [&](int slot, int hv, unsigned) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax); };
   if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan(sh.due, st, idx, N, head);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// Flush of the 64-dim GDN heads (K = 64; kernels.py:1089-1097): four waves, the tile 64 key channels x 128 rows.
+// (64, 128): one head per tile.  (64, 64) at even GQA: two heads hv0, hv0 + 1 of one key head stacked in the rows
+// (HP = 2, the reference's packing), so that the tile is full and the pair's shared window keys enter one rank-L
+// product.  Each head keeps its own arithmetic: the factor columns are block-diagonal (head h owns columns 4 h ..
+// 4 h + 3 of every rank-R product, so the P, Q and Gram MFMAs separate by head by themselves), and the CholeskyQR, pn,
+// the column scales Sk and the stores are per head.  (64, 64) at odd GQA: one head, rows 64.. zero (HP = 1).
+// Wave w owns key channels 16 w .. 16 w + 15 and lane l holds
+//     a[nt][i] = M[16 w + 4 (l >> 4) + i][v' = 16 nt + (l & 15)],   v' = 64 h + v for head h (HP = 2).
+// A head outside the unit's due mask (one head of a pair due; a listed head whose partner is its own entry) loads as
+// zeros and stores nothing.
+// ------------------------------------------------------------------------------------------------------------------
+constexpr int K64 = 64, ROWS = 128;
+
+struct FlushShared64 {
+  union {
+    struct {
+      bf16_t k[K64][OPS4];     // window keys K_j[c] of one half
+      bf16_t u[2][ROWS][OPS4]; // hi / lo of w_j u_j[v'] of one half
+    } op;
+    struct {                   // after the rebuild
+      f32x4 qpart[NW4][ROWS];  // per-wave partial Q rows (the row's head's four columns)
+      float rmx[4 * NW4][ROWS];
+      float rq[ROWS];
+      f16_t ppT[8][K64];       // P16^T, column 4 h + r = factor r of head h
+    } r;
+  };
+  float skl[2][K64];           // Sk per head
+  float svr[ROWS];             // Sv pn / qmax per row
+  float w[2][LPMAX];           // entry weights per head
+  f32x4 uoc[2][K64];           // old U rows per head [c][a], a >= R zero
+  f32x4 qov[ROWS];             // old Q rows [v'][a] of the row's head
+  f16_t uoT[8][K64];           // old U^T, row 4 h + a
+  f16_t qoT[4][ROWS];          // old Q^T of the row's head
+  f16_t qT[4][ROWS];           // Q^T operand of the P steps (row's head): fp16 Q0, then Q16
+  f32x4 qv[ROWS];              // Q rows of the row's head: fp32, then Q16
+  unsigned long long due;
+};
+static_assert(sizeof(FlushShared64) <= 40960, "four workgroups per CU");
+
+// window rows of one half: thread t takes entries 2 (t % 16), + 1 and columns 8 (t / 16) .. + 7 -- keys for the
+// first 64 columns, the rows v' of the pair's values for all 128 (rows past the heads, or of a head outside the mask,
+// zero)
+template <int V_, int HP>
+__device__ __forceinline__ void load_half64(WinHalf& r, const lq_state& st, int slot, int hv0, unsigned mask, int hf) {
+  const int G = st.HV / st.H, hk = hv0 / G, L = st.L;
+  const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K64;
+  const int t = opaque_tid(), jp = t % 16, c8 = (t / 16) * 8;
+  const int hh = min(c8 / V_, HP - 1), v = c8 - hh * V_;
+  const bool uok = c8 < HP * V_ && ((mask >> hh) & 1);
+  const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv0 + hh) * L * V_ + (c8 < HP * V_ ? v : 0);
+  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const int j = HALF * hf + 2 * jp + k, jr = j < L ? j : 0;
+    const uint4 kx = *(const uint4*)(Kb + (long long)jr * K64 + min(c8, K64 - 8));
+    const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_);
+    r.k[k] = c8 < K64 ? kx : z;
+    r.u[k] = uok ? ux : z;
+  }
+}
+template <int V_, int HP>
+__device__ __forceinline__ void store_half64(FlushShared64& sh, const WinHalf& r, int L, int hf) {
+#pragma clang fp contract(off)    // the split is of the fp32-rounded product (kernels.py:1509-1511)
+  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8;
+  const int hh = min(c8 / V_, HP - 1);
+  const int j0 = HALF * hf + jl;
+  const float w0 = j0 < L ? sh.w[hh][j0] : 0.f, w1 = j0 + 1 < L ? sh.w[hh][j0 + 1] : 0.f;
+  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
+  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int x = e >> 1;
+    const bool odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;
+    if (c8 < K64) *(uint32_t*)&sh.op.k[c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
+    const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+    const uint32_t hi = pk_bf16(wu0, wu1);
+    *(uint32_t*)&sh.op.u[0][c8 + e][jl] = hi;
+    *(uint32_t*)&sh.op.u[1][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+  }
+}
+// acc[c][v'] += sum_j K_j[c] B[v'][j] over one staged half
+template <int NTV>
+__device__ __forceinline__ void rebuild_half64(Tile& t, const bf16_t (*A)[OPS4], const bf16_t (*B)[OPS4]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  const bf16x8 af = *(const bf16x8*)&A[16 * w + (l & 15)][8 * q];
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {
+    const bf16x8 bfr = *(const bf16x8*)&B[16 * nt + (l & 15)][8 * q];
+    t.a[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bfr, t.a[nt], 0, 0, 0);
+  }
+}
+// M[a][r] = sum over the rows v' of head h of X[v'][a] Y[v'][r] (4 x 4; X^T, Y^T fp16 [4][128]); every lane gets all
+template <int V_>
+__device__ __forceinline__ void gram_head(const f16_t (*XT)[ROWS], const f16_t (*YT)[ROWS], int h, float M[4][4]) {
+  const int l = lane_id(), q = l >> 4, l16 = l & 15;
+  const f16x8 z8 = {};
+  f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int ks = 0; ks < V_ / 32; ++ks) {
+    const int v0 = h * V_ + 32 * ks + 8 * q;
+    const f16x8 ao = l16 < 4 ? *(const f16x8*)&XT[l16][v0] : z8;
+    const f16x8 by = l16 < 4 ? *(const f16x8*)&YT[l16][v0] : z8;
+    macc = mma32(ao, by, macc);
+  }
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+}
+// P = B^T Q + pn_h U_old (Q_old^T Q) per head, fp16-rounded (kernels.py:1580-1700): lanes l < 16 HP return
+// P_h[16 w + (l & 15)][i] of head h = l >> 4 (zero for i >= R); the other lanes zeros.  bt: the transposed packing.
+template <int V_, int HP>
+__device__ __forceinline__ f32x4 p_step64(const FlushShared64& sh, const f16x4 bt[8], const float pn[2], int R) {
+  constexpr int NTV = HP * V_ / 16;                   // row tiles holding data
+  const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  float M[2][4][4];
+#pragma unroll
+  for (int h = 0; h < HP; ++h) gram_head<V_>(sh.qoT, sh.qT, h, M[h]);
+  const f16x4 z4 = {};
+  f32x4 pacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {                  // P^T[4 h + r][c] = sum over head h's rows of Q^T[r][v'] B[c][v']
+    const int hh = (16 * nt) / V_;
+    const f16x4 aq = (l16 < 4 * HP && (l16 >> 2) == hh) ? *(const f16x4*)&sh.qT[l16 & 3][16 * nt + 4 * q] : z4;
+    pacc = mma16(aq, bt[nt], pacc);
+  }
+  const int qh = q < HP ? q : HP - 1;
+  const f32x4 uo = sh.uoc[qh][16 * w + l16];
+  f32x4 p;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float corr = 0.f;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      float m = M[0][a][i];
+      if (HP == 2) m = qh == 1 ? M[1][a][i] : m;
+      corr = a == 0 ? uo[0] * m : corr + uo[a] * m;
+    }
+    const float pnh = qh == 1 ? pn[1] : pn[0];
+    p[i] = (q < HP && i < R) ? hround(pacc[i] + pnh * corr) : 0.f;
+  }
+  return p;
+}
+
+template <int V_, int HP>
+__device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv0,
+                             unsigned mask, float qmax) {
+  static_assert(HP * V_ <= ROWS && V_ % 32 == 0, "rows of the tile");
+  constexpr int NTV = HP * V_ / 16;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
+  const long long s0 = (long long)slot * HV + hv0;
+  char* base[2];
+  float pn[2], rpn[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int hs = h < HP ? h : 0;
+    base[h] = block_base(st, slot, hv0 + hs);
+    const float pb = st.Pbuf[s0 + hs];
+    pn[h] = ((mask >> h) & 1) ? fmaxf(pb, LQ_PNMIN) : 1.f;                        // kernels.py:1471
+    rpn[h] = 1.0f / pn[h];                                                         // kernels.py:1477
+  }
+  // ---- stage 1: every load up front.  Thread t < 64: column c = t of each head (Sk, U_old); 64 <= t < 192: row
+  //      v' = t - 64 (Sv, Q_old, Q0); 192 <= t: window weight j = t - 192 of each head ----
+  float uqv[4], q0v[4], scv;
+  const int vr = tid - K64;
+  const bool rowt = tid >= K64 && tid < K64 + ROWS;
+  const bool rin = rowt && vr < HP * V_;                                           // a row of the unit's heads
+  const int hr = rin ? vr / V_ : 0;
+  const bool rok = rin && ((mask >> hr) & 1);
+  const int vq = rin ? vr - hr * V_ : 0;                                           // the row within its head
+  const int vv = rok ? vq : 0;
+  float colsk[2], coluq[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const bool cok = tid < K64 && h < HP && ((mask >> h) & 1);
+    const float* Skh = (const float*)(base[h] + V_ * K64);
+    const f16_t* UQh = (const f16_t*)(base[h] + V_ * K64 + 4 * (K64 + V_));
+    const int c = tid < K64 ? tid : 0;
+    const float x = Skh[c];
+    colsk[h] = cok ? x : 0.f;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float y = h2f(UQh[min(a, R - 1) * (K64 + V_) + c]);
+      coluq[h][a] = (cok && a < R) ? y : 0.f;
+    }
+  }
+  {
+    char* bh_ = hr ? base[1] : base[0];              // (selects, not register-array indexing, for per-thread heads)
+    const float* Svh = (const float*)(bh_ + V_ * K64 + 4 * K64);
+    const f16_t* UQh = (const f16_t*)(bh_ + V_ * K64 + 4 * (K64 + V_));
+    const float x = Svh[vv];
+    scv = rok ? x : 0.f;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      const float y = h2f(UQh[min(a, R - 1) * (K64 + V_) + K64 + vv]);
+      uqv[a] = (rok && a < R) ? y : 0.f;
+      const float z = Q0[vq * R + min(a, R - 1)];
+      q0v[a] = (rin && a < R) ? z : 0.f;
+    }
+  }
+  const int jw = tid - (K64 + ROWS);                                               // window weight j for tid >= 192
+  float wj[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    const int hs = h < HP ? h : 0;
+    const float x = st.Wbuf[(s0 + hs) * L + min(max(jw, 0), L - 1)];
+    wj[h] = (jw >= 0 && jw < L && h < HP && ((mask >> h) & 1)) ? x : 0.f;
+  }
+  WinHalf win;
+  load_half64<V_, HP>(win, st, slot, hv0, mask, 0);
+  uint32_t wds[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {                    // code words of the lane's tile entries
+    const int v2 = 16 * nt + l16;
+    const int h = min((16 * nt) / V_, HP - 1);
+    const bool ok = nt < NTV && ((mask >> h) & 1);
+    const int8_t* Sq = (const int8_t*)base[h];
+    const uint32_t x = *(const uint32_t*)(Sq + (ok ? v2 - h * V_ : 0) * K64 + 16 * w + 4 * q);
+    wds[nt] = ok ? x : 0u;
+  }
+  if (tid < K64) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sh.skl[h][tid] = colsk[h];
+      f32x4 u;
+#pragma unroll
+      for (int a = 0; a < 4; ++a) {
+        u[a] = coluq[h][a];
+        sh.uoT[4 * h + a][tid] = f2h(u[a]);
+      }
+      sh.uoc[h][tid] = u;
+    }
+  } else if (rowt) {
+    sh.svr[vr] = scv * ((hr ? pn[1] : pn[0]) / qmax);                              // kernels.py:1483
+    f32x4 o;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) {
+      o[a] = uqv[a];
+      sh.qoT[a][vr] = f2h(o[a]);
+      sh.qT[a][vr] = f2h(hround(q0v[a]));                                          // kernels.py:1573-1577
+    }
+    sh.qov[vr] = o;
+  } else {
+    sh.w[0][jw] = wj[0];
+    sh.w[1][jw] = wj[1];
+  }
+  __syncthreads();
+
+  // ---- stage 2: B = deq(S0) pn + window, fp16, the window half by half (kernels.py:1483-1571) ----
+  f16x4 bh[8], bt[8];
+  {
+    Tile t;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    store_half64<V_, HP>(sh, win, L, 0);
+    __syncthreads();
+    rebuild_half64<NTV>(t, sh.op.k, sh.op.u[0]);
+    rebuild_half64<NTV>(t, sh.op.k, sh.op.u[1]);
+    if (L > HALF) {
+      load_half64<V_, HP>(win, st, slot, hv0, mask, 1);
+      __syncthreads();
+      store_half64<V_, HP>(sh, win, L, 1);
+      __syncthreads();
+      rebuild_half64<NTV>(t, sh.op.k, sh.op.u[0]);
+      rebuild_half64<NTV>(t, sh.op.k, sh.op.u[1]);
+    }
+    {                                                 // + codes x svr[v'] x skl[h][c], after the window products
+#pragma clang fp contract(off)
+      const int c0 = 16 * w + 4 * q;
+#pragma unroll
+      for (int nt = 0; nt < NTV; ++nt) {
+        const int hh = (16 * nt) / V_;
+        const float rv = sh.svr[16 * nt + l16];
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          t.a[nt][i] = t.a[nt][i] + ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * rv) * sh.skl[hh][c0 + i];
+      }
+    }
+    f16x4 ident;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ident[i] = (4 * q + i == l16) ? (_Float16)1.0f : (_Float16)0.0f;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      bh[nt] = to_h4(t.a[nt]);
+      bt[nt] = to_h4(mma16(bh[nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));
+    }
+  }
+
+  // ---- stage 3: subspace iteration with the per-head corrections (kernels.py:1580-1842) ----
+  const f32x4 p16 = p_step64<V_, HP>(sh, bt, pn, R);
+  __syncthreads();                                    // every wave is past the rebuild: the operand region is free
+  if (q < HP) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sh.r.ppT[4 * q + i][16 * w + l16] = f2h(p16[i]);
+  }
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+  {
+    const f16x4 z4 = {};
+    const f16x4 ap = l16 < 4 * HP ? *(const f16x4*)&sh.r.ppT[l16][16 * w + 4 * q] : z4;   // A[4 h + r][c]
+#pragma unroll
+    for (int nt = 0; nt < NTV; ++nt) {
+      const f32x4 d = mma16(ap, bh[nt], f32x4{0.f, 0.f, 0.f, 0.f});              // Q^T[4 q + i][16 nt + l]
+      if (q == (16 * nt) / V_) sh.r.qpart[w][16 * nt + l16] = d;                  // the row's head's columns
+    }
+  }
+  __syncthreads();
+  if (tid < HP * V_) {                                // one row v' per thread; the head is wave-uniform
+    const int v2 = tid, hh = v2 / V_;
+    float M2[4][4];                                   // U_old_h^T P16_h over the 64 channels
+    {
+      const f16x8 z8 = {};
+      f32x4 macc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < K64 / 32; ++ks) {
+        const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.uoT[4 * hh + l16][32 * ks + 8 * q] : z8;
+        const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[4 * hh + l16][32 * ks + 8 * q] : z8;
+        macc = mma32(ao, bp, macc);
+      }
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    }
+    f32x4 s = sh.r.qpart[0][v2];
+#pragma unroll
+    for (int w2 = 1; w2 < NW4; ++w2) s += sh.r.qpart[w2][v2];
+    const f32x4 qo = sh.qov[v2];
+    const float pnh = hh ? pn[1] : pn[0];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] += pnh * (qo[0] * M2[0][r] + qo[1] * M2[1][r] + qo[2] * M2[2][r] + qo[3] * M2[3][r]);
+    sh.qv[v2] = s;
+  } else if (tid < ROWS) {
+    sh.qv[tid] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+  __syncthreads();
+  if (w == 0) {                                       // CholeskyQR2 per head, fp16 Q (kernels.py:1778-1835)
+    __builtin_amdgcn_s_setprio(3);
+    f32x4 p0 = sh.qv[l], p1 = sh.qv[l + 64];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) { if (r >= R) { p0[r] = 0.f; p1[r] = 0.f; } }
+    if (HP == 2) {                                    // rows l: head 0, rows l + 64: head 1
+      cholqr_pass1(p0);
+      cholqr_pass1(p0);
+      cholqr_pass1(p1);
+      cholqr_pass1(p1);
+    } else {
+      cholqr_pass(p0, p1);
+      cholqr_pass(p0, p1);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      p0[r] = r < R ? hround(p0[r]) : 0.f;
+      p1[r] = (r < R && l + 64 < HP * V_) ? hround(p1[r]) : 0.f;
+      sh.qT[r][l] = f2h(p0[r]);
+      sh.qT[r][l + 64] = f2h(p1[r]);
+    }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+  const f32x4 u16 = p_step64<V_, HP>(sh, bt, pn, R);  // U16 (lanes < 16 HP: head l >> 4)
+
+  // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) per head (kernels.py:1888-1928) ----
+  Tile t;
+  {
+    const f16x4 z4 = {};
+    f32x4 uh[2];                                      // head h's U16 rows in lanes l < 16 (k = a of the MFMA)
+    uh[0] = u16;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) uh[1][i] = __shfl_xor(u16[i], 16);
+    f16x4 auo[2], aun[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      auo[h] = q == 0 ? to_h4(sh.uoc[h][16 * w + l16]) : z4;                     // A[c][a] = U_old
+      aun[h] = q == 0 ? to_h4(-uh[h]) : z4;                                      // A[c][r] = -U16
+    }
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      if (nt < NTV) {
+        const int hh = (16 * nt) / V_, v2 = 16 * nt + l16;
+        const f16x4 bqo = q == 0 ? to_h4(sh.qov[v2]) : z4;                       // B[a][v'] = Q_old^T
+        const f16x4 bqn = q == 0 ? to_h4(sh.qv[v2]) : z4;                        // B[r][v'] = Q16^T
+        f32x4 e = from_h4(bh[nt]) * rpn[hh];
+        e = mma16(auo[hh], bqo, e);
+        e *= pn[hh];
+        e = mma16(aun[hh], bqn, e);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(e[i]);
+      } else {
+        t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  }
+
+  // ---- stage 5: column smoothing scales per head (kernels.py:1929-1958) ----
+  float rsk[2][4];
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    float cs[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.f;
+#pragma unroll
+      for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) x += fabsf(t.a[nt][i]);
+      cs[i] = sum16(x);
+    }
+    const int ic = l & 3;
+    const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
+    const float sq = sqrtf(msum);
+    const float rs = fminf(1.0f / sq, 1.0f / LQ_EPS);
+    if (l16 < 4 && ((mask >> h) & 1)) ((float*)(base[h] + V_ * K64))[16 * w + 4 * q + l16] = fmaxf(sq, LQ_EPS);
+    rsk[h][0] = dpp<0x00>(rs);
+    rsk[h][1] = dpp<0x55>(rs);
+    rsk[h][2] = dpp<0xaa>(rs);
+    rsk[h][3] = dpp<0xff>(rs);
+  }
+  if (HP == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rsk[1][i] = rsk[0][i];
+  }
+  // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const int hh = min((16 * nt) / V_, 1);
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      t.a[nt][i] *= rsk[hh][i];
+      m = fmaxf(m, fabsf(t.a[nt][i]));
+    }
+    sh.r.rmx[4 * w + q][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  if (tid < ROWS) {
+    float m = sh.r.rmx[0][tid];
+#pragma unroll
+    for (int k = 1; k < 4 * NW4; ++k) m = fmaxf(m, sh.r.rmx[k][tid]);
+    const float rmax = fmaxf(m, LQ_EPS);
+    const int hh = min(tid / V_, HP - 1);
+    char* bhh = hh ? base[1] : base[0];
+    if (tid < HP * V_ && ((mask >> hh) & 1)) ((float*)(bhh + V_ * K64 + 4 * K64))[tid - hh * V_] = rmax;
+    sh.r.rq[tid] = qmax * (1.0f / rmax);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {
+    const int hh = (16 * nt) / V_, v2 = 16 * nt + l16;
+    const float rq = sh.r.rq[v2];
+    uint32_t b[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
+    const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+    if ((mask >> hh) & 1) *(uint32_t*)(base[hh] + (v2 - hh * V_) * K64 + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
+  if (q < HP && ((mask >> q) & 1)) {
+    f16_t* UQ = (f16_t*)((q ? base[1] : base[0]) + V_ * K64 + 4 * (K64 + V_));
+    for (int r = 0; r < R; ++r) UQ[r * (K64 + V_) + 16 * w + l16] = f2h(u16[r]);
+  }
+  if (tid < HP * V_) {
+    const int hh = tid / V_;
+    if ((mask >> hh) & 1) {
+      f16_t* UQ = (f16_t*)((hh ? base[1] : base[0]) + V_ * K64 + 4 * (K64 + V_));
+      for (int r = 0; r < R; ++r) UQ[r * (K64 + V_) + K64 + tid - hh * V_] = f2h(sh.qv[tid][r]);
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    if ((mask >> h) & 1) {
+      if (tid < L) st.Wbuf[(s0 + h) * L + tid] = 0.f;
+      if (tid == 0) {
+        st.Pbuf[s0 + h] = 1.f;
+        st.hcnt[s0 + h] = 0;
+      }
+    }
+  }
+  __syncthreads();                                    // LDS reuse by the next unit of this workgroup
+}
+
+template <int V_, int HP>
+__global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
+void flush64_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
+                    int* dlist) {
+  __shared__ FlushShared64 sh;
+  auto head = [&](int slot, int hv0, unsigned mask) { flush_head64<V_, HP>(sh, st, Q0, slot, hv0, mask, qmax); };
+  if (dlist) flush_listed<HP>(sh.due, st, idx, N, dlist, head);
+  else flush_scan<HP>(sh.due, st, idx, N, head);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -729,8 +1240,11 @@ int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, 
   if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else if (st->K == KD && st->R > 4) flush_kernel<false, KD, VD, 8><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   else if (st->K == KD) flush4_kernel<><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if (st->V == VD) flush_kernel<false, 64, 128><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else flush_kernel<false, 64, 64><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if (st->V == VD) flush64_kernel<128, 1><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  else if ((st->HV / st->H) % 2 == 0) {               // two heads of one key head per workgroup (kernels.py:1095-1097)
+    const dim3 gp((unsigned)(total / 2 < 4 * num_cus() ? total / 2 : 4 * num_cus()));
+    flush64_kernel<64, 2><<<gp, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+  } else flush64_kernel<64, 1><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

@@ -143,15 +143,9 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
   }
 }
 
-// CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835) on the 2 rows a lane of wave 0 holds
-__device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
-  float gg[10];
-  int k = 0;
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
-  float ll[10];
+// CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835): 1 / L factors of the 4 x 4 Gram (packed
+// lower triangle), then the rows times L^-T
+__device__ __forceinline__ void chol4(const float gg[10], float ll[10]) {
   ll[0] = rsqrtf_rn(fmaxf(gg[0], 1e-30f));
   ll[1] = gg[1] * ll[0];
   ll[2] = rsqrtf_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
@@ -162,14 +156,35 @@ __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
   ll[7] = (gg[7] - ll[6] * ll[1]) * ll[2];
   ll[8] = (gg[8] - ll[6] * ll[3] - ll[7] * ll[4]) * ll[5];
   ll[9] = rsqrtf_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
+}
+__device__ __forceinline__ void chol4_solve(const float ll[10], f32x4& p) {
+  p[0] = p[0] * ll[0];
+  p[1] = (p[1] - p[0] * ll[1]) * ll[2];
+  p[2] = (p[2] - p[0] * ll[3] - p[1] * ll[4]) * ll[5];
+  p[3] = (p[3] - p[0] * ll[6] - p[1] * ll[7] - p[2] * ll[8]) * ll[9];
+}
+// on the 2 rows (l, l + 64) a lane of wave 0 holds: the Gram over all 128 rows
+__device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
+  float gg[10], ll[10];
+  int k = 0;
 #pragma unroll
-  for (int s = 0; s < 2; ++s) {
-    f32x4& p = s ? p1 : p0;
-    p[0] = p[0] * ll[0];
-    p[1] = (p[1] - p[0] * ll[1]) * ll[2];
-    p[2] = (p[2] - p[0] * ll[3] - p[1] * ll[4]) * ll[5];
-    p[3] = (p[3] - p[0] * ll[6] - p[1] * ll[7] - p[2] * ll[8]) * ll[9];
-  }
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
+  chol4(gg, ll);
+  chol4_solve(ll, p0);
+  chol4_solve(ll, p1);
+}
+// on the one row a lane holds: the Gram over the wave's 64 rows (one head of a pair, K = 64 flush)
+__device__ __forceinline__ void cholqr_pass1(f32x4& p) {
+  float gg[10], ll[10];
+  int k = 0;
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(p[r] * p[c]);
+  chol4(gg, ll);
+  chol4_solve(ll, p);
 }
 
 // modified Gram-Schmidt on the R columns of the 128 x 4 matrix whose rows l, l + 64 a lane of wave 0 holds

@@ -275,6 +275,39 @@ def test_flush_r8_code_sensitivity():
     assert moved[8] > 1e-3 > moved[4], moved
 
 
+def test_flush_head_dim_code_sensitivity():
+    """Sets the K = 64 flush's GPU code bar (0.25 %): at (64, 128), GQA 1, W = 16 one fp16 ulp in one entry of each
+    head's rebuilt B moves more than 0.1 % of the codes (by one LSB each) -- a head of 8192 codes, and each factor
+    rounding flip shifts a row or column of its residual -- while at 128 x 128 on the same window it moves 0.01 %."""
+    def bump(B):
+        B = B.copy()
+        for d in range(B.shape[0]):
+            B[d, 3, 5] = float(np.nextafter(np.float16(B[d, 3, 5]), np.float16(np.inf)))
+        return B
+    moved = {}
+    for K, V in ((64, 128), (128, 128)):
+        rng = np.random.default_rng(1300 + K + V + 16 + 7)
+        NS, HV, H, L = 6, 4, 4, 16
+        st, _, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=L)
+        A_log, dt_bias = gate_params(HV, K)
+        for _ in range(L + 5):
+            sl = rng.permutation(np.arange(1, NS))[: rng.integers(1, NS)]
+            mixed, a, b = make_inputs(rng, len(sl), HV, H, K, V)
+            O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
+            O.flush(st, Q0, sl)
+        for s in (1, 3):
+            while st["hcnt"][s, 0] < L:
+                mixed, a, b = make_inputs(rng, 1, HV, H, K, V)
+                O.gdn_step(st, mixed, a, b, A_log, dt_bias, np.array([s]))
+        x, y = O.copy_state(st), O.copy_state(st)
+        O.flush(x, Q0, np.array([1, 3]))
+        O.flush(y, Q0, np.array([1, 3]), b_hook=bump)
+        d = np.abs(x["Sq"][[1, 3]].astype(np.int32) - y["Sq"][[1, 3]].astype(np.int32))
+        assert d.max() <= 1
+        moved[(K, V)] = (d > 0).mean()
+    assert moved[(64, 128)] > 1e-3 > moved[(128, 128)], moved
+
+
 def test_flush_r8_of_a_rank_deficient_state():
     """R = 8 on the rank-2 state: CholeskyQR drops factors 3..8 (their pivots vanish), so those Q and U columns are
     exactly zero, the first two span the state's columns, and the logical state survives within its bound."""
