@@ -17,12 +17,21 @@ from tests.test_gpu_parity import _prestep
 pytestmark = pytest.mark.gpu
 
 
-def _to_full_minus_one(rng, st, slots, kda, L, HV, H):
-    A_log, dt_bias = gate_params(HV, 128, kda)
+def _to_full_minus_one(rng, st, slots, kda, L, HV, H, K=128, V=128):
+    A_log, dt_bias = gate_params(HV, K, kda)
     for s in slots:
         while st["hcnt"][s, 0] < L - 1:
-            mixed, a, b = make_inputs(rng, 1, HV, H, kda=kda)
+            mixed, a, b = make_inputs(rng, 1, HV, H, K, V, kda=kda)
             (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, np.array([s]))
+
+
+def _prestep_dims(rng, st, Q0, steps, NS, HV, H, K, V):
+    A_log, dt_bias = gate_params(HV, K)
+    for _ in range(steps):
+        sl = rng.permutation(np.arange(1, NS))[: rng.integers(1, NS)]
+        mixed, a, b = make_inputs(rng, len(sl), HV, H, K, V)
+        O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
+        O.flush(st, Q0, sl)
 
 
 def _noalloc(lq, ssm, mixed, a, b, A_log, dt_bias, idx, out):
@@ -35,25 +44,30 @@ def _noalloc(lq, ssm, mixed, a, b, A_log, dt_bias, idx, out):
                                         1 if lq.kda else 0, ctypes.c_float(lq.glb), stream)
 
 
-@pytest.mark.parametrize("kda", [False, True])
-def test_noalloc_decode_equals_step_then_flush(kda):
+@pytest.mark.parametrize("kda,K,V", [(False, 128, 128), (True, 128, 128), (False, 64, 64), (False, 64, 128)])
+def test_noalloc_decode_equals_step_then_flush(kda, K, V):
+    """(64, 64) at GQA 2: the flush takes the two heads of a key head together when it scans, and each listed head
+    alone (its partner's entry in another workgroup) from the due list -- the same bytes either way."""
     L, NS, HV = 16, 10, 4
     H = HV if kda else 2
-    rng = np.random.default_rng(1500 + kda)
-    st, S, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda)
-    _prestep(rng, st, Q0, kda, steps=L // 2, NS=NS, HV=HV, H=H)
-    _to_full_minus_one(rng, st, (1, 2, 3, 7, 8), kda, L, HV, H)      # the next step of these slots fills them
+    rng = np.random.default_rng(1500 + kda + K + V)
+    st, S, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=L, kda=kda)
+    if K == 128:
+        _prestep(rng, st, Q0, kda, steps=L // 2, NS=NS, HV=HV, H=H)
+    else:
+        _prestep_dims(rng, st, Q0, L // 2, NS, HV, H, K, V)
+    _to_full_minus_one(rng, st, (1, 2, 3, 7, 8), kda, L, HV, H, K, V)   # the next step of these slots fills them
     ssm_a, lq_a = G.to_gpu(st, H=H)                                   # existing entry points
     ssm_b, lq_b = G.to_gpu(st, H=H)                                   # lq_decode_noalloc
-    A_log, dt_bias = gate_params(HV, 128, kda)
+    A_log, dt_bias = gate_params(HV, K, kda)
     calls = [np.array([1, 2, 0, 4, 5, 3, 6], np.int64),             # fills slots 1, 2, 3; row 2 is padding
              np.array([7, 1, 8], np.int64)]                           # fewer rows; fills 7 and 8
     for k, idx in enumerate(calls):
-        mixed, a, b = make_inputs(rng, len(idx), HV, H, kda=kda)
+        mixed, a, b = make_inputs(rng, len(idx), HV, H, K, V, kda=kda)
         mg, ag, bg, Ag, dg, ig = G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx)
-        out_a = torch.empty(len(idx), HV, 128, dtype=torch.bfloat16, device=G.DEV)
-        out_b = torch.full((len(idx), HV, 128), 9.0, dtype=torch.bfloat16, device=G.DEV)
-        print("no-alloc decode, %s, call %d (%d rows)" % ("KDA" if kda else "GDN", k, len(idx)), flush=True)
+        out_a = torch.empty(len(idx), HV, V, dtype=torch.bfloat16, device=G.DEV)
+        out_b = torch.full((len(idx), HV, V), 9.0, dtype=torch.bfloat16, device=G.DEV)
+        print("no-alloc decode, %s %dx%d, call %d (%d rows)" % ("KDA" if kda else "GDN", K, V, k, len(idx)), flush=True)
         lq_a.decode(ssm_a, mg, ag, bg, Ag, dg, ig, out_a)
         assert _noalloc(lq_b, ssm_b, mg, ag, bg, Ag, dg, ig, out_b) == 0
         torch.cuda.synchronize()
