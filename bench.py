@@ -173,7 +173,7 @@ def head_dims_bench(torch, dev, stream, capture):
     """GDN head-dim variants (K, V) = (64, 128), (64, 64) (reference kernels.py:62-65) at config 1's batch and heads
     (B = 64, HV = 32, H = 16) and the reference's window for these shapes, W = 16 (R = 4), int8 state, 4 rotated slot
     sets.  Per shape: the amortised decode call (step + flush), the step alone (mean over h = 0..15) with its
-    algorithmic GB/s, and the flush with every head of a set due."""
+    algorithmic GB/s, the flush with every head of a set due, and the standalone quantize of a set's fp32 states."""
     from leapquant_amd.state import LeapQuantState
     B, HV, H, L, R, NSET = 64, 32, 16, 16, 4, 4
     NS = B * NSET + 1
@@ -235,9 +235,19 @@ def head_dims_bench(torch, dev, stream, capture):
         step_us = sum(st_ms[1:]) / len(st_ms[1:]) * 1e3 / CH
         flush_us = sum(fl_ms[NSET:]) / len(fl_ms[NSET:]) * 1e3
         bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L)) / L
+        # the standalone quantize of one set's fp32 states (B x HV heads), sets rotated
+        q_ms = []
+        for r in range(2 * NSET):
+            ssm[1 + B * (r % NSET): 1 + B * (r % NSET + 1)].normal_(0.0, 0.02, generator=g)
+            torch.cuda.synchronize()                    # the refill (default stream) before the timed quantize
+            q_ms.append(event_ms(torch, stream, lambda kk=r % NSET: lq.quantize(ssm, sets[kk]), 1))
+        quant_us = sum(q_ms[NSET:]) / NSET * 1e3
+        qbytes = B * HV * (V * K * 4 + V * K + 4 * (K + V) + 2 * R * (K + V))
         res["K%d_V%d" % (K, V)] = {"decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
                                    "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
-                                   "step_bytes_per_launch": int(bytes_step), "flush_due_us": round(flush_us, 2)}
+                                   "step_bytes_per_launch": int(bytes_step), "flush_due_us": round(flush_us, 2),
+                                   "quantize_us": round(quant_us, 2),
+                                   "quantize_gbps": round(qbytes / (quant_us * 1e-6) / 1e9, 1)}
         del gdec, gst, gfl, lq, ssm
         torch.cuda.empty_cache()
     return res

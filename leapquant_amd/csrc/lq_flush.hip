@@ -914,6 +914,227 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 }
 
 // ------------------------------------------------------------------------------------------------------------------
+// standalone quantize of the 64-dim GDN heads: the K = 64 flush's tile (64 key channels x 128 rows, four waves: wave w
+// channels 16 w .. 16 w + 15, lane l rows 16 nt + (l & 15)) with the quantize's arithmetic per head
+// (kernels.py:2126-2242).  (64, 64): two heads of the slot per workgroup (HV even), stacked in the rows; (64, 128):
+// one head.  Per head: P = S^T Q0, MGS over the 64 channels; Q = S P, MGS over the head's rows; U = fp16(S^T Q);
+// E = S - Q U^T; column scales, row scales and codes.
+// ------------------------------------------------------------------------------------------------------------------
+struct QuantShared64 {
+  f32x4 qv[ROWS];              // Q rows of the row's head
+  f32x4 pp[2][K64];            // P, then U, per head [c][r]
+  f32x4 qpart[NW4][ROWS];      // per-wave partial rows of S P (16 channels each)
+  float rowmax[NW4][ROWS];
+  float sk[2][K64];
+};
+
+// per head h: pp[h][c][r] = sum over the head's rows v' of S[v'][c] X[v'][r] (X: the row's head's columns); the rows of
+// a lane first, in order, then across its 16 lanes; fn(h, i, s) for the lane's channel 16 w + 4 (l >> 4) + i
+template <int V_, int HP, typename F>
+__device__ __forceinline__ void colred64(const Tile& t, const f32x4* X, F fn) {
+  const int l = lane_id();
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    f32x4 acc[4] = {};
+#pragma unroll
+    for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) {
+      const f32x4 xv = X[16 * nt + (l & 15)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(t.a[nt][i], xv[r], acc[i][r]);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f32x4 s;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = sum16(acc[i][r]);
+      fn(h, i, s);
+    }
+  }
+}
+
+template <int V_, int HP>
+__global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
+void quantize64_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, float qmax) {
+  static_assert(HP * V_ <= ROWS, "rows of the tile");
+  constexpr int NTV = HP * V_ / 16;
+  __shared__ QuantShared64 sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int NU = HV / HP;
+  const int n = blockIdx.x / NU, hv0 = (blockIdx.x - n * NU) * HP;
+  const int slot = idx[n];
+  if (slot <= 0 || slot >= st.NS) return;
+  const long long s0 = (long long)slot * HV + hv0;
+  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
+  char* base[2];
+#pragma unroll
+  for (int h = 0; h < 2; ++h) base[h] = block_base(st, slot, hv0 + (h < HP ? h : 0));
+  Tile t;                                             // t.a[nt][i] = S[v'][16 w + 4 q + i], v' = 16 nt + l16
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    if (nt < NTV) {
+      const int h = (16 * nt) / V_, v = 16 * nt + l16 - h * V_;
+      const float4 x = *(const float4*)((const float*)base[h] + v * K64 + 16 * w + 4 * q);
+      t.a[nt] = f32x4{x.x, x.y, x.z, x.w};
+    } else {
+      t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  }
+  if (tid < ROWS) {
+    const bool rin = tid < HP * V_;
+    const int v = rin ? tid % V_ : 0;
+    f32x4 q0v;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float x = Q0[v * R + min(r, R - 1)];
+      q0v[r] = (rin && r < R) ? x : 0.f;
+    }
+    sh.qv[tid] = q0v;
+  }
+  __syncthreads();
+  // P = S^T Q, MGS over the channels; Q = S P, MGS over the head's rows (one round: GDN's ITERS = 1)
+  colred64<V_, HP>(t, sh.qv, [&](int h, int i, f32x4 s) { if (l16 == 0) sh.pp[h][16 * w + 4 * q + i] = s; });
+  __syncthreads();
+  if (w == 0) {
+    __builtin_amdgcn_s_setprio(3);
+#pragma unroll
+    for (int h = 0; h < HP; ++h) {
+      f32x4 p = sh.pp[h][l];
+      mgs1(p, R);
+      sh.pp[h][l] = p;
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {                  // partial rows over this wave's 16 channels
+    const int h = (16 * nt) / V_;
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x4 y = sh.pp[h][16 * w + 4 * q + i];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) s[r] = fmaf(t.a[nt][i], y[r], s[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s[r] = xor32_sum(xor16_sum(s[r]));
+    if (q == 0) sh.qpart[w][16 * nt + l16] = s;
+  }
+  __syncthreads();
+  if (w == 0) {
+    __builtin_amdgcn_s_setprio(3);
+    f32x4 p0 = sh.qpart[0][l], p1 = sh.qpart[0][l + 64];
+#pragma unroll
+    for (int w2 = 1; w2 < NW4; ++w2) { p0 += sh.qpart[w2][l]; p1 += sh.qpart[w2][l + 64]; }
+    if (l + 64 >= HP * V_) p1 = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (HP == 2) {                                    // rows l: head 0, rows l + 64: head 1
+      mgs1(p0, R);
+      mgs1(p1, R);
+    } else {
+      mgs(p0, p1, R);
+    }
+    sh.qv[l] = p0;
+    sh.qv[l + 64] = p1;
+    __builtin_amdgcn_s_setprio(0);
+  }
+  __syncthreads();
+  // U = fp16(S^T Q) (sh.pp is not read again before the next barrier), Q16 = fp16(Q)
+  colred64<V_, HP>(t, sh.qv, [&](int h, int i, f32x4 s) {
+    if (l16 == 0) {
+      f32x4 u;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) u[r] = r < R ? hround(s[r]) : 0.f;
+      sh.pp[h][16 * w + 4 * q + i] = u;
+    }
+  });
+  __syncthreads();
+  if (tid < ROWS) {
+    f32x4 x = sh.qv[tid];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) x[r] = r < R ? hround(x[r]) : 0.f;
+    sh.qv[tid] = x;
+  }
+  __syncthreads();
+  // E = S - Q U^T (fp32), column scales per head (kernels.py:2212-2222)
+#pragma unroll
+  for (int h = 0; h < HP; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 16 * w + 4 * q + i;
+      const f32x4 unc = sh.pp[h][c];
+      float sa = 0.f;
+#pragma unroll
+      for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) {
+        const f32x4 qnv = sh.qv[16 * nt + l16];
+        float e = t.a[nt][i];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
+        t.a[nt][i] = e;
+        sa += fabsf(e);
+      }
+      sa = sum16(sa);
+      const float skc = fmaxf(sqrtf(sa / (float)V_), LQ_EPS);                     // kernels.py:2222
+      if (l16 == 0) sh.sk[h][c] = skc;
+    }
+  __syncthreads();
+  float rsk[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) rsk[h][i] = h < HP ? 1.0f / sh.sk[h][16 * w + 4 * q + i] : 1.f;
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {
+    const int h = (16 * nt) / V_;
+    float m = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i] * rsk[h][i]));                   // kernels.py:2224-2227
+    m = xor32_max(xor16_max(m));
+    if (q == 0) sh.rowmax[w][16 * nt + l16] = m;
+  }
+  __syncthreads();
+  // every read of the fp32 states is done: the checkpoints may now overwrite the blocks
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {
+    const int h = (16 * nt) / V_, v = 16 * nt + l16 - h * V_;
+    float rm = sh.rowmax[0][16 * nt + l16];
+#pragma unroll
+    for (int w2 = 1; w2 < NW4; ++w2) rm = fmaxf(rm, sh.rowmax[w2][16 * nt + l16]);
+    const float svv = fmaxf(rm, LQ_EPS);
+    const float rsv = qmax / svv;
+    uint32_t word = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float x = (t.a[nt][i] * rsk[h][i]) * rsv;                                         // kernels.py:2229
+      const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
+      word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
+    }
+    *(uint32_t*)(base[h] + v * K64 + 16 * w + 4 * q) = word;
+    if (w == 0 && q == 0) ((float*)(base[h] + V_ * K64 + 4 * K64))[v] = svv;
+  }
+  if (tid < K64) {
+#pragma unroll
+    for (int h = 0; h < HP; ++h) {
+      ((float*)(base[h] + V_ * K64))[tid] = sh.sk[h][tid];
+      f16_t* UQ = (f16_t*)(base[h] + V_ * K64 + 4 * (K64 + V_));
+      for (int r = 0; r < R; ++r) UQ[r * (K64 + V_) + tid] = f2h(sh.pp[h][tid][r]);
+    }
+  } else if (tid < K64 + HP * V_) {
+    const int v2 = tid - K64, h = v2 / V_;
+    f16_t* UQ = (f16_t*)((h ? base[1] : base[0]) + V_ * K64 + 4 * (K64 + V_));
+    for (int r = 0; r < R; ++r) UQ[r * (K64 + V_) + K64 + v2 - h * V_] = f2h(sh.qv[v2][r]);
+  }
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    if (tid < L) st.Wbuf[(s0 + h) * L + tid] = 0.f;
+    if (tid == 0) {
+      st.Pbuf[s0 + h] = 1.f;
+      st.hcnt[s0 + h] = 0;
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
 // prefill dequant, KDA (state.py:118-128): S = diag(exp(P)) applied to S0 = Q U^T + deq(Sq) over the key channels,
 // plus sum_{j<h} w_j u_j (K_j * D_j)^T with D_j = prod_{j<i<h} e_i, written in place as fp32.  The window is left as
 // it is (the checkpoint after the engine's prefill resets it).  w_j K_j D_j goes into the rank-h MFMA as three bf16
@@ -1264,8 +1485,10 @@ extern "C" int lq_quantize(const lq_state* st, const float* Q0, const int* idx, 
   if (st->K == KD && st->R > 8) quantize_kernel<false, KD, VD, 16><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   else if (st->K == KD && st->R > 4) quantize_kernel<false, KD, VD, 8><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
   else if (st->K == KD) quantize_kernel<false><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
-  else if (st->V == VD) quantize_kernel<false, 64, 128><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
-  else quantize_kernel<false, 64, 64><<<g, QT, 0, s>>>(*st, Q0, idx, qmax, 1);
+  else if (st->V == VD) quantize64_kernel<128, 1><<<g, FT4, 0, s>>>(*st, Q0, idx, qmax);
+  else if (st->HV % 2 == 0)                           // two heads of the slot per workgroup
+    quantize64_kernel<64, 2><<<dim3((unsigned)(N * st->HV / 2)), FT4, 0, s>>>(*st, Q0, idx, qmax);
+  else quantize64_kernel<64, 1><<<g, FT4, 0, s>>>(*st, Q0, idx, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

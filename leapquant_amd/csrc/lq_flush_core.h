@@ -206,6 +206,21 @@ __device__ __forceinline__ void mgs(f32x4& p0, f32x4& p1, int R) {
     }
   }
 }
+// the same on one row per lane (the 64 rows of one head of a pair, or the 64 key channels of a K = 64 head)
+__device__ __forceinline__ void mgs1(f32x4& p, int R) {
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    if (j < R) {
+#pragma unroll
+      for (int c = 0; c < j; ++c) {
+        const float sc = sum64u(p[c] * p[j]);
+        p[j] = p[j] - sc * p[c];
+      }
+      const float nrm = sum64u(p[j] * p[j]);
+      p[j] *= rsqrt_rn(fmaxf(nrm, 1e-30f));
+    }
+  }
+}
 // the same on N columns held as plain arrays (rows l, l + 64 of a lane of wave 0), for ranks up to 16
 template <int N>
 __device__ __forceinline__ void mgs_n(float (&p0)[N], float (&p1)[N], int R) {

@@ -119,10 +119,11 @@ def test_flush_matches_oracle(K, V, L, GQA):
 
 
 @pytest.mark.parametrize("K,V", DIMS)
-@pytest.mark.parametrize("qmax", [127.0, 31.0])
-def test_quantize_matches_oracle(K, V, qmax):
-    rng = np.random.default_rng(1400 + K + V + int(qmax))
-    NS, HV, H = 5, 4, 2
+@pytest.mark.parametrize("qmax,HV,H", [(127.0, 4, 2), (31.0, 4, 2), (127.0, 3, 3)])
+def test_quantize_matches_oracle(K, V, qmax, HV, H):
+    """The K = 64 quantize: (64, 64) with HV even takes two heads of a slot per workgroup, with HV odd one."""
+    rng = np.random.default_rng(1400 + K + V + int(qmax) + HV)
+    NS = 5
     S = (0.02 * rng.standard_t(3, (NS, HV, V, K))).astype(np.float32)
     S[2, 1] = 0.0                                        # all-zero state: EPS floors
     st = O.new_state(NS, HV, H, K=K, V=V, L=16)
