@@ -19,7 +19,8 @@ Measurement:
     (lq_gdn_step), algorithmic bytes per launch over the average launch duration, from HIP events around graph replays
     of step launches over the same rotated sets (every window runs h = 0..63).  `traffic`: the HBM bytes per launch that
     rocprofv3's FETCH_SIZE / WRITE_SIZE counters read for this same command, calibrated on the 64 MiB copies it ends with.
-  * the same step on a dense bf16 state (`lq_dense_step`) as the baseline.
+  * the same step on a dense bf16 state (`lq_dense_step`, tuned as the INT8 step is) as the baseline, beside the
+    ceiling of its access pattern (`bf16_state_rmw_ceiling`: a pure read-and-write-back stream of the same blocks).
 Usage: python bench.py [--gpus 1] [--steps 1024] [--warmup 128] [--no-cpu]
 """
 import argparse
@@ -433,6 +434,44 @@ def loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture):
     return out
 
 
+def dense_rmw_ceiling(torch, stream, Sd, B, HV, NSET, capture):
+    """The ceiling of the bf16-state baseline's access pattern: liblq_probe.so reads each (row, value head) block of the
+    dense bf16 state (32 KiB) and writes it back in place (unchanged), two blocks per 256-thread workgroup as the
+    baseline's workgroups take them, over the same rotated sets, in graphs of 64 launches; plain and non-temporal."""
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(ROOT, "leapquant_amd", "_build", "liblq_probe.so"))
+    probe.lq_probe_rmw.restype = ctypes.c_int
+    probe.lq_probe_rmw.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_int, ctypes.c_uint, ctypes.c_void_p]
+    blk = Sd.stride(1) * Sd.element_size()
+    nblk = B * HV
+    base = [Sd.data_ptr() + (1 + B * k) * HV * blk for k in range(NSET)]
+    out = {"workload": "read and write back each %d-byte (row, value head) block of the dense bf16 state, two per "
+                       "256-thread workgroup, %d rotated sets" % (blk, NSET)}
+    for nt, tag in ((0, "plain"), (1, "nt")):
+        def launch(i, nt=nt):
+            rc = probe.lq_probe_rmw(ctypes.c_void_p(base[i % NSET]), blk, blk, nblk, 2, nt, 0,
+                                    ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+            if rc:
+                raise RuntimeError("lq_probe_rmw failed (%d)" % rc)
+        gr = capture(launch, 64)
+        gr.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        with torch.cuda.stream(stream):
+            e0.record(stream)
+            for _ in range(4):
+                gr.replay()
+            e1.record(stream)
+        e1.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / (64 * 4)
+        out["%s_us" % tag] = round(us, 3)
+        out["%s_gbps" % tag] = round(2 * nblk * blk / (us * 1e-6) / 1e9, 1)
+        del gr
+    out["bytes_per_launch"] = 2 * nblk * blk
+    return out
+
+
 def traffic_bytes(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE runs of this command, each
     scaled by what the counter reads for the 64 MiB copies the bench ends with (None when the summary is absent)."""
@@ -686,6 +725,7 @@ def main():
     torch.cuda.synchronize()
     bf16_us = d0.elapsed_time(d1) * 1e3 / (4 * CH)
     bf16_gbps = dense_bytes(B, HV, H, K, V) / (bf16_us * 1e-6) / 1e9
+    rmw = dense_rmw_ceiling(torch, stream, Sd, B, HV, NSET, capture)
     del gd, Sd
 
     # ---- conv1d update fused into the step (lq_gdn_step_conv) against the conv update kernel + step, same rotated
@@ -770,6 +810,7 @@ def main():
                    "batch": B, "value_heads": HV, "key_heads": H, "head_dim": K, "window": L, "rank": R},
         "achieved_gbps": round(decode_gbps, 1),
         "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
+        "bf16_state_rmw_ceiling": rmw,
         "speedup_vs_bf16_step": round(bf16_us / us_per_step, 3),
         # the timed region is one kernel per decode call: the step that flushes the heads it fills
         "roofline": {"bound": "hbm", "achieved": round(decode_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
