@@ -26,7 +26,8 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 3
+#define LQ_ABI_VERSION 4
+#define LQ_SCHED_INTS 512   /* ints of lq_state.sched: eight counters, 256 bytes apart */
 
 enum lq_status {
   LQ_OK = 0,
@@ -53,6 +54,12 @@ typedef struct lq_state {
                              flush scans hcnt (the contract). */
   float qmax;             /* code range of the stored checkpoint: 127 (INT8) or 31 (6-bit codes in the int8
                              container); 0 means 127.  The decode steps dequantise with it (Sq Sk Sv / qmax). */
+  int* sched;             /* optional (NULL: static schedule): int[LQ_SCHED_INTS], zero-initialised by the owner and
+                             left zero by every flush.  With it, the persistent flush hands out its candidate heads
+                             through counters in this buffer (each workgroup takes its next head when it is near the
+                             end of the current one), so that the workgroups sharing a CU -- which the hardware does
+                             not serve equally -- finish together; without it, workgroup b takes candidates b,
+                             b + grid, ...  Same results either way.  One flush at a time per buffer. */
 } lq_state;
 
 /* Decode inputs of one call: N rows, one token each. */

@@ -5,7 +5,8 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_build", "liblq.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
+SCHED_INTS = 512           # include/lq.h: LQ_SCHED_INTS
 
 c_void_p, c_int, c_float, c_ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
 
@@ -14,7 +15,7 @@ class LqState(ctypes.Structure):
     _fields_ = [("ssm", c_void_p), ("slot_stride", c_ll), ("Kbuf", c_void_p), ("Ubuf", c_void_p),
                 ("Wbuf", c_void_p), ("Pbuf", c_void_p), ("Gbuf", c_void_p), ("hcnt", c_void_p),
                 ("NS", c_int), ("HV", c_int), ("H", c_int), ("K", c_int), ("V", c_int), ("L", c_int), ("R", c_int),
-                ("ctl", c_void_p), ("qmax", c_float)]
+                ("ctl", c_void_p), ("qmax", c_float), ("sched", c_void_p)]
 
 
 class LqStepIO(ctypes.Structure):

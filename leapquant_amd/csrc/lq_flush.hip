@@ -14,16 +14,21 @@ namespace {
 
 using namespace lqf;
 
-// Persistent flush: workgroup b checks the candidate units p = b + gridDim.x k (row n = p / (HV / U), heads
-// U (p % (HV / U)) .. + U - 1; U = 1 but for the paired 64-dim heads) 64 at a time (wave 0, one per lane), and
-// processes the due ones (slot > 0, hcnt == L for some head of the unit; kernels.py:1200) one after another.
+// Persistent flush over the candidate units p (row n = p / (HV / U), heads U (p % (HV / U)) .. + U - 1; U = 1 but for
+// the paired 64-dim heads); a due unit (slot > 0, hcnt == L for some head of the unit; kernels.py:1200) is flushed by
+// one workgroup.  With the schedule counters st.sched (and more candidates than workgroups), workgroup b takes
+// candidate b first and then the next candidate its counter hands out, one at a time: the four workgroups that share
+// a CU are not served equally by the hardware (at config 3 the first dispatched took 403k cycles for its eight heads,
+// the last 611k), so a fixed share per workgroup ends when the slowest does, while taken heads let the faster ones
+// take more.  Without them, workgroup b checks the candidates b + gridDim.x k 64 at a time (wave 0, one per lane) and
+// processes the due ones in turn.
 // With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
 // otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
 // With a due list (dlist, lq_decode_noalloc) the flush takes exactly the listed heads instead: workgroup b the entries
 // b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, so
 // an entry left by an interrupted call is skipped; the last workgroup to finish empties the list.
-// `head(slot, hv0, mask)` flushes the due heads hv0 + h (bit h of mask) of one unit with the whole workgroup; `due` is
-// a word of the workgroup's shared memory.
+// `head(slot, hv0, mask, sched)` flushes the due heads hv0 + h (bit h of mask) of one unit with the whole workgroup
+// and, with sched set, leaves the workgroup's next candidate in `due`, a word of the workgroup's shared memory.
 template <int U>
 __device__ __forceinline__ unsigned unit_mask(const lq_state& st, int slot, int hv0) {
   unsigned m = 0;
@@ -39,28 +44,58 @@ __device__ void flush_scan(unsigned long long& due, const lq_state& st, const in
   const int total = N * NU;
   const int stride = gridDim.x;
   if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
-  for (int base = blockIdx.x; base < total; base += 64 * stride) {
-    if (threadIdx.x < 64) {
-      const int p = base + stride * (int)threadIdx.x;
-      bool d = false;
-      if (p < total) {
-        const int n = p / NU, u = p - n * NU;
-        const int slot = idx[n];
-        d = slot > 0 && slot < st.NS && unit_mask<U>(st, slot, u * U) != 0;
-      }
-      const unsigned long long m = __ballot(d);
-      if (threadIdx.x == 0) due = m;
-    }
+  if (st.sched && total > stride && total < (1 << lqf::SCHED_BITS)) {
+    // dynamic schedule: candidate b first, then whichever the workgroup's counter hands out (each head takes the next
+    // one near its end and leaves it in `due`); a candidate that is not due takes the next at once
+    if (threadIdx.x == 0) due = blockIdx.x;
     __syncthreads();
-    unsigned long long m = due;
-    __syncthreads();
-    while (m) {
-      const int b = __ffsll((long long)m) - 1;
-      m &= m - 1;
-      const int p = base + stride * b;
+    for (;;) {
+      const int p = (int)due;
+      __syncthreads();                                // every thread has its candidate before a head rewrites `due`
+      if (p >= total) break;
       const int n = p / NU, u = p - n * NU;
       const int slot = idx[n];
-      head(slot, u * U, unit_mask<U>(st, slot, u * U));
+      const unsigned m = slot > 0 && slot < st.NS ? unit_mask<U>(st, slot, u * U) : 0u;
+      if (m) {
+        head(slot, u * U, m, st.sched);
+      } else {
+        if (threadIdx.x == 0) due = (unsigned long long)lqf::sched_next(st.sched);
+        __syncthreads();
+      }
+    }
+    // every workgroup's last take precedes its count here, so the last of a group counted clears the group's counter
+    // for the next call
+    const int grp = (int)(blockIdx.x % lqf::SCHED_GROUPS);
+    const int members = (stride - grp + lqf::SCHED_GROUPS - 1) / lqf::SCHED_GROUPS;   // workgroups of the group
+    int* ctr = lqf::sched_counter(st.sched);
+    if (threadIdx.x == 0 &&
+        (__hip_atomic_fetch_add(ctr, 1 << lqf::SCHED_BITS, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >>
+         lqf::SCHED_BITS) == members - 1)
+      __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    for (int base = blockIdx.x; base < total; base += 64 * stride) {
+      if (threadIdx.x < 64) {
+        const int p = base + stride * (int)threadIdx.x;
+        bool d = false;
+        if (p < total) {
+          const int n = p / NU, u = p - n * NU;
+          const int slot = idx[n];
+          d = slot > 0 && slot < st.NS && unit_mask<U>(st, slot, u * U) != 0;
+        }
+        const unsigned long long m = __ballot(d);
+        if (threadIdx.x == 0) due = m;
+      }
+      __syncthreads();
+      unsigned long long m = due;
+      __syncthreads();
+      while (m) {
+        const int b = __ffsll((long long)m) - 1;
+        m &= m - 1;
+        const int p = base + stride * b;
+        const int n = p / NU, u = p - n * NU;
+        const int slot = idx[n];
+        head(slot, u * U, unit_mask<U>(st, slot, u * U), nullptr);
+      }
     }
   }
   if (st.ctl) {                 // every workgroup has read the flag; the last one to finish clears it
@@ -95,7 +130,7 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
     __syncthreads();
     if (take >= 0) {
       const int slot = (int)(take / HV), hv = (int)(take % HV);
-      head(slot, hv - hv % U, 1u << (hv % U));
+      head(slot, hv - hv % U, 1u << (hv % U), nullptr);
     }
   }
   __syncthreads();
@@ -111,7 +146,9 @@ __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
   __shared__ FlushShared<RA> sh;
-  auto head = [&](int slot, int hv, unsigned) { flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax); };
+  auto head = [&](int slot, int hv, unsigned, int* sched) {
+    flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax, sched);
+  };
   if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan(sh.due, st, idx, N, head);
 }
@@ -121,7 +158,7 @@ __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush4_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                    int* dlist) {
   __shared__ FlushShared4 sh;
-  auto head = [&](int slot, int hv, unsigned) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax); };
+  auto head = [&](int slot, int hv, unsigned, int* sched) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax, sched); };
   if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan(sh.due, st, idx, N, head);
 }
@@ -275,7 +312,7 @@ __device__ __forceinline__ f32x4 p_step64(const FlushShared64& sh, const f16x4 b
 
 template <int V_, int HP>
 __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv0,
-                             unsigned mask, float qmax) {
+                             unsigned mask, float qmax, int* sched = nullptr) {
   static_assert(HP * V_ <= ROWS && V_ % 32 == 0, "rows of the tile");
   constexpr int NTV = HP * V_ / 16;
   const int HV = st.HV, L = st.L, R = st.R;
@@ -552,6 +589,8 @@ __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float*
 #pragma unroll
     for (int i = 0; i < 4; ++i) rsk[1][i] = rsk[0][i];
   }
+  int next = 0;                                       // dynamic schedule: this workgroup's next candidate
+  if (sched && tid == 0) next = sched_next(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
@@ -608,6 +647,7 @@ __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float*
       }
     }
   }
+  if (sched && tid == 0) sh.due = (unsigned long long)next;
   __syncthreads();                                    // LDS reuse by the next unit of this workgroup
 }
 
@@ -616,7 +656,9 @@ __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush64_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                     int* dlist) {
   __shared__ FlushShared64 sh;
-  auto head = [&](int slot, int hv0, unsigned mask) { flush_head64<V_, HP>(sh, st, Q0, slot, hv0, mask, qmax); };
+  auto head = [&](int slot, int hv0, unsigned mask, int* sched) {
+    flush_head64<V_, HP>(sh, st, Q0, slot, hv0, mask, qmax, sched);
+  };
   if (dlist) flush_listed<HP>(sh.due, st, idx, N, dlist, head);
   else flush_scan<HP>(sh.due, st, idx, N, head);
 }

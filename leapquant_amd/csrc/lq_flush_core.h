@@ -555,9 +555,29 @@ __device__ __forceinline__ f32x4 p_step(const FlushShared<RA>& sh, const f16x4 b
 // its loads read zeros past its rows / columns, every product and Gram sum then only adds exact zeros, the column
 // means divide by V_, and the stores write its own rows / columns only.  RA = 8 (GDN 128 x 128, R = 8): the factor
 // products carry eight columns (lanes l < 32 of each MFMA) and CholeskyQR drops dependent columns (kernels.py:1744-1772).
+// Dynamic head schedule of the persistent flush (lq_state.sched, LQ_SCHED_INTS ints): eight counters 256 bytes apart;
+// workgroup b uses counter b % 8 (the dispatcher deals workgroups round-robin over the eight XCDs), so that the
+// grid's takes spread over eight addresses instead of queueing on one (one counter measured 41.5 -> 51 us on a flush
+// where every workgroup took once at the same time).  Counter x hands out the candidates after the grid's first
+// ones with x = (p - gridDim.x) % 8, take g giving p = gridDim.x + 8 g + x; its low SCHED_BITS count the takes, the
+// high bits the group's workgroups done, and the last of them clears it.  A head takes its workgroup's next candidate
+// (thread 0) after its column scales, so that the atomic's latency hides behind the rest of the head and the
+// workgroup commits to the next head only near the end of this one, and leaves it in the shared `due` word before
+// the head's last barrier.
+constexpr int SCHED_BITS = 20, SCHED_GROUPS = 8, SCHED_STRIDE = 64;
+static_assert(SCHED_GROUPS * SCHED_STRIDE == LQ_SCHED_INTS, "counters of lq_state.sched");
+__device__ __forceinline__ int* sched_counter(int* sched) {
+  return sched + SCHED_STRIDE * (int)(blockIdx.x % SCHED_GROUPS);
+}
+__device__ __forceinline__ int sched_next(int* sched) {
+  const int g = __hip_atomic_fetch_add(sched_counter(sched), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                ((1 << SCHED_BITS) - 1);
+  return (int)gridDim.x + SCHED_GROUPS * g + (int)(blockIdx.x % SCHED_GROUPS);
+}
+
 template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
 __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
-                           float qmax) {
+                           float qmax, int* sched = nullptr) {
   static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
   static_assert(RA == 4 || (RA == 8 && !KDA && K_ == KD && V_ == VD), "R = 8: GDN 128 x 128 heads");
   constexpr int NB = RA / 4;
@@ -810,6 +830,8 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
     rsk[2] = dpp<0xaa>(rs);
     rsk[3] = dpp<0xff>(rs);
   }
+  int next = 0;                                       // dynamic schedule: this workgroup's next candidate
+  if (sched && tid == 0) next = sched_next(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
@@ -860,6 +882,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   if (tid == 0) {
     if (!KDA) st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
+    if (sched) sh.due = (unsigned long long)next;
   }
   __syncthreads();                                    // LDS reuse by the next head of this workgroup
 }
@@ -967,10 +990,47 @@ __device__ __forceinline__ void rebuild_half4(Tile4& t, const bf16_t (*A)[OPS4],
     __builtin_amdgcn_sched_barrier(0);
   }
 }
-// the 16 code words of the lane's tile entries (zero past a K_ x V_ < 128 x 128 head's rows / columns)
+// exchanges of 32-bit values between lane groups: swap32 trades the upper 32 lanes of a with the lower 32 of b,
+// swap16 the odd 16-lane rows of a with the even rows of b (gfx950 v_permlane32_swap / v_permlane16_swap)
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+// the 16 code words of the lane's tile entries, wds[g][nt] = Sq[16 nt + l16][32 w + 16 g + 4 q .. + 3] (zero past a
+// K_ x V_ < 128 x 128 head's rows / columns).  128 x 128: 16-byte loads, then a transpose across the lane groups.  Load
+// k of lane (q, l16) takes Sq[16 (2 k + (q >> 1)) + l16][32 w + 16 (q & 1) .. + 15], so that one wave instruction
+// covers the wave's 32 bytes of 32 rows (dword loads straight into the layout touch 16 rows for 256 bytes, and the
+// tile load measured 10.3k -> 9.6k cycles per head this way at config 3); word j of lane group q's run is the word
+// lane group j needs, so a 4 x 4 transpose over the lane groups (two swap32, two swap16) delivers it.
 template <int K_, int V_>
 __device__ __forceinline__ void load_code_words4(uint32_t wds[2][8], const int8_t* Sq) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
+  if constexpr (K_ == KD && V_ == VD) {
+    const int l16 = l & 15;
+    uint4 x[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      x[k] = *(const uint4*)(Sq + (16 * (2 * k + (q >> 1)) + l16) * KD + 32 * w + 16 * (q & 1));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t a0 = x[k].x, a1 = x[k].y, a2 = x[k].z, a3 = x[k].w;
+      swap32(a0, a2);
+      swap32(a1, a3);
+      swap16(a0, a1);
+      swap16(a2, a3);
+      wds[0][2 * k] = a0;                             // lane group 0's run: g = 0, nt = 2 k
+      wds[1][2 * k] = a1;                             // group 1: g = 1, nt = 2 k
+      wds[0][2 * k + 1] = a2;                         // group 2: g = 0, nt = 2 k + 1
+      wds[1][2 * k + 1] = a3;                         // group 3: g = 1, nt = 2 k + 1
+    }
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
     const int c = 32 * w + 16 * g + 4 * q;
@@ -1057,7 +1117,7 @@ __device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh
 
 template <int K_ = KD, int V_ = VD>
 __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
-                            float qmax) {
+                            float qmax, int* sched = nullptr) {
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
@@ -1271,6 +1331,8 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
     rsk[g][2] = dpp<0xaa>(rs);
     rsk[g][3] = dpp<0xff>(rs);
   }
+  int next = 0;                                       // dynamic schedule: this workgroup's next candidate
+  if (sched && tid == 0) next = sched_next(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
@@ -1325,6 +1387,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   if (tid == 0) {
     st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
+    if (sched) sh.due = (unsigned long long)next;
   }
   __syncthreads();                                    // LDS reuse by the next head of this workgroup
 }

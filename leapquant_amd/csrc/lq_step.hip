@@ -131,6 +131,24 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
 
+  // The row's own inputs (q, k, v, gate) do not depend on its slot: requested before the slot index, so that their
+  // latency overlaps its load (a padding row reads them too and ignores them).
+  const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
+  bf16_t kxr[NE], qxr[NE];
+  if (!CONV) {
+#pragma unroll
+    for (int e = 0; e < NE; ++e) {
+      const int c = lane + 64 * e;
+      kxr[e] = mrow[H * KD + hk * KD + c];
+      qxr[e] = mrow[hk * KD + c];
+    }
+  }
+  const bf16_t araw = ((const bf16_t*)io.a)[(long long)n * HV + hv];
+  const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
+  const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
+  float vin = 0.f;
+  if (!CONV) vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
+
   const int slot = io.idx[n];
   // padding row (kernels.py:374-378); a slot outside the cache (or, fused conv, outside the conv state) counts as one
   if (slot <= 0 || slot >= st.NS || (CONV && slot >= cv.NS)) {
@@ -145,26 +163,17 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const float* Skp = (const float*)(base + VD * KD);
   const float* Svp = Skp + KD;
   const f16_t* UQp = (const f16_t*)(Svp + VD);
-  const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
   const long long sh_ = (long long)slot * HV + hv;
   float* Wp = st.Wbuf + sh_ * L;
-  bf16_t kxr[NE], qxr[NE];
   float skx[NE], wx[NE];
   ConvTaps ktap[NE], qtap[NE], vtap;  // CONV: taps of the key / query channels c and of the value channel lt
   const long long cvb = CONV ? (long long)slot * cv.slot_stride : 0;
 #pragma unroll
   for (int e = 0; e < NE; ++e) {
     const int c = lane + 64 * e;
-    if (!CONV) {
-      kxr[e] = mrow[H * KD + hk * KD + c];
-      qxr[e] = mrow[hk * KD + c];
-    }
     skx[e] = Skp[c];
     wx[e] = Wp[min(c, L - 1)];
   }
-  const bf16_t araw = ((const bf16_t*)io.a)[(long long)n * HV + hv];
-  const bf16_t braw = ((const bf16_t*)io.b)[(long long)n * HV + hv];
-  const float dtb = io.dt_bias[hv], alog = io.A_log[hv];
   // factor rows U^T (fp16) of all G heads: A fragment rows m = g2 R + r of the factor-dot MFMA, tile ft of them
   f16x8 ufr[KS32];
   const int ft = RM == 4 ? 0 : g;
@@ -175,9 +184,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 #pragma unroll
     for (int ks = 0; ks < KS32; ++ks) ufr[ks] = *(const f16x8*)(U + 32 * ks + 8 * q4);
   }
-  float vin = 0.f;
   if (CONV) vtap = conv_taps(cv, mrow, cvb, 2 * H * KD + hv * VD + lt);
-  else vin = bf2f(mrow[2ll * H * KD + hv * VD + lt]);
   const float sv = Svp[lt];
   float qt[RM];                 // Q^T[r][lt]
 #pragma unroll

@@ -80,15 +80,21 @@ def _check_qmax(qmax):
     return float(qmax)
 
 
-def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, ctl=None, qmax=QMAX):
+def state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, NS, HV, H, K, V, L, R, ctl=None, qmax=QMAX,
+                 sched=None):
     """lq_state of a layer: `Sq` is any view whose data pointer is the checkpoint of (slot 0, head 0), i.e. the fp32
     cache's data pointer.  `ctl`: optional int32 [2] due flag + flush counter kept by the kernels (None: the flush scans
-    hcnt).  `qmax`: code range of the stored checkpoint (the decode steps dequantise Sq Sk Sv / qmax)."""
+    hcnt).  `qmax`: code range of the stored checkpoint (the decode steps dequantise Sq Sk Sv / qmax).  `sched`:
+    optional int32 [LQ_SCHED_INTS] zero buffer of the counters through which the persistent flush hands out its heads
+    (None: static schedule; same results)."""
     if ctl is not None and (ctl.dtype != torch.int32 or ctl.numel() < 2):
         raise ValueError("ctl: int32 [2] expected")
+    if sched is not None and (sched.dtype != torch.int32 or sched.numel() < _lib.SCHED_INTS or not sched.is_contiguous()):
+        raise ValueError("sched: contiguous int32 [%d] expected" % _lib.SCHED_INTS)
     return _lib.LqState(_dev(Sq), SS, _dev(Kbuf), _dev(Ubuf), _dev(Wbuf), _dev(Pbuf),
                         _dev(Gbuf) if Gbuf is not None else 0, _dev(hcnt), NS, HV, H, K, V, L, R,
-                        _dev(ctl) if ctl is not None else 0, _check_qmax(qmax))
+                        _dev(ctl) if ctl is not None else 0, _check_qmax(qmax),
+                        _dev(sched) if sched is not None else 0)
 
 
 def _check_view(Sq, NS, HV, V, K, SS):
@@ -176,10 +182,11 @@ def make_kda_step(NS, HV, H, K, V, L, SS, R=4, SMS=None, NSTAGE=6, NSTAGEQ=4, NC
 
 
 def make_flush(NS, HV, K, V, L, SS, R=4, ITERS=1, SMS=None, NCG=3, MAXIT=128, PAD=8, KDA=False, MMT="bf16",
-               PNMIN=1e-20, NMAX=0, NTP=0, RSG=None, qmax=QMAX):
+               PNMIN=1e-20, NMAX=0, NTP=0, RSG=None, qmax=QMAX, sched=None):
     """End-of-window flush (kernels.py:1077-2033).  Returns
     flush(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, Sq16, UQ, Q0, idx).  Due heads (hcnt == L) are found on
-    the device; ITERS = 1 and PNMIN = 1e-20 as in the reference's use (state.py:79)."""
+    the device; ITERS = 1 and PNMIN = 1e-20 as in the reference's use (state.py:79).  `sched` (not in the reference's
+    signature): the optional int32 [LQ_SCHED_INTS] zero buffer of the flush's dynamic head schedule (see state_struct)."""
     _check_dims(K, V, L, R, kda=KDA, rank="flush")
     assert ITERS == 1, "liblq: one subspace iteration per flush (ITERS = 1)"
     assert PNMIN == 1e-20
@@ -199,7 +206,8 @@ def make_flush(NS, HV, K, V, L, SS, R=4, ITERS=1, SMS=None, NCG=3, MAXIT=128, PA
         _need(idx, torch.int32, (N,), "idx")
         if KDA and (Gbuf.element_size() != 2 or tuple(Gbuf.shape) != (NS, HV, L, K)):
             raise ValueError("Gbuf: 16-bit [NS, HV, L, K] expected")
-        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf if KDA else None, hcnt, NS, HV, H, K, V, L, R)
+        st = state_struct(Sq, SS, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf if KDA else None, hcnt, NS, HV, H, K, V, L, R,
+                          sched=sched)
         _lib.check(L_.lq_flush(ctypes.byref(st), _p(Q0), _p(idx), N, kda, ctypes.c_float(qmax), _stream(idx)),
                    "lq_flush")
 

@@ -86,13 +86,15 @@ class LeapQuantState:
         # heads made due by decode steps since the last flush / flush workgroups done: lets an idle flush return at
         # once (kept by the kernels; zero between calls)
         self.ctl = torch.zeros(2, dtype=torch.int32, device=dev)
+        # the flush's dynamic head schedule (counters the flush leaves at zero)
+        self.sched = torch.zeros(_lib.SCHED_INTS, dtype=torch.int32, device=dev)
         self.Q0 = torch.randn(V, R, generator=torch.Generator().manual_seed(0)).to(dev)
 
         if kda:
             self.kstep = KN.make_kda_step(NS, HV, H, K, V, L, SS, R=R, GLB=float(gate_lower_bound), qmax=qmax)
         else:
             self.kstep = KN.make_gdn_step(NS, HV, H, K, V, L, SS, R=R, qmax=qmax)
-        self.kflush = KN.make_flush(NS, HV, K, V, L, SS, R=R, ITERS=1, KDA=kda, NMAX=nmax, qmax=qmax)
+        self.kflush = KN.make_flush(NS, HV, K, V, L, SS, R=R, ITERS=1, KDA=kda, NMAX=nmax, qmax=qmax, sched=self.sched)
         if not kda:                          # the KDA prefill round trip has its own entry points
             self.kdeq = _make_dequant(NS, HV, K, V, L, SS, buf_dtype=KN.BF16, R=R, qmax=qmax)
             self.kquant = _make_quantize(NS, HV, K, V, L, SS, R=R, ITERS=1, qmax=qmax)
@@ -126,7 +128,7 @@ class LeapQuantState:
                 raise ValueError("the fp32 state cache must be 16-byte aligned with a slot stride divisible by 4")
             self._st = KN.state_struct(ssm, self.SS, self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf,
                                        self.Gbuf if self.kda else None, self.hcnt, self.NS, self.HV, self.H, self.K,
-                                       self.V, self.L, self.R, ctl=self.ctl, qmax=self.qmax)
+                                       self.V, self.L, self.R, ctl=self.ctl, qmax=self.qmax, sched=self.sched)
             self._skey = k
         return self._st
 

@@ -8,7 +8,8 @@ derived from the kernels' own index arithmetic (leapquant_amd/csrc/lq_step.hip, 
     checkpoint region of the (slot, hv) block (codes, Sk, Sv, U^T | Q^T; the whole fp32 block for quantize / dequant),
     the window rows Kbuf[slot, hv // G, 0:L], Ubuf / Wbuf / Gbuf [slot, hv, 0:L], Pbuf[slot, hv], hcnt[slot, hv], and
     for the fused conv the slot's three taps of every channel;
-  * per call: A_log, dt_bias, Q0, the due flag pair ctl and the conv weights / bias.
+  * per call: A_log, dt_bias, Q0, the due flag pair ctl, the flush's schedule counter sched and the conv weights /
+    bias.
 
 The model is conservative about data: every valid (slot, head) of a flush is taken as due.  `CheckingLib` stands in for
 liblq.so: each entry point validates its arguments as the library does, computes the call's footprint and checks that
@@ -69,7 +70,7 @@ def _arg(x):
 class CheckingLib:
     """Drop-in for the ctypes handle of liblq.so: checks the footprint of every call, launches nothing."""
 
-    ABI = 3
+    ABI = 4
 
     def __init__(self):
         self.storages = Storages()
@@ -142,6 +143,8 @@ class CheckingLib:
     def _ctl(self, st, what):
         if st.ctl:
             self.storages.check(what + " ctl", st.ctl, 0, 8)
+        if st.sched:
+            self.storages.check(what + " sched", st.sched, 0, 4 * 512)
 
     # ---- entry points ---------------------------------------------------------------------------------------------
     def lq_abi_version(self):

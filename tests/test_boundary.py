@@ -324,6 +324,27 @@ def test_factories_check_static_shapes(lib):
     assert (KN.QMAX, KN.EPS, KN.SOFTPLUS_THRESHOLD) == (127.0, 1e-12, 20.0)
 
 
+def test_flush_schedule_counter(lib):
+    """lq_state.sched: an int32 [LQ_SCHED_INTS] buffer of counters, zero between calls, that the state allocates and
+    passes to its flush; the struct carries it after qmax (the header's layout), and a buffer of another type or size
+    is refused on the host."""
+    from leapquant_amd import _lib, kernels as KN
+    from leapquant_amd.state import LeapQuantState
+    fields = [f[0] for f in _lib.LqState._fields_]
+    assert fields[-3:] == ["ctl", "qmax", "sched"]
+    assert re.search(r"float qmax;.*?int\* sched;.*?\} lq_state;", open(HEADER).read(), re.S)
+    ssm = torch.zeros(3, 2, 128, 128)
+    z = torch.zeros(1)
+    with pytest.raises(ValueError, match="sched"):
+        KN.state_struct(ssm, ssm.stride(0), z, z, z, z, None, z, 3, 2, 1, 128, 128, 16, 4, sched=torch.zeros(512))
+    with pytest.raises(ValueError, match="sched"):
+        KN.state_struct(ssm, ssm.stride(0), z, z, z, z, None, z, 3, 2, 1, 128, 128, 16, 4,
+                        sched=torch.zeros(1, dtype=torch.int32))
+    lq = LeapQuantState(ssm, 1, L=16)
+    assert lq.sched.dtype == torch.int32 and lq.sched.shape == (_lib.SCHED_INTS,) and int(lq.sched.abs().sum()) == 0
+    assert int(re.search(r"#define\s+LQ_SCHED_INTS\s+(\d+)", open(HEADER).read()).group(1)) == _lib.SCHED_INTS
+
+
 def test_get_state_registry(lib):
     """One LeapQuantState per cache tensor identity; a re-allocated cache drops the old buffers (state.py:172-189)."""
     from leapquant_amd import state as S
