@@ -158,10 +158,18 @@ def kda_bench(torch, dev, stream, capture):
         rt_d.append(event_ms(torch, stream, lambda: lq.dequantize(ssm, sets[0]), 1))
         rt_q.append(event_ms(torch, stream, lambda: lq.quantize(ssm, sets[0]), 1))
     bytes_step = sum(kda_step_bytes(B, HV, K, V, R, h) for h in range(L)) / L
+    # a pure loader of the same traffic (per (row, head) the step's mean bytes, writes included, as one contiguous run
+    # from the head's 64 KiB block; two heads per 256-thread workgroup; the same rotated sets)
+    blk = ssm.stride(1) * 4
+    per_head = (int(bytes_step) // (B * HV) + 15) // 16 * 16
+    sink = torch.empty(B * HV * 256, dtype=torch.int32, device=dev)
+    bases = [ssm.data_ptr() + (1 + B * kk) * HV * blk for kk in range(NSET)]
+    loader_us = min(probe_read_us(torch, stream, capture, bases, blk, per_head, B * HV, 2, nt, sink) for nt in (0, 1))
     res = {"workload": "KDA decode, BASELINE config 2: B=128, HV=H=32, d=128, W=64, R=4, int8 state, %d rotated slot "
                        "sets" % NSET,
            "decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
            "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1), "step_bytes_per_launch": int(bytes_step),
+           "loader_us": round(loader_us, 3), "loader_gbps": round(bytes_step / (loader_us * 1e-6) / 1e9, 1),
            "flush_due_us": round(flush_us, 2),
            "prefill_dequant_us": round(sum(rt_d[1:]) / 2 * 1e3, 1),
            "prefill_checkpoint_us": round(sum(rt_q[1:]) / 2 * 1e3, 1)}
@@ -174,7 +182,8 @@ def head_dims_bench(torch, dev, stream, capture):
     """GDN head-dim variants (K, V) = (64, 128), (64, 64) (reference kernels.py:62-65) at config 1's batch and heads
     (B = 64, HV = 32, H = 16) and the reference's window for these shapes, W = 16 (R = 4), int8 state, 4 rotated slot
     sets.  Per shape: the amortised decode call (step + flush), the step alone (mean over h = 0..15) with its
-    algorithmic GB/s, the flush with every head of a set due, and the standalone quantize of a set's fp32 states."""
+    algorithmic GB/s, a pure streaming loader of the same bytes (the latency-and-launch ceiling of a one-round kernel
+    of this size), the flush with every head of a set due, and the standalone quantize of a set's fp32 states."""
     from leapquant_amd.state import LeapQuantState
     B, HV, H, L, R, NSET = 64, 32, 16, 16, 4, 4
     NS = B * NSET + 1
@@ -236,6 +245,15 @@ def head_dims_bench(torch, dev, stream, capture):
         step_us = sum(st_ms[1:]) / len(st_ms[1:]) * 1e3 / CH
         flush_us = sum(fl_ms[NSET:]) / len(fl_ms[NSET:]) * 1e3
         bytes_step = sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L)) / L
+        # a pure loader of the same traffic at this shape: per (row, value head), as many bytes as the step moves per
+        # head (its mean over the window, writes included), read as one contiguous run from the head's checkpoint
+        # block, two heads per 256-thread workgroup, over the same rotated sets; the faster of plain / non-temporal
+        blk = ssm.stride(1) * 4
+        per_head = (int(bytes_step) // (B * HV) + 15) // 16 * 16
+        sink = torch.empty(B * HV * 256, dtype=torch.int32, device=dev)
+        bases = [ssm.data_ptr() + (1 + B * kk) * HV * blk for kk in range(NSET)]
+        loader_us = min(probe_read_us(torch, stream, capture, bases, blk, per_head, B * HV, 2, nt, sink)
+                        for nt in (0, 1))
         # the standalone quantize of one set's fp32 states (B x HV heads), sets rotated
         q_ms = []
         for r in range(2 * NSET):
@@ -246,7 +264,10 @@ def head_dims_bench(torch, dev, stream, capture):
         qbytes = B * HV * (V * K * 4 + V * K + 4 * (K + V) + 2 * R * (K + V))
         res["K%d_V%d" % (K, V)] = {"decode_us": round(decode_us, 3), "step_us": round(step_us, 3),
                                    "step_gbps": round(bytes_step / (step_us * 1e-6) / 1e9, 1),
-                                   "step_bytes_per_launch": int(bytes_step), "flush_due_us": round(flush_us, 2),
+                                   "step_bytes_per_launch": int(bytes_step),
+                                   "loader_us": round(loader_us, 3),
+                                   "loader_gbps": round(bytes_step / (loader_us * 1e-6) / 1e9, 1),
+                                   "flush_due_us": round(flush_us, 2),
                                    "quantize_us": round(quant_us, 2),
                                    "quantize_gbps": round(qbytes / (quant_us * 1e-6) / 1e9, 1)}
         del gdec, gst, gfl, lq, ssm
@@ -330,6 +351,37 @@ def flush_quantize_bench(torch, dev, stream):
     return res
 
 
+def probe_read_us(torch, stream, capture, bases, stride, nbytes, nblk, per_wg, nt, sink):
+    """µs per launch of leapquant_amd/_build/liblq_probe.so's streaming read: bytes [0, nbytes) of nblk blocks
+    `stride` apart from bases[i % len(bases)] (launch i), per_wg blocks per 256-thread workgroup, plain (nt = 0) or
+    non-temporal 16-byte loads; graphs of 64 launches, HIP events over whole rotations of the bases."""
+    import ctypes
+    probe = ctypes.CDLL(os.path.join(ROOT, "leapquant_amd", "_build", "liblq_probe.so"))
+    probe.lq_probe_read.restype = ctypes.c_int
+    probe.lq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+    NSET = len(bases)
+
+    def launch(i):
+        rc = probe.lq_probe_read(ctypes.c_void_p(bases[i % NSET]), stride, nbytes, nblk, per_wg, nt,
+                                 ctypes.c_void_p(sink.data_ptr()),
+                                 ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        if rc:
+            raise RuntimeError("lq_probe_read failed (%d)" % rc)
+    gr = capture(launch, 64)
+    gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = NSET // 2 if NSET >= 2 else 1
+    with torch.cuda.stream(stream):
+        e0.record(stream)
+        for _ in range(reps):
+            gr.replay()
+        e1.record(stream)
+    e1.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (64 * reps)
+
+
 def loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture):
     """What the memory system delivers to a pure streaming read of the step's own byte pattern, over the same rotated
     slot sets: leapquant_amd/_build/liblq_probe.so reads, per (row, value head) block of 64 KiB, the checkpoint bytes
@@ -337,11 +389,6 @@ def loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture):
     as the step's workgroups take them; the same bytes contiguous; and whole 64 KiB blocks -- each with plain and with
     non-temporal 16-byte loads, in graphs of 64 launches (set i % NSET).  Also the fixed cost of a launch in a graph (one
     empty workgroup)."""
-    import ctypes
-    probe = ctypes.CDLL(os.path.join(ROOT, "leapquant_amd", "_build", "liblq_probe.so"))
-    probe.lq_probe_read.restype = ctypes.c_int
-    probe.lq_probe_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int, ctypes.c_int,
-                                    ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
     blk = ssm.stride(1) * 4                                       # bytes per (slot, head) block
     nblk = B * HV
     ck = 128 * 128 + 4 * (128 + 128) + 2 * R * (128 + 128)       # codes, Sk | Sv, UQ: 19456 bytes at R = 4
@@ -349,24 +396,7 @@ def loader_ceiling(torch, dev, stream, ssm, B, HV, NSET, R, capture):
     base = [ssm.data_ptr() + (1 + B * k) * HV * blk for k in range(NSET)]
 
     def run(stride, nbytes, nb, nt):
-        def launch(i):
-            rc = probe.lq_probe_read(ctypes.c_void_p(base[i % NSET]), stride, nbytes, nb, 2, nt,
-                                     ctypes.c_void_p(sink.data_ptr()),
-                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
-            if rc:
-                raise RuntimeError("lq_probe_read failed (%d)" % rc)
-        gr = capture(launch, 64)
-        gr.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        reps = NSET // 2 if NSET >= 2 else 1
-        with torch.cuda.stream(stream):
-            e0.record(stream)
-            for _ in range(reps):
-                gr.replay()
-            e1.record(stream)
-        e1.synchronize()
-        return e0.elapsed_time(e1) * 1e3 / (64 * reps)
+        return probe_read_us(torch, stream, capture, base, stride, nbytes, nb, 2, nt, sink)
 
     out = {"workload": "pure streaming reads over config 1's rotated slot sets (%d sets): per (row, value head) "
                        "block of %d bytes, two blocks per 256-thread workgroup" % (NSET, blk)}
