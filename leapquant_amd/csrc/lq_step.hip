@@ -524,8 +524,11 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 // KDA step  (kernels.py:694-1075): per-channel gate; decayed buffered keys; pc folded into the checkpoint operands.
 //
 // One workgroup of two waves per (row n, value head hv); wave wi owns tile rows 64 wi .. 64 wi + 63.  The window --
-// values u_j, keys K_j of the key head and the per-entry step decays e_j -- reaches LDS by direct global -> LDS loads
-// issued before the int8 tile, so the decay scan, the key dots and A4 / A5 run while the tile streams.
+// values u_j and keys K_j of the key head in registers, the per-entry step decays e_j in LDS by direct global -> LDS
+// loads -- is taken in chunks of up to KCH = 32 entries, newest first (the decay scan runs from the newest entry
+// back), so that one chunk is held at a time: 17.7 KiB of LDS and <= 128 VGPRs, eight workgroups per CU (the whole
+// window at once needs 26 KiB and 148 VGPRs: six, and the step is bound by the workgroups in flight).  The first
+// chunk's loads precede the int8 tile's, so the first scan, the key dots and A4 / A5 run while the tile streams.
 //   * gate (kernels.py:704-712, 802, 887-896): g = glb sigmoid(e^A_log (a + dt_bias)) (glb != 0) or
 //     -e^A_log softplus(a + dt_bias); gn = P + g, pc = exp(gn), en = exp(g);
 //   * m = deq(Sq) diag(pc) kn, y = deq(Sq) diag(pc) qn: int8 MFMA against kf = kn Sk pc / 127, qf = qn Sk pc / 127 as
@@ -535,12 +538,15 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 //   * dU_r = U^T_r (pc kn), dQ_r = U^T_r (pc qn) on fp16 MFMA (kernels.py:1036-1047);
 //   * u = beta (v - (m + A6 + A4)), y = y_q + A7 + A5 + kappa u (kernels.py:1065-1066).
 // ------------------------------------------------------------------------------------------------------------------
+constexpr int KCH = 32;             // window entries per chunk
+
 struct KdaShared {
-  f16_t gk[LMAX][KD];       // window step decays e_j; the scan overwrites entry j with the decayed key K~_j (bf16)
-  float2 part[2][VD];       // per wave: (A4, A5) sums of row v over the wave's window entries
+  f16_t gk[KCH][KD];        // a chunk's step decays e_j (row j - cb); the scan overwrites them with K~_j (bf16)
+  float2 part[2][VD];       // per wave: (A4, A5) sums of row v over the wave's entries of every chunk
   float2 mq[VD];            // GEMV rows (k, q) in digit units
-  float2 cwq[LMAX];         // (w_j dk_j, w_j dq_j)
-  float2 dhand[KD / 2];     // running decay product after wave 1's entries, channel pairs (2 p, 2 p + 1)
+  float2 cwq[KCH];          // (w_j dk_j, w_j dq_j) of the chunk's entries
+  float2 dhand[KD / 2];     // running decay product handed on (wave 1 -> wave 0 -> the next chunk's wave 1), channel
+                            // pairs (2 p, 2 p + 1)
   int8_t dig[6][KD];        // int8 GEMV B operand: k digits 0-2, q digits 0-2
   bf16_t bkq[6][KD];        // key-dot B operand: bf16 hi / mid / lo of kn, then of qn
   f16_t hkq[4][KD];         // factor-dot B operand: fp16 hi / lo of 64 pc kn, then of 64 pc qn
@@ -556,22 +562,22 @@ __device__ __forceinline__ float kda_gate(float a, float dt, float ea, float glb
   return glb != 0.f ? glb / (1.0f + expf(-ea * xg)) : -ea * softplus20f(xg);
 }
 
-// Decayed keys K~_j = bf16(K_j dcur), dcur *= e_j, backwards over rows jb + cnt - 1 .. jb of the window (kernels.py:
-// 966-979), for the lane's channel pair (2 lane, 2 lane + 1): raw keys from registers, decays read from LDS and
-// overwritten in place by K~.  8 rows per pass, the pass's LDS reads first.
-__device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr)[32], int jb, int cnt, int lane,
+// Decayed keys K~_j = bf16(K_j dcur), dcur *= e_j, backwards over a wave's cnt <= 16 entries of a chunk, LDS rows
+// gb + cnt - 1 .. gb (kernels.py:966-979), for the lane's channel pair (2 lane, 2 lane + 1): raw keys from registers,
+// decays read from LDS and overwritten in place by K~.  8 rows per pass, the pass's LDS reads first.
+__device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr)[16], int gb, int cnt, int lane,
                                               float& d0, float& d1) {
 #pragma unroll
-  for (int g8 = 3; g8 >= 0; --g8) {
+  for (int g8 = 1; g8 >= 0; --g8) {
     if (8 * g8 < cnt) {
       uint32_t ev[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) ev[i] = *(const uint32_t*)&sh.gk[jb + 8 * g8 + i][2 * lane];
+      for (int i = 0; i < 8; ++i) ev[i] = *(const uint32_t*)&sh.gk[min(gb + 8 * g8 + i, KCH - 1)][2 * lane];
 #pragma unroll
       for (int i = 7; i >= 0; --i) {
         const int r = 8 * g8 + i;
         if (r < cnt) {
-          *(uint32_t*)&sh.gk[jb + r][2 * lane] = pk_bf16(bf_lo(kr[r]) * d0, bf_hi(kr[r]) * d1);
+          *(uint32_t*)&sh.gk[gb + r][2 * lane] = pk_bf16(bf_lo(kr[r]) * d0, bf_hi(kr[r]) * d1);
           d0 = d0 * h2f((f16_t)(ev[i] & 0xffffu));
           d1 = d1 * h2f((f16_t)(ev[i] >> 16));
         }
@@ -580,7 +586,19 @@ __device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr
   }
 }
 
-__global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io io, float glb, int* dlist) {
+// chunk k of a window of h entries (k = 0 the newest): entries [cb, ce), ce = h - KCH k, cb = max(ce - KCH, 0); wave 0
+// takes [cb, cb + c0), wave 1 [cb + c0, ce), c0 a multiple of 4 (or the whole chunk), each at most 16 entries
+struct KdaChunk {
+  int cb, jb, cnt;          // chunk start; this wave's first entry and entry count
+};
+__device__ __forceinline__ KdaChunk kda_chunk(int h, int k, int wi) {
+  const int ce = h - KCH * k, cb = max(ce - KCH, 0), c = ce - cb;
+  const int c0 = min(c, 4 * ((c + 7) >> 3));
+  return KdaChunk{cb, wi ? cb + c0 : cb, wi ? c - c0 : c0};
+}
+
+__global__ __launch_bounds__(128) __attribute__((amdgpu_waves_per_eu(4)))
+void kda_step_kernel(lq_state st, lq_step_io io, float glb, int* dlist) {
   __shared__ KdaShared sh;
   const int H = st.H, HV = st.HV, L = st.L, R = st.R;
   const int G = HV / H;
@@ -633,34 +651,34 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
   }
   // the four factor rows (2 KiB, inside the checkpoint block whatever R) to LDS, one KiB per wave
   lds_load16((const char*)UQp + 1024 * wi + 16 * lane, (char*)&sh.uq[2 * wi][0]);
-  // The window's live entries j < h split between the waves: wave 0 takes [0, h0), wave 1 [h0, h), h0 a multiple of 4
-  // (or h), each at most 32 entries.  Each wave's decays go straight to its own LDS rows (1 KiB = 4 rows per wave
-  // instruction, rows past the buffer's last re-reading it); its values u_j and keys K_j go to registers, a channel
-  // pair (2 lane, 2 lane + 1) per lane and row.  Then the int8 tile.
-  const int h0 = min(h, 4 * ((h + 7) >> 3));
-  const int jb = wi ? h0 : 0, cnt = wi ? h - h0 : h0;
-  uint32_t ur[32], kr[32];
-  {
-    const char* gg = (const char*)((const f16_t*)st.Gbuf + sh_ * L * KD);
-    for (int r = 0; r < cnt; r += 4) {
-      const int row = min(jb + r + q4, L - 1);
-      lds_load16(gg + row * (KD * 2) + 16 * n16, (char*)&sh.gk[jb + r][0]);
+  // The window's live entries j < h, chunk by chunk (kda_chunk).  Each wave's decays go straight to its own LDS rows
+  // (1 KiB = 4 rows per wave instruction, rows past the buffer's last re-reading it); its values u_j and keys K_j go
+  // to registers, a channel pair (2 lane, 2 lane + 1) per lane and row.  The first chunk, then the int8 tile.
+  const int nck = (h + KCH - 1) / KCH;
+  uint32_t ur[16], kr[16];
+  const char* gg = (const char*)((const f16_t*)st.Gbuf + sh_ * L * KD);
+  const uint32_t* ug = (const uint32_t*)((const bf16_t*)st.Ubuf + sh_ * L * VD) + lane;
+  const uint32_t* kg = (const uint32_t*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD) + lane;
+  auto load_chunk = [&](const KdaChunk& c) {
+    for (int r = 0; r < c.cnt; r += 4) {
+      const int row = min(c.jb + r + q4, L - 1);
+      lds_load16(gg + row * (KD * 2) + 16 * n16, (char*)&sh.gk[c.jb - c.cb + r][0]);
     }
-    const uint32_t* ug = (const uint32_t*)((const bf16_t*)st.Ubuf + sh_ * L * VD) + lane;
-    const uint32_t* kg = (const uint32_t*)((const bf16_t*)st.Kbuf + ((long long)slot * H + hk) * L * KD) + lane;
 #pragma unroll
-    for (int g4 = 0; g4 < 8; ++g4)
-      if (4 * g4 < cnt) {
+    for (int g4 = 0; g4 < 4; ++g4)
+      if (4 * g4 < c.cnt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) ur[4 * g4 + i] = ld_once(ug + (jb + min(4 * g4 + i, cnt - 1)) * (VD / 2));
+        for (int i = 0; i < 4; ++i) ur[4 * g4 + i] = ld_once(ug + (c.jb + min(4 * g4 + i, c.cnt - 1)) * (VD / 2));
       }
 #pragma unroll
-    for (int g4 = 0; g4 < 8; ++g4)
-      if (4 * g4 < cnt) {
+    for (int g4 = 0; g4 < 4; ++g4)
+      if (4 * g4 < c.cnt) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) kr[4 * g4 + i] = ld_once(kg + (jb + min(4 * g4 + i, cnt - 1)) * (KD / 2));
+        for (int i = 0; i < 4; ++i) kr[4 * g4 + i] = ld_once(kg + (c.jb + min(4 * g4 + i, c.cnt - 1)) * (KD / 2));
       }
-  }
+  };
+  KdaChunk ck = kda_chunk(h, 0, wi);                  // h = 0: no entries
+  load_chunk(ck);
   __builtin_amdgcn_sched_barrier(0);
   i32x4 afr[4][2];
   {
@@ -670,11 +688,11 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) afr[rt][ks] = ld_once((const i32x4*)(rp + 16 * rt * KD + 64 * ks));
   }
-  constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the window's loads: the tile
+  constexpr int AFTER_WINDOW = 8;   // vector memory operations issued after the first chunk's loads: the tile
   __builtin_amdgcn_sched_barrier(0);
   const float ea = expf(alog);
 
-  // ---- wave 0: per-channel gate, norms, digits, dot operands.  wave 1: its own entries' decayed keys ----
+  // ---- wave 0: per-channel gate, norms, digits, dot operands.  wave 1: its own entries' decayed keys (chunk 0) ----
   float gnv[2] = {0.f, 0.f}, env[2] = {0.f, 0.f};
   if (wi == 0) {
     const float beta = beta_f(bf2f(braw));
@@ -741,14 +759,15 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
     float d0 = expf(kda_gate(bf2f(axr[0]), dtx[0], ea, glb));
     float d1 = expf(kda_gate(bf2f(axr[1]), dtx[1], ea, glb));
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");   // own decay rows in LDS, keys in registers
-    kda_scan_rows(sh, kr, jb, cnt, lane, d0, d1);
+    kda_scan_rows(sh, kr, ck.jb - ck.cb, ck.cnt, lane, d0, d1);
     sh.dhand[lane] = make_float2(d0, d1);
   }
   __syncthreads();              // gate, digits, dot operands, w_j, factor rows; wave 1's decayed keys and hand-over
 
   if (wi == 0) {
     float2 d = sh.dhand[lane];
-    kda_scan_rows(sh, kr, jb, cnt, lane, d.x, d.y);
+    kda_scan_rows(sh, kr, ck.jb - ck.cb, ck.cnt, lane, d.x, d.y);
+    sh.dhand[lane] = d;         // where the next chunk's wave 1 continues (read after the next barrier)
   } else {
     // ---- factor dots: U^T rows against fp16 (hi, lo) of 64 pc kn (columns 0, 1) and 64 pc qn (2, 3) ----
     f16x8 bh[4], ufr[4];        // ufr: A fragment row m = r (U^T_r, fp16)
@@ -770,7 +789,7 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       if ((n16 == 0 || n16 == 2) && r < R) ((float*)&sh.duq[r])[n16 >> 1] = s;
     }
   }
-  // ---- decayed-key dots of this wave's entries, 16-row tiles from jb (rows past the wave's own are not kept) ----
+  // ---- decayed-key dots and A4 / A5 of this wave's entries of a chunk ----
   bf16x8 bk[4];                 // B operand: columns 0-2 hi / mid / lo of kn, 4-6 of qn
   {
     const bool bcol = (n16 & 3) < 3 && n16 < 8;
@@ -781,34 +800,36 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
       bk[ks] = bcol ? b : bf16x8{};
     }
   }
-  for (int j0 = jb; j0 < jb + cnt; j0 += 16) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  float a40 = 0.f, a50 = 0.f, a41 = 0.f, a51 = 0.f;   // A4 / A5 of rows v = 2 lane, 2 lane + 1, over the wave's entries
+  auto chunk_dots = [&](const KdaChunk& c) {
+    // key dots: one 16-row tile of the chunk's LDS rows from the wave's first (rows past its own are not kept)
+    const int gb = c.jb - c.cb;
+    if (c.cnt > 0) {
+      f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const bf16x8 a = *(const bf16x8*)((const bf16_t*)&sh.gk[j0 + n16][0] + 32 * ks + 8 * q4);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bk[ks], acc, 0, 0, 0);
+      for (int ks = 0; ks < 4; ++ks) {
+        const bf16x8 a = *(const bf16x8*)((const bf16_t*)&sh.gk[gb + n16][0] + 32 * ks + 8 * q4);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, bk[ks], acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
+        const int jj = 4 * q4 + i;
+        if ((n16 == 0 || n16 == 4) && jj < c.cnt) ((float*)&sh.cwq[gb + jj])[n16 >> 2] = sh.w[c.jb + jj] * s;
+      }
     }
+    __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's own cwq rows: LDS round trip within the wave
+    // A4 / A5 over the wave's entries of the chunk, in the order of j
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float s = acc[i] + quad_bcast<1>(acc[i]) + quad_bcast<2>(acc[i]);   // hi + mid + lo (lanes 0 / 4)
-      const int j = j0 + 4 * q4 + i;
-      if ((n16 == 0 || n16 == 4) && j < jb + cnt) ((float*)&sh.cwq[j])[n16 >> 2] = sh.w[j] * s;
-    }
-  }
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);   // the wave's own cwq rows: LDS round trip within the wave
-  // ---- A4 / A5 over this wave's entries for rows v = 2 lane, 2 lane + 1, in the order of j ----
-  {
-    float a40 = 0.f, a50 = 0.f, a41 = 0.f, a51 = 0.f;
-#pragma unroll
-    for (int g8 = 0; g8 < 4; ++g8) {
-      if (8 * g8 < cnt) {
+    for (int g8 = 0; g8 < 2; ++g8) {
+      if (8 * g8 < c.cnt) {
         float2 cc[8];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) cc[i] = sh.cwq[min(jb + 8 * g8 + i, LMAX - 1)];
+        for (int i = 0; i < 8; ++i) cc[i] = sh.cwq[min(gb + 8 * g8 + i, KCH - 1)];
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
           const int r = 8 * g8 + i;
-          if (r < cnt) {
+          if (r < c.cnt) {
             const float u0 = bf_lo(ur[r]), u1 = bf_hi(ur[r]);
             a40 = fmaf(u0, cc[i].x, a40); a50 = fmaf(u0, cc[i].y, a50);
             a41 = fmaf(u1, cc[i].x, a41); a51 = fmaf(u1, cc[i].y, a51);
@@ -816,8 +837,29 @@ __global__ __launch_bounds__(128) void kda_step_kernel(lq_state st, lq_step_io i
         }
       }
     }
-    *(float4*)&sh.part[wi][2 * lane] = make_float4(a40, a50, a41, a51);
+  };
+  chunk_dots(ck);
+  // ---- older chunks: each wave loads its entries once every wave is done with the previous chunk's rows; wave 1
+  //      continues the product wave 0 reached, wave 0 the one wave 1 reaches ----
+  for (int k = 1; k < nck; ++k) {
+    __syncthreads();            // the previous chunk's decayed keys and cwq are read; wave 0's product is in dhand
+    ck = kda_chunk(h, k, wi);
+    load_chunk(ck);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this chunk's decay rows in LDS (keys and values with them)
+    if (wi == 1) {
+      float2 d = sh.dhand[lane];
+      kda_scan_rows(sh, kr, ck.jb - ck.cb, ck.cnt, lane, d.x, d.y);
+      sh.dhand[lane] = d;
+    }
+    __syncthreads();            // wave 1's decayed keys and hand-over
+    if (wi == 0) {
+      float2 d = sh.dhand[lane];
+      kda_scan_rows(sh, kr, ck.jb - ck.cb, ck.cnt, lane, d.x, d.y);
+      sh.dhand[lane] = d;
+    }
+    chunk_dots(ck);
   }
+  *(float4*)&sh.part[wi][2 * lane] = make_float4(a40, a50, a41, a51);
   {
     i32x4 bfr[2];
     const int drow = (n16 & 3) * 3 + (n16 >> 2);
