@@ -650,6 +650,46 @@ def main():
     decode_gbps = timed_bytes / (ms_total * 1e-3) / 1e9
     progress("decode loop: %.3f us per call over %d calls (%d whole rotations of %d sets)"
              % (us_per_step, calls, timed_rot, NSET))
+    # ---- staggered windows (beside the BASELINE workload, not it): row n of every set starts at fill n % 64, so on
+    # every call one row per set fills its window and is flushed, as in serving, where rows reach their flush at
+    # different calls; the same decode graph over whole rotations ----
+    fill0 = (torch.arange(B, device=dev, dtype=torch.int32) % L)[:, None].expand(B, HV)
+    for kk in range(NSET):
+        lq.hcnt[sets[kk].long()] = fill0
+    torch.cuda.synchronize()
+    s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for _ in range(NSET):
+        gdec.replay()
+    with torch.cuda.stream(stream):
+        s0.record(stream)
+        for _ in range(NSET):
+            gdec.replay()
+        s1.record(stream)
+    s1.synchronize()
+    staggered_us = s0.elapsed_time(s1) * 1e3 / ROT
+    # the same with the step and the flush as two launches (lq_gdn_step, then lq_flush of the call's rows: every due
+    # head its own workgroup), for comparison
+    lq.quantize(ssm, all_slots)
+    for kk in range(NSET):
+        lq.hcnt[sets[kk].long()] = fill0
+
+    def step_then_flush(i):
+        step_only(i, i % NSET)
+        flush_only(i % NSET)
+    gsf = capture(step_then_flush, CH)
+    torch.cuda.synchronize()
+    for _ in range(NSET):
+        gsf.replay()
+    with torch.cuda.stream(stream):
+        s0.record(stream)
+        for _ in range(NSET):
+            gsf.replay()
+        s1.record(stream)
+    s1.synchronize()
+    staggered_two_us = s0.elapsed_time(s1) * 1e3 / ROT
+    del gsf
+    progress("decode loop, staggered windows: %.3f us per call (step + flush launches: %.3f)"
+             % (staggered_us, staggered_two_us))
     # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
     # of the NSET sets 64 / NSET steps; NSET replays take every window from h = 0 to h = 64, then every head is due) ----
     lq.quantize(ssm, all_slots)                                   # every window back to h = 0
@@ -803,6 +843,10 @@ def main():
                           "kernel": STEP_KERNEL, "bytes_per_launch": int(bytes_step)},
         # the standalone flush kernel (lq_flush: the KDA path, the other head shapes, the reference-API factories)
         "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
+        "decode_staggered_us": round(staggered_us, 3),
+        "decode_staggered_two_launch_us": round(staggered_two_us, 3),
+        "decode_staggered_note": "not the BASELINE workload: row n starts at window fill n % 64, so on every call one "
+                                 "row per set is flushed (rows reach their flush at different calls, as in serving)",
     }
     res["conv_fused_config1"] = {
         "workload": "config 1 step with vLLM's causal_conv1d_update (width 4, SiLU, bf16 state [NS, C, 3]) fused in, "
