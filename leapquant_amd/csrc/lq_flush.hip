@@ -1318,7 +1318,7 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   const float* Sk = (const float*)(base + V_ * K_);
   const float* Sv = Sk + K_;
   const f16_t* UQ = (const f16_t*)(Sv + V_);
-  const int h = min(st.hcnt[sh_], L);
+  const int h = __builtin_amdgcn_readfirstlane(min(st.hcnt[sh_], L));   // uniform: one word per head
   const float P = st.Pbuf[sh_];
   const int LP = h > 0 ? ((h + 31) & ~31) : 32;
   const int cv = tid & 127;
@@ -1334,8 +1334,10 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     uqv[a] = (cok && a < R) ? x : 0.f;
   }
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  // an empty window (h == 0, uniform: the prefill of a slot just checkpointed) skips the window's loads, staging and
+  // products
   WinRegs win;
-  load_window<false, K_, V_>(win, st, slot, hv, h, LP);
+  if (h > 0) load_window<false, K_, V_>(win, st, slot, hv, h, LP);
   uint32_t wds[8];
   load_code_words<K_, V_>(wds, Sq);
   if (tid < KD + VD) {
@@ -1350,7 +1352,7 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   }
   if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
   __syncthreads();
-  store_window<false>(sh, win, h, LP);
+  if (h > 0) store_window<false>(sh, win, h, LP);
   Tile t;
   {
     const float inv = 1.0f / qmax;
@@ -1376,9 +1378,11 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
       }
     }
   }
-  __syncthreads();
-  rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
-  rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+  if (h > 0) {
+    __syncthreads();
+    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
+  }
   __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
   float* S = (float*)base;
 #pragma unroll

@@ -40,6 +40,37 @@ __device__ __forceinline__ f16x4 to_h4(f32x4 x) {
   return f16x4{(_Float16)x[0], (_Float16)x[1], (_Float16)x[2], (_Float16)x[3]};
 }
 __device__ __forceinline__ f32x4 from_h4(f16x4 x) { return f32x4{(float)x[0], (float)x[1], (float)x[2], (float)x[3]}; }
+// Mixed-precision VALU forms (v_fma_mix_f32: an fp16 half of a packed word widened exactly, one fp32 rounding).
+// hmul<H>(x, s) = fp32(half H of x) * s, rounded once: the product of cvt + mul (a zero result may be +0 where the
+// two-instruction form gives -0).  habs_add<H>(x, acc) = acc + |fp32(half H of x)|, rounded once, as cvt + add.
+// The compiler forms neither by itself (it widens with v_cvt_f32_f16 first), so each is one instruction here.
+template <int H>
+__device__ __forceinline__ float hmul(uint32_t x, float s) {
+  float r;
+  if constexpr (H == 0) asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s));
+  else asm("v_fma_mix_f32 %0, %1, %2, 0 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(s));
+  return r;
+}
+template <int H>
+__device__ __forceinline__ float habs_add(uint32_t x, float acc) {
+  float r;
+  if constexpr (H == 0) asm("v_fma_mix_f32 %0, |%1|, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(acc));
+  else asm("v_fma_mix_f32 %0, |%1|, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(x), "v"(acc));
+  return r;
+}
+// the two 32-bit words of a packed f16x4 (halves 0, 1 and 2, 3)
+__device__ __forceinline__ uint2 h4_words(f16x4 x) { return __builtin_bit_cast(uint2, x); }
+// element i of a packed f16x4 times s (one rounding), and acc + |element i|
+template <int I>
+__device__ __forceinline__ float h4mul(f16x4 x, float s) {
+  const uint2 w = h4_words(x);
+  return hmul<I & 1>(I < 2 ? w.x : w.y, s);
+}
+template <int I>
+__device__ __forceinline__ float h4abs_add(f16x4 x, float acc) {
+  const uint2 w = h4_words(x);
+  return habs_add<I & 1>(I < 2 ? w.x : w.y, acc);
+}
 // The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
 // redo the conversion where the value is used (twice the registers).
 __device__ __forceinline__ f16x4 pinned(f16x4 x) {
@@ -1281,7 +1312,8 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   p_step4(sh, bh, pn, R, u16);                        // U16 = P step with Q16 (lanes < 16)
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
-  Tile4 t;
+  // E is kept packed (fp16, in B's registers: B is dead after the U step); the products B / pn, E rsk and the |E| sums
+  // take its halves through v_fma_mix_f32, each the single rounding of the widen-then-operate form.
   {
     const f16x4 z4 = {};
     f16x4 auo[2], aun[2];
@@ -1297,12 +1329,12 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
       const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                               // B[r][v] = Q16^T
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
-        f32x4 e = from_h4(bh[g][nt]) * rpn;
+        const f16x4 b = bh[g][nt];
+        f32x4 e = {h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
         e = mma16(auo[g], bqo, e);
         e *= pn;
         e = mma16(aun[g], bqn, e);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) t.a[g][nt][i] = hround(e[i]);
+        bh[g][nt] = to_h4(e);                                                       // E, fp16
       }
     }
   }
@@ -1311,14 +1343,18 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   float rsk[2][4];
 #pragma unroll
   for (int g = 0; g < 2; ++g) {
-    float cs[4];
+    float cs[4], x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float x = 0.f;
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[g][nt][i]);
-      cs[i] = sum16(x);
+    for (int nt = 0; nt < 8; ++nt) {
+      x0 = h4abs_add<0>(bh[g][nt], x0);
+      x1 = h4abs_add<1>(bh[g][nt], x1);
+      x2 = h4abs_add<2>(bh[g][nt], x2);
+      x3 = h4abs_add<3>(bh[g][nt], x3);
     }
+    cs[0] = sum16(x0);
+    cs[1] = sum16(x1);
+    cs[2] = sum16(x2);
+    cs[3] = sum16(x3);
     // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
     const int ic = l & 3;
     const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
@@ -1334,16 +1370,18 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   int next = 0;                                       // dynamic schedule: this workgroup's next candidate
   if (sched && tid == 0) next = sched_next(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+  Tile4 t;                                            // E rsk, fp32
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
+    for (int g = 0; g < 2; ++g) {
+      const f16x4 e = bh[g][nt];
+      t.a[g][nt] = f32x4{h4mul<0>(e, rsk[g][0]), h4mul<1>(e, rsk[g][1]), h4mul<2>(e, rsk[g][2]),
+                         h4mul<3>(e, rsk[g][3])};
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        t.a[g][nt][i] *= rsk[g][i];
-        m = fmaxf(m, fabsf(t.a[g][nt][i]));
-      }
+      for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[g][nt][i]));
+    }
     sh.r.rmx[4 * w + q][16 * nt + l16] = m;
   }
   __syncthreads();
