@@ -28,6 +28,13 @@ __device__ __forceinline__ bf16_t f2bf(float f) { return __builtin_bit_cast(bf16
 __device__ __forceinline__ uint32_t pk_bf16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, lq_bf16x2{(__bf16)lo, (__bf16)hi});
 }
+// the same, the word kept as computed: a half of it read back (bf_lo / bf_hi) then costs one shift or mask, where the
+// compiler would otherwise convert that value again on its own
+__device__ __forceinline__ uint32_t pk_bf16_kept(float lo, float hi) {
+  uint32_t w = pk_bf16(lo, hi);
+  asm("" : "+v"(w));
+  return w;
+}
 // bf16 halves of a word as fp32
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }

@@ -241,7 +241,7 @@ __device__ __forceinline__ void store_half64(FlushShared64& sh, const WinHalf& r
     if (c8 < K64) *(uint32_t*)&sh.op.k[c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
     const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
     const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
-    const uint32_t hi = pk_bf16(wu0, wu1);
+    const uint32_t hi = pk_bf16_kept(wu0, wu1);
     *(uint32_t*)&sh.op.u[0][c8 + e][jl] = hi;
     *(uint32_t*)&sh.op.u[1][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
   }

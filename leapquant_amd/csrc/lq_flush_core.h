@@ -434,7 +434,7 @@ __device__ __forceinline__ void store_window(SH& sh, const WinRegs& r, int h, in
 #pragma clang fp contract(off)
       const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
       const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
-      const uint32_t hi = pk_bf16(wu0, wu1);
+      const uint32_t hi = pk_bf16_kept(wu0, wu1);
       *o1 = hi;
       *o2 = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
     } else {
@@ -999,7 +999,7 @@ __device__ __forceinline__ void store_half(FlushShared4& sh, const WinHalf& r, i
     *(uint32_t*)&sh.op[0][c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
     const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
     const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
-    const uint32_t hi = pk_bf16(wu0, wu1);
+    const uint32_t hi = pk_bf16_kept(wu0, wu1);
     *(uint32_t*)&sh.op[1][c8 + e][jl] = hi;
     *(uint32_t*)&sh.op[2][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
   }
@@ -1097,13 +1097,11 @@ __device__ __forceinline__ void tile_add_words4(Tile4& t, const uint32_t wds[2][
 // M[a][r] = sum_v Q_old[v][a] Q[v][r] (Q from sh.qT): every lane gets all 16 entries
 __device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4]) {
   const int l = lane_id(), q = l >> 4, l16 = l & 15;
-  const bool rl4 = l16 < 4;
-  const f16x8 z8 = {};
   f32x4 macc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    const f16x8 ao = rl4 ? *(const f16x8*)&sh.r.qoT[l16][32 * ks + 8 * q] : z8;
-    const f16x8 bq = rl4 ? *(const f16x8*)&sh.qT[l16][32 * ks + 8 * q] : z8;
+    const f16x8 ao = *(const f16x8*)&sh.r.qoT[l16 & 3][32 * ks + 8 * q];       // rows / columns >= 4: unused
+    const f16x8 bq = *(const f16x8*)&sh.qT[l16 & 3][32 * ks + 8 * q];
     macc = mma32(ao, bq, macc);
   }
 #pragma unroll
@@ -1118,8 +1116,6 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4
 __device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], float pn, int R,
                                         f32x4 p[2]) {
   const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
-  const bool rl4 = l16 < 4;
-  const f16x4 z4 = {};
   float M[4][4];
   gram_qold_q(sh, M);
   f16x4 ident;
@@ -1128,7 +1124,7 @@ __device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh
   f32x4 pacc[2] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {                    // P^T[r][c] = sum_v Q^T[r][v] B[c][v] (k = v)
-    const f16x4 aq = rl4 ? *(const f16x4*)&sh.qT[l16][16 * nt + 4 * q] : z4;
+    const f16x4 aq = *(const f16x4*)&sh.qT[l16 & 3][16 * nt + 4 * q];          // rows >= 4 of P^T: unused
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       const f16x4 bt = to_h4(mma16(bh[g][nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));
@@ -1252,10 +1248,9 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   {                                                   // Q^T partial over the wave's 32 channels
-    const f16x4 z4 = {};
     f16x4 ap[2];
 #pragma unroll
-    for (int g = 0; g < 2; ++g) ap[g] = l16 < 4 ? *(const f16x4*)&sh.r.ppT[l16][32 * w + 16 * g + 4 * q] : z4;
+    for (int g = 0; g < 2; ++g) ap[g] = *(const f16x4*)&sh.r.ppT[l16 & 3][32 * w + 16 * g + 4 * q];   // rows >= 4: unused
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       f32x4 d = mma16(ap[0], bh[0][nt], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -1266,12 +1261,11 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   __syncthreads();
   if (tid < VD) {                                     // waves 0 and 1: one row v per thread
     // M2[a][r] = sum_c U_old[c][a] P16[c][r] over all 128 channels
-    const f16x8 z8 = {};
     f32x4 macc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
-      const f16x8 ao = l16 < 4 ? *(const f16x8*)&sh.r.uoT[l16][32 * ks + 8 * q] : z8;
-      const f16x8 bp = l16 < 4 ? *(const f16x8*)&sh.r.ppT[l16][32 * ks + 8 * q] : z8;
+      const f16x8 ao = *(const f16x8*)&sh.r.uoT[l16 & 3][32 * ks + 8 * q];     // rows / columns >= 4: unused
+      const f16x8 bp = *(const f16x8*)&sh.r.ppT[l16 & 3][32 * ks + 8 * q];
       macc = mma32(ao, bp, macc);
     }
     float M2[4][4];
