@@ -946,6 +946,8 @@ struct FlushShared4 {
       f16_t ppT[4][KD];        // P16^T
       f16_t uoT[4][KD];        // old U^T, fp16 (MFMA operand)
       f16_t qoT[4][VD];        // old Q^T, fp16
+      f16x4 qo16[VD];          // old Q rows [v][a], fp16 (residual B operand)
+      f16x4 qn16[VD];          // Q16 rows [v][r] (residual B operand)
     } r;
   };
   float skl[KD];               // column factor of the dequant (Sk)
@@ -1233,6 +1235,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   } else {
 #pragma unroll
     for (int a = 0; a < 4; ++a) sh.r.qoT[a][cv] = f2h(sh.qov[cv][a]);
+    sh.r.qo16[cv] = to_h4(sh.qov[cv]);
   }
   __syncthreads();
 
@@ -1299,6 +1302,8 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
     }
     sh.qv[l] = p0;
     sh.qv[l + 64] = p1;
+    sh.r.qn16[l] = to_h4(p0);
+    sh.r.qn16[l + 64] = to_h4(p1);
     __builtin_amdgcn_s_setprio(0);
   }
   __syncthreads();
@@ -1319,8 +1324,9 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + l16;
-      const f16x4 bqo = q == 0 ? to_h4(sh.qov[v]) : z4;                              // B[a][v] = Q_old^T
-      const f16x4 bqn = q == 0 ? to_h4(sh.qv[v]) : z4;                               // B[r][v] = Q16^T
+      // B[a][v] = Q_old^T, B[r][v] = Q16^T; rows a, r >= 4 (lanes q > 0) meet the zero columns of A
+      const f16x4 bqo = sh.r.qo16[v];
+      const f16x4 bqn = sh.r.qn16[v];
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         const f16x4 b = bh[g][nt];
@@ -1388,6 +1394,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
     sh.r.rq[tid] = qmax * (1.0f / rmax);
   }
   __syncthreads();
+  uint32_t cw[2][8];                                  // code words, laid out as load_code_words4 delivers them
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + l16;
@@ -1398,9 +1405,30 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
 #pragma unroll
       for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[g][nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
       const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
-      const int c = 32 * w + 16 * g + 4 * q;
-      if ((K_ == KD || c < K_) && (V_ == VD || v < V_))
-        *(uint32_t*)(Sq + v * K_ + c) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+      cw[g][nt] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    }
+  }
+  if constexpr (K_ == KD && V_ == VD) {
+    // the inverse of load_code_words4's transpose, then four 16-byte stores per lane (each wave instruction 32 rows x
+    // 32 bytes) instead of sixteen 4-byte ones
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t a0 = cw[0][2 * k], a1 = cw[1][2 * k], a2 = cw[0][2 * k + 1], a3 = cw[1][2 * k + 1];
+      swap16(a0, a1);
+      swap16(a2, a3);
+      swap32(a0, a2);
+      swap32(a1, a3);
+      *(uint4*)(Sq + (16 * (2 * k + (q >> 1)) + l16) * KD + 32 * w + 16 * (q & 1)) = make_uint4(a0, a1, a2, a3);
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int c = 32 * w + 16 * g + 4 * q;
+        if ((K_ == KD || c < K_) && (V_ == VD || v < V_)) *(uint32_t*)(Sq + v * K_ + c) = cw[g][nt];
+      }
     }
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
