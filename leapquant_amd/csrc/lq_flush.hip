@@ -911,6 +911,10 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   float* Sk = (float*)(base + V_ * K_);
   float* Sv = Sk + K_;
   f16_t* UQ = (f16_t*)(Sv + V_);
+  // codes: |x| <= qmax (1 + 2^-22) since svv is the row's largest |E rsk| (or above it), so the rounding to the nearest
+  // integer is the add of 1.5 2^23 (round to nearest even, as rintf) and the clamp to [-qmax, qmax] never binds for
+  // a finite x; the code is the low byte of the sum
+  uint32_t cw[2][8];
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
@@ -921,17 +925,39 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     const float rsv = qmax / svv;
 #pragma unroll
     for (int cg = 0; cg < 2; ++cg) {
-      uint32_t word = 0;
+      uint32_t b[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float x = (t.a[cg][nt][i] * rsk[cg][i]) * rsv;     // kernels.py:2229
-        const float cq = fminf(fmaxf(rintf(x), -qmax), qmax);
-        word |= ((uint32_t)(int)cq & 0xffu) << (8 * i);
+#pragma clang fp contract(off)
+        const float x = (t.a[cg][nt][i] * rsk[cg][i]) * rsv;     // kernels.py:2229 (rounded before the add)
+        b[i] = __float_as_uint(x + 12582912.0f);
       }
-      const int c = 32 * w + 16 * cg + 4 * q;
-      if ((V_ == VD || v < V_) && (K_ == KD || c < K_)) *(uint32_t*)(Sq + v * K_ + c) = word;
+      const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
+      cw[cg][nt] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
     if ((V_ == VD || v < V_) && w == 0 && q == 0) Sv[v] = svv;
+  }
+  if constexpr (K_ == KD && V_ == VD) {
+    // the same lane layout as the four-wave flush's tile: four 16-byte stores per lane after its transpose
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      uint32_t a0 = cw[0][2 * k], a1 = cw[1][2 * k], a2 = cw[0][2 * k + 1], a3 = cw[1][2 * k + 1];
+      swap16(a0, a1);
+      swap16(a2, a3);
+      swap32(a0, a2);
+      swap32(a1, a3);
+      *(uint4*)(Sq + (16 * (2 * k + (q >> 1)) + (l & 15)) * KD + 32 * w + 16 * (q & 1)) = make_uint4(a0, a1, a2, a3);
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + (l & 15);
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg) {
+        const int c = 32 * w + 16 * cg + 4 * q;
+        if ((V_ == VD || v < V_) && (K_ == KD || c < K_)) *(uint32_t*)(Sq + v * K_ + c) = cw[cg][nt];
+      }
+    }
   }
   if (tid < KD) {
     if (K_ == KD || tid < K_) {
