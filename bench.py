@@ -76,9 +76,12 @@ def progress(msg):
 
 
 def event_ms(torch, stream, fn, reps):
-    """Average duration of fn() (work on `stream`), from HIP events on that stream."""
+    """Average duration of fn() (work on `stream`), from HIP events on that stream.  A spin kernel (~1 ms) queued ahead
+    of the start event keeps the GPU busy while the host enqueues fn()'s launches, so that the events bracket the GPU's
+    work and not the host's launch latency (which a single eager launch would otherwise add, ~20-30 us here)."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)
         e0.record(stream)
         for _ in range(reps):
             fn()
@@ -374,6 +377,7 @@ def probe_read_us(torch, stream, capture, bases, stride, nbytes, nblk, per_wg, n
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = NSET // 2 if NSET >= 2 else 1
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         e0.record(stream)
         for _ in range(reps):
             gr.replay()
@@ -438,6 +442,7 @@ def dense_rmw_ceiling(torch, stream, Sd, B, HV, NSET, capture):
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
+            torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
             e0.record(stream)
             for _ in range(4):
                 gr.replay()
@@ -634,6 +639,7 @@ def main():
     assert int(lq.hcnt[1:].max()) == 0                           # every window back at the start of a rotation
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         e0.record(stream)
         for _ in range(timed_rot * NSET):
             gdec.replay()
@@ -661,6 +667,7 @@ def main():
     for _ in range(NSET):
         gdec.replay()
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         s0.record(stream)
         for _ in range(NSET):
             gdec.replay()
@@ -681,6 +688,7 @@ def main():
     for _ in range(NSET):
         gsf.replay()
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         s0.record(stream)
         for _ in range(NSET):
             gsf.replay()
@@ -701,6 +709,8 @@ def main():
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(NSET + 2)] for _ in range(rounds)]
     with torch.cuda.stream(stream):
         for r in range(rounds):
+            if r == 0:
+                torch.cuda._sleep(2_000_000)
             ev[r][0].record(stream)
             for _ in range(NSET):
                 gsteps.replay()
@@ -709,6 +719,7 @@ def main():
                 gflush[kk].replay()
                 ev[r][kk + 2].record(stream)
         i0, i1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         i0.record(stream)
         gidle.replay()
         i1.record(stream)
@@ -737,6 +748,7 @@ def main():
     torch.cuda.synchronize()
     d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.cuda.stream(stream):
+        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         d0.record(stream)
         for _ in range(4):
             gd.replay()
@@ -788,6 +800,7 @@ def main():
         torch.cuda.synchronize()
         c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         with torch.cuda.stream(stream):
+            torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
             c0.record(stream)
             for _ in range(NSET):                                 # every set steps h = 0 .. 63
                 gr.replay()
