@@ -71,6 +71,20 @@ __device__ __forceinline__ float h4abs_add(f16x4 x, float acc) {
   const uint2 w = h4_words(x);
   return habs_add<I & 1>(I < 2 ? w.x : w.y, acc);
 }
+// exchanges of 32-bit values between lane groups: swap32 trades the upper 32 lanes of a with the lower 32 of b,
+// swap16 the odd 16-lane rows of a with the even rows of b (gfx950 v_permlane32_swap / v_permlane16_swap).  The
+// sequence swap32(a0, a2), swap32(a1, a3), swap16(a0, a1), swap16(a2, a3) transposes four registers over the four
+// 16-lane groups: register j of group q goes to register q of group j.
+__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
+__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
+  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
+  a = r[0];
+  b = r[1];
+}
 // The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
 // redo the conversion where the value is used (twice the registers).
 __device__ __forceinline__ f16x4 pinned(f16x4 x) {
@@ -93,6 +107,8 @@ struct FlushShared {
       float rmx[4 * NW][VD];   // per-(wave, lane group) row maxima of the scaled residual
       float rq[VD];            // qmax / row scale
       f16_t ppT[RA][KD];       // P16^T
+      f16x4 qo16[NB][VD];      // old Q rows [v][a], fp16 (residual B operand)
+      f16x4 qn16[NB][VD];      // Q16 rows [v][r] (residual B operand)
     } r;
   };
   float skl[KD];               // column factor of the dequant (Sk, KDA: Sk pc)
@@ -720,6 +736,10 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
   const f32x4 p16 = p_step<RA>(sh, bt, pn, R);        // P16 rows of this wave (lanes < 16 NB)
   __syncthreads();                                    // every wave is past the rebuild: the op region is free
+  if (tid < VD) {
+#pragma unroll
+    for (int b = 0; b < NB; ++b) sh.r.qo16[b][tid] = to_h4(sh.qov[b][tid]);
+  }
   // Q = B P16 + pn Q_old (U_old^T P16): per-wave partials of B P16 over the wave's 16 channels, summed below
   if (q < NB) {
 #pragma unroll
@@ -785,6 +805,8 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
       }
       sh.qv[0][l] = p0;
       sh.qv[0][l + 64] = p1;
+      sh.r.qn16[0][l] = to_h4(p0);
+      sh.r.qn16[0][l + 64] = to_h4(p1);
     } else {
       float p0[RA], p1[RA];
 #pragma unroll
@@ -811,6 +833,8 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
         }
         sh.qv[b][l] = y0;
         sh.qv[b][l + 64] = y1;
+        sh.r.qn16[b][l] = to_h4(y0);
+        sh.r.qn16[b][l + 64] = to_h4(y1);
       }
     }
     __builtin_amdgcn_s_setprio(0);
@@ -819,7 +843,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   const f32x4 u16 = p_step<RA>(sh, bt, pn, R);        // U16 = P step with Q16 (lanes < 16 NB: rows 16 w + l)
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
-  Tile t;
+  // E kept packed in B's registers (B is dead after the Q partials), consumed through v_fma_mix_f32 as in flush_head4
   {
     const f16x4 z4 = {};
     const f16x4 auo = q < NB ? to_h4(sh.uoc[qb][16 * w + l16]) : z4;                // A[c][a] = U_old
@@ -827,29 +851,33 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
       const int v = 16 * nt + l16;
-      const f16x4 bqo = q < NB ? to_h4(sh.qov[qb][v]) : z4;                           // B[a][v] = Q_old^T
-      const f16x4 bqn = q < NB ? to_h4(sh.qv[qb][v]) : z4;                            // B[r][v] = Q16^T
-      f32x4 e = from_h4(bh[nt]);
-      if (!KDA) e *= rpn;
+      // B[a][v] = Q_old^T, B[r][v] = Q16^T; rows past the lane's factor block meet the zero columns of A
+      const f16x4 bqo = sh.r.qo16[qb][v];
+      const f16x4 bqn = sh.r.qn16[qb][v];
+      const f16x4 b = bh[nt];
+      f32x4 e = KDA ? from_h4(b) : f32x4{h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
       e = mma16(auo, bqo, e);
       if (!KDA) e *= pn;
       e = mma16(aun, bqn, e);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) t.a[nt][i] = hround(e[i]);
+      bh[nt] = to_h4(e);                                                            // E, fp16
     }
   }
 
   // ---- stage 5: column smoothing scales (kernels.py:1929-1958) ----
   float rsk[4];
   {
-    float cs[4];
+    float cs[4], x0 = 0.f, x1 = 0.f, x2 = 0.f, x3 = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float x = 0.f;
-#pragma unroll
-      for (int nt = 0; nt < 8; ++nt) x += fabsf(t.a[nt][i]);
-      cs[i] = sum16(x);
+    for (int nt = 0; nt < 8; ++nt) {
+      x0 = h4abs_add<0>(bh[nt], x0);
+      x1 = h4abs_add<1>(bh[nt], x1);
+      x2 = h4abs_add<2>(bh[nt], x2);
+      x3 = h4abs_add<3>(bh[nt], x3);
     }
+    cs[0] = sum16(x0);
+    cs[1] = sum16(x1);
+    cs[2] = sum16(x2);
+    cs[3] = sum16(x3);
     // the square root and division once per column: lane l takes column 4 q + (l & 3) of its row group
     const int ic = l & 3;
     const float msum = (ic == 0 ? cs[0] : ic == 1 ? cs[1] : ic == 2 ? cs[2] : cs[3]) * (1.0f / V_);
@@ -864,14 +892,14 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   int next = 0;                                       // dynamic schedule: this workgroup's next candidate
   if (sched && tid == 0) next = sched_next(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
+  Tile t;                                             // E rsk, fp32
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
+    const f16x4 e = bh[nt];
+    t.a[nt] = f32x4{h4mul<0>(e, rsk[0]), h4mul<1>(e, rsk[1]), h4mul<2>(e, rsk[2]), h4mul<3>(e, rsk[3])};
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      t.a[nt][i] *= rsk[i];
-      m = fmaxf(m, fabsf(t.a[nt][i]));
-    }
+    for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[nt][i]));
     sh.r.rmx[4 * w + q][16 * nt + l16] = m;
   }
   __syncthreads();
@@ -884,6 +912,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
     sh.r.rq[tid] = qmax * (1.0f / rmax);
   }
   __syncthreads();
+  uint32_t cw[8];                                     // code words of rows 16 nt + l16, channels 16 w + 4 q ..
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + l16;
@@ -892,8 +921,26 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
 #pragma unroll
     for (int i = 0; i < 4; ++i) b[i] = __float_as_uint(__builtin_fmaf(t.a[nt][i], rq, 12582912.0f));   // RNE via 1.5 2^23
     const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
-    if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_))
-      *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+    cw[nt] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+  }
+  if constexpr (K_ == KD && V_ == VD) {
+    // a 4 x 4 transpose over the lane groups (register j of group q -> register q of group j) gives lane (q, l16) the
+    // four words of row 16 (4 m + q) + l16, channels 16 w .. 16 w + 15: two 16-byte stores instead of eight 4-byte ones
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+      uint32_t a0 = cw[4 * m], a1 = cw[4 * m + 1], a2 = cw[4 * m + 2], a3 = cw[4 * m + 3];
+      swap32(a0, a2);
+      swap32(a1, a3);
+      swap16(a0, a1);
+      swap16(a2, a3);
+      *(uint4*)(Sq + (16 * (4 * m + q) + l16) * KD + 16 * w) = make_uint4(a0, a1, a2, a3);
+    }
+  } else {
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int v = 16 * nt + l16;
+      if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_)) *(uint32_t*)(Sq + v * K_ + 16 * w + 4 * q) = cw[nt];
+    }
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
   if (q < NB && (K_ == KD || 16 * w + l16 < K_)) {
@@ -1023,18 +1070,6 @@ __device__ __forceinline__ void rebuild_half4(Tile4& t, const bf16_t (*A)[OPS4],
     __builtin_amdgcn_sched_barrier(0);
   }
 }
-// exchanges of 32-bit values between lane groups: swap32 trades the upper 32 lanes of a with the lower 32 of b,
-// swap16 the odd 16-lane rows of a with the even rows of b (gfx950 v_permlane32_swap / v_permlane16_swap)
-__device__ __forceinline__ void swap32(uint32_t& a, uint32_t& b) {
-  const auto r = __builtin_amdgcn_permlane32_swap(a, b, false, false);
-  a = r[0];
-  b = r[1];
-}
-__device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
-  const auto r = __builtin_amdgcn_permlane16_swap(a, b, false, false);
-  a = r[0];
-  b = r[1];
-}
 // the 16 code words of the lane's tile entries, wds[g][nt] = Sq[16 nt + l16][32 w + 16 g + 4 q .. + 3] (zero past a
 // K_ x V_ < 128 x 128 head's rows / columns).  128 x 128: 16-byte loads, then a transpose across the lane groups.  Load
 // k of lane (q, l16) takes Sq[16 (2 k + (q >> 1)) + l16][32 w + 16 (q & 1) .. + 15], so that one wave instruction
@@ -1113,10 +1148,12 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4
 }
 // P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lanes
 // l < 16 return P[32 w + 16 g + l][0..3] (zero for r >= R) in p[g]; the other lanes zeros.  The contraction runs over
-// v, so each block of B is transposed on the way in (one exact MFMA against the identity: lane l then holds
-// B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]) rather than kept transposed in registers.
-__device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], float pn, int R,
-                                        f32x4 p[2]) {
+// v, so each block of B is transposed (one exact MFMA against the identity: lane l then holds
+// B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]); the first call (TR) forms the transposed blocks into bt, the
+// second (the U step) reads them from there.
+template <bool TR>
+__device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], f16x4 (&bt)[2][8], float pn,
+                                        int R, f32x4 p[2]) {
   const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
   float M[4][4];
   gram_qold_q(sh, M);
@@ -1129,8 +1166,8 @@ __device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh
     const f16x4 aq = *(const f16x4*)&sh.qT[l16 & 3][16 * nt + 4 * q];          // rows >= 4 of P^T: unused
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
-      const f16x4 bt = to_h4(mma16(bh[g][nt], ident, f32x4{0.f, 0.f, 0.f, 0.f}));
-      pacc[g] = mma16(aq, bt, pacc[g]);
+      if constexpr (TR) bt[g][nt] = pinned(to_h4(mma16(bh[g][nt], ident, f32x4{0.f, 0.f, 0.f, 0.f})));
+      pacc[g] = mma16(aq, bt[g][nt], pacc[g]);
     }
   }
 #pragma unroll
@@ -1178,8 +1215,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinHalf win;
   load_half<K_, V_>(win, st, slot, hv, L, 0);
-  uint32_t wds[2][8];
-  load_code_words4<K_, V_>(wds, Sq);
+  uint32_t wds[2][8];                                 // loaded after the first window half's products
 
   if (colt) {
     sh.skl[cv] = scv;
@@ -1209,13 +1245,15 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) t.a[g][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
     store_half(sh, win, L, 0);
+    // the second half's rows are requested as soon as the first half's are in LDS, and the code words after the first
+    // half's products, so that each load's latency overlaps a half's products (holding the code words from stage 1
+    // as well would take the registers past 128)
+    if (two) load_half<K_, V_>(win, st, slot, hv, L, 1);
     __syncthreads();
     rebuild_half4(t, sh.op[0], sh.op[1]);
     rebuild_half4(t, sh.op[0], sh.op[2]);
+    load_code_words4<K_, V_>(wds, Sq);
     if (two) {
-      // the second half's rows are loaded only now: held across the first half's products they would push the
-      // code words (live from stage 1 to the end of the rebuild) out of the 128 registers
-      load_half<K_, V_>(win, st, slot, hv, L, 1);
       __syncthreads();                                // every wave is past the first half's operands
       store_half(sh, win, L, 1);
       __syncthreads();
@@ -1241,7 +1279,8 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
 
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
   f32x4 p16[2];
-  p_step4(sh, bh, pn, R, p16);                        // P16 rows of this wave's channels (lanes < 16)
+  f16x4 bt[2][8];                                     // B^T blocks, formed by the first P step
+  p_step4<true>(sh, bh, bt, pn, R, p16);              // P16 rows of this wave's channels (lanes < 16)
   if (q == 0) {
 #pragma unroll
     for (int g = 0; g < 2; ++g)
@@ -1308,7 +1347,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   }
   __syncthreads();
   f32x4 u16[2];
-  p_step4(sh, bh, pn, R, u16);                        // U16 = P step with Q16 (lanes < 16)
+  p_step4<false>(sh, bh, bt, pn, R, u16);             // U16 = P step with Q16 (lanes < 16)
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
   // E is kept packed (fp16, in B's registers: B is dead after the U step); the products B / pn, E rsk and the |E| sums
