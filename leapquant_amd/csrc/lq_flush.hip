@@ -1410,12 +1410,12 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
   }
   __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
-  float* S = (float*)base;
+  float* S = (float*)base;                            // non-temporal: 64 KiB per head, written once (171 -> 165 us)
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
     if ((K_ == KD || 16 * w + 4 * q < K_) && (V_ == VD || v < V_))
-      *(float4*)(S + v * K_ + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
+      __builtin_nontemporal_store(t.a[nt], (f32x4*)(S + v * K_ + 16 * w + 4 * q));
   }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {

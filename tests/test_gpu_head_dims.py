@@ -197,6 +197,28 @@ def test_dequant_matches_oracle(K, V):
 
 
 @pytest.mark.parametrize("K,V", DIMS)
+def test_dequant_empty_and_partial_windows(K, V):
+    """Heads with an empty window (no window products) and with a partial one in one dequant call."""
+    rng = np.random.default_rng(1600 + K + V)
+    NS, HV, H = 6, 4, 2
+    st, S, Q0 = make_state(rng, NS, HV, H, K=K, V=V, L=64)
+    A_log, dt_bias = gate_params(HV, K)
+    for _ in range(9):                                  # slot 3 only: h = 9; the others stay at h = 0
+        mixed, a, b = make_inputs(rng, 1, HV, H, K, V)
+        O.gdn_step(st, mixed, a, b, A_log, dt_bias, np.array([3]))
+    idx = np.array([1, 3, 0, 5], np.int64)
+    ssm, lq = G.to_gpu(st)
+    ref = O.dequant(st, idx)
+    lq.dequantize(ssm, torch.from_numpy(idx).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    for s in (1, 3, 5):
+        got = ssm[s].cpu().numpy()
+        err = np.abs(got - ref[s]).max() / np.abs(ref[s]).max()
+        assert err < 1e-5, (s, err)
+    assert np.array_equal(g["hcnt"], st["hcnt"]) and np.array_equal(g["Wbuf"], st["Wbuf"])
+
+
+@pytest.mark.parametrize("K,V", DIMS)
 def test_decode_over_windows_matches_oracle(K, V):
     """LeapQuantState.decode (step + flush on the device's due flag) for 2.5 windows of L = 16, every step's outputs
     against the oracle run from the same state.  Before the first flush both sides hold the same state (>= 99 % of the

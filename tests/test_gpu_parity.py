@@ -337,6 +337,33 @@ def test_dequant_matches_oracle():
     assert np.array_equal(g["hcnt"], st["hcnt"]) and np.array_equal(g["Wbuf"], st["Wbuf"])
 
 
+def test_dequant_empty_and_partial_windows():
+    """One dequant call over heads with an empty window (h == 0: no window products) and heads with a partial one,
+    padding rows between them: every slot against the oracle, an unlisted slot's bytes untouched."""
+    rng = np.random.default_rng(601)
+    NS, HV, H = 7, 4, 2
+    st, S, Q0 = make_state(rng, NS, HV, H, L=64)
+    A_log, dt_bias = gate_params(HV, 128, False)
+    for _ in range(23):                                 # slots 1 and 4 only: h = 23; slots 2, 3, 5, 6 stay at h = 0
+        sl = np.array([1, 4])
+        mixed, a, b = make_inputs(rng, len(sl), HV, H)
+        O.gdn_step(st, mixed, a, b, A_log, dt_bias, sl)
+    assert np.all(st["hcnt"][[1, 4]] == 23) and np.all(st["hcnt"][[2, 3, 5, 6]] == 0)
+    idx = np.array([2, 1, 0, 4, 5, 6], np.int64)
+    ssm, lq = G.to_gpu(st)
+    before = ssm[3].view(torch.int32).clone()          # checkpoint bytes (as floats some are NaN)
+    ref = O.dequant(st, idx)
+    lq.dequantize(ssm, torch.from_numpy(idx).to(G.DEV))
+    g = G.from_gpu(ssm, lq)
+    for s_ in (1, 2, 4, 5, 6):
+        got = ssm[s_].cpu().numpy()
+        err = np.abs(got - ref[s_]).max() / np.abs(ref[s_]).max()
+        assert err < 1e-5, (s_, err)
+    assert torch.equal(ssm[3].view(torch.int32), before)
+    assert np.array_equal(g["hcnt"], st["hcnt"]) and np.array_equal(g["Wbuf"], st["Wbuf"])
+    assert np.array_equal(g["Pbuf"], st["Pbuf"])
+
+
 @pytest.mark.parametrize("dtype", ["bf16", "f32"])
 def test_dense_step_matches_oracle(dtype):
     from leapquant_amd import kernels as KN
