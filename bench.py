@@ -80,6 +80,7 @@ def event_ms(torch, stream, fn, reps):
     of the start event keeps the GPU busy while the host enqueues fn()'s launches, so that the events bracket the GPU's
     work and not the host's launch latency (which a single eager launch would otherwise add, ~20-30 us here)."""
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)
         e0.record(stream)
@@ -376,6 +377,7 @@ def probe_read_us(torch, stream, capture, bases, stride, nbytes, nblk, per_wg, n
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     reps = NSET // 2 if NSET >= 2 else 1
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         e0.record(stream)
@@ -441,6 +443,7 @@ def dense_rmw_ceiling(torch, stream, Sd, B, HV, NSET, capture):
         gr.replay()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()                                  # warm-up replays (default stream) done
         with torch.cuda.stream(stream):
             torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
             e0.record(stream)
@@ -603,6 +606,13 @@ def main():
         mixed, a, b = pool[s % P]
         lq.decode(ssm, mixed, a, b, A_log, dt_bias, sets[s % NSET], out)
 
+    def reset_windows(q):
+        """Every window of state q back to empty (h = 0; weights 0, decay product 1), the checkpoints kept: the timed
+        loops after the first start from there, as after a flush."""
+        q.hcnt.zero_()
+        q.Wbuf.zero_()
+        q.Pbuf.fill_(1.0)
+
     v = lq.views(ssm)
 
     def step_only(s, kset):
@@ -638,6 +648,7 @@ def main():
     torch.cuda.synchronize()
     assert int(lq.hcnt[1:].max()) == 0                           # every window back at the start of a rotation
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         e0.record(stream)
@@ -666,6 +677,7 @@ def main():
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     for _ in range(NSET):
         gdec.replay()
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         s0.record(stream)
@@ -676,7 +688,7 @@ def main():
     staggered_us = s0.elapsed_time(s1) * 1e3 / ROT
     # the same with the step and the flush as two launches (lq_gdn_step, then lq_flush of the call's rows: every due
     # head its own workgroup), for comparison
-    lq.quantize(ssm, all_slots)
+    reset_windows(lq)
     for kk in range(NSET):
         lq.hcnt[sets[kk].long()] = fill0
 
@@ -687,6 +699,7 @@ def main():
     torch.cuda.synchronize()
     for _ in range(NSET):
         gsf.replay()
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         s0.record(stream)
@@ -696,17 +709,48 @@ def main():
     s1.synchronize()
     staggered_two_us = s0.elapsed_time(s1) * 1e3 / ROT
     del gsf
+    # the deferred-flush decode (lq_gdn_decode_deferred: of the two heads of a key head a call fills, the second is
+    # flushed at the start of the next call that steps the slot): synchronized windows, then staggered ones
+    lqd = LeapQuantState(ssm, H, L=L, R=R, defer_flush=True)
+
+    def decode_deferred(s):
+        mixed, a, b = pool[s % P]
+        lqd.decode(ssm, mixed, a, b, A_log, dt_bias, sets[s % NSET], out)
+    gdd = capture(decode_deferred, CH)
+    deferred_us = {}
+    for regime in ("synchronized", "staggered"):
+        reset_windows(lqd)
+        if regime == "staggered":
+            for kk in range(NSET):
+                lqd.hcnt[sets[kk].long()] = fill0
+        torch.cuda.synchronize()
+        for _ in range(NSET):
+            gdd.replay()
+        torch.cuda.synchronize()                                  # warm-up replays (default stream) done
+        with torch.cuda.stream(stream):
+            torch.cuda._sleep(2_000_000)            # keeps the GPU busy while the host enqueues
+            s0.record(stream)
+            for _ in range(NSET):
+                gdd.replay()
+            s1.record(stream)
+        s1.synchronize()
+        deferred_us[regime] = s0.elapsed_time(s1) * 1e3 / ROT
+    del gdd
+    lqd.flush(ssm, all_slots)                                     # settle the deferred heads
+    torch.cuda.synchronize()
+    del lqd
     progress("decode loop, staggered windows: %.3f us per call (step + flush launches: %.3f)"
              % (staggered_us, staggered_two_us))
     # ---- step-only and flush timings, sets rotated as in the decode loop (a graph of 64 step launches gives each
     # of the NSET sets 64 / NSET steps; NSET replays take every window from h = 0 to h = 64, then every head is due) ----
-    lq.quantize(ssm, all_slots)                                   # every window back to h = 0
+    reset_windows(lq)                                             # every window back to h = 0
     gsteps = capture(lambda i: step_only(i, i % NSET), CH)
     gflush = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
     gidle = capture(lambda i: lq.flush(ssm, sets[0]), CH)         # 64 flush launches with no head due, as decode runs them
     torch.cuda.synchronize()
     rounds = 3
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(NSET + 2)] for _ in range(rounds)]
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         for r in range(rounds):
             if r == 0:
@@ -747,6 +791,7 @@ def main():
     gd.replay()
     torch.cuda.synchronize()
     d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
         torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
         d0.record(stream)
@@ -796,9 +841,10 @@ def main():
     conv_us = {}
     for name, fn in (("fused", fused), ("unfused", unfused), ("decode", fused_decode)):
         gr = capture(fn, CH)
-        lq.quantize(ssm, all_slots)                               # every window back to h = 0
+        reset_windows(lq)                                         # every window back to h = 0
         torch.cuda.synchronize()
         c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()                                  # warm-up replays (default stream) done
         with torch.cuda.stream(stream):
             torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
             c0.record(stream)
@@ -858,8 +904,13 @@ def main():
         "flush_due_us": round(flush_due_us, 2), "flush_idle_us": round(flush_idle_us, 3),
         "decode_staggered_us": round(staggered_us, 3),
         "decode_staggered_two_launch_us": round(staggered_two_us, 3),
+        "decode_deferred_us": round(deferred_us["synchronized"], 3),
+        "decode_staggered_deferred_us": round(deferred_us["staggered"], 3),
         "decode_staggered_note": "not the BASELINE workload: row n starts at window fill n % 64, so on every call one "
-                                 "row per set is flushed (rows reach their flush at different calls, as in serving)",
+                                 "row per set is flushed (rows reach their flush at different calls, as in serving); "
+                                 "deferred = lq_gdn_decode_deferred (LeapQuantState(defer_flush=True)): of the two "
+                                 "heads of a key head a call fills, the second is flushed at the start of the next "
+                                 "call that steps the slot (same outputs)",
     }
     res["conv_fused_config1"] = {
         "workload": "config 1 step with vLLM's causal_conv1d_update (width 4, SiLU, bf16 state [NS, C, 3]) fused in, "

@@ -114,6 +114,18 @@ int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const lq_conv* cv
  * shapes run the step and the flush as two launches.  Same limits as lq_gdn_step and lq_flush. */
 int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0, void* stream);
 
+/* lq_gdn_decode with the flush of a key head's second value head deferred: no counterpart in the reference (whose
+ * flush follows every step); for continuous batching, where rows reach the end of their window on different calls.
+ * At (K, V) = (128, 128), HV = 2 H, of the two heads of a key head that a call fills, the step workgroup flushes the
+ * first right after its step and leaves the second full (hcnt == L, flagged in st->ctl); the next call that steps the
+ * slot flushes it before its step, on the same threads, or lq_flush does.  Every output is the one lq_gdn_decode gives
+ * (a full head is flushed before any step reads it); between calls a slot may hold a full head, so a reader of the
+ * checkpoint other than these two calls runs lq_flush on its slots first (LeapQuantState.dequantize does).  A filling
+ * call costs one head's flush instead of two: the latency that a due row adds to the call halves.  Other shapes: as
+ * lq_gdn_decode. */
+int lq_gdn_decode_deferred(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0,
+                           void* stream);
+
 /* KDA decode step (per-key-channel gate).  glb != 0: GLM's bounded gate glb * sigmoid(exp(A_log) (a + dt_bias));
  * glb == 0: Kimi's -exp(A_log) softplus(a + dt_bias).
  * Replaces make_kda_step(...)(Sq, Sk, Sv, Skv, Kbuf, Ubuf, Wbuf, Pbuf, Gbuf, hcnt, mixed, a, b, A_log, dt_bias, UQ,

@@ -36,6 +36,8 @@ SIGNATURES = {
     "lq_kda_step": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_float, c_void_p]),
     "lq_gdn_decode": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv), c_void_p,
                               c_void_p]),
+    "lq_gdn_decode_deferred": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv),
+                                       c_void_p, c_void_p]),
     "lq_flush": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_int, c_float, c_void_p]),
     "lq_quantize": (c_int, [ctypes.POINTER(LqState), c_void_p, c_void_p, c_int, c_float, c_void_p]),
     "lq_dequant": (c_int, [ctypes.POINTER(LqState), c_void_p, c_int, c_float, c_void_p]),

@@ -105,9 +105,10 @@ struct StepLds<K_, V_, G, true, RM> {
 // RM: factors held per head.  4 (R <= 4): the G R <= 16 factor rows of the workgroup's heads are one MFMA tile, taken
 // by the last wave.  16 (the rank ablation R <= 16, K = V = 128; kernels.py:63, 457-469): up to G tiles, tile g taken
 // by the second wave of head g.
-template <int K_, int V_, int G, bool CONV, bool FL, int RM = 4>
+template <int K_, int V_, int G, bool CONV, bool FL, int RM = 4, bool DF = false>
 __global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
 void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const float* Q0) {
+  static_assert(!DF || FL, "deferred flush (lq_gdn_decode_deferred): the fused decode kernel");
   static_assert(!FL || (K_ == 128 && V_ == 128 && G == 2), "fused flush: the four-wave layout, 128 x 128 heads");
   static_assert(RM == 4 || (RM == 16 && K_ == 128 && V_ == 128 && !FL), "ranks above 4: 128 x 128 heads, no fused flush");
   constexpr int KD = K_, VD = V_;
@@ -131,6 +132,23 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
   bf16_t* out = (bf16_t*)io.out + ((long long)n * HV + hv) * VD;
 
+  if constexpr (DF) {
+    // deferred flush (lq_gdn_decode_deferred): a head that the previous call left full is flushed first, on this
+    // workgroup's threads, before anything of the step is loaded (so that no loaded value waits across the flush; the
+    // cost is the slot index and the fills read before the row's inputs are requested)
+    const int slot0 = io.idx[n];
+    if (slot0 > 0 && slot0 < st.NS && !(CONV && slot0 >= cv.NS)) {
+      unsigned pend = 0;
+#pragma unroll
+      for (int g2 = 0; g2 < G; ++g2) pend |= (st.hcnt[(long long)slot0 * HV + hk * G + g2] >= L ? 1u : 0u) << g2;
+      if (pend) {
+        const float qm = code_range(st);
+#pragma unroll
+        for (int g2 = 0; g2 < G; ++g2)
+          if ((pend >> g2) & 1u) lqf::flush_head4<128, 128>(lds.fl, st, Q0, slot0, hk * G + g2, qm);
+      }
+    }
+  }
   // The row's own inputs (q, k, v, gate) do not depend on its slot: requested before the slot index, so that their
   // latency overlaps its load (a padding row reads them too and ignores them).
   const bf16_t* mrow = (const bf16_t*)io.mixed + (long long)n * MIX;
@@ -513,9 +531,14 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
     if (any) {
       __syncthreads();          // the step is done with the shared bytes, and its appends are visible to the workgroup
       const float qm = code_range(st);
+      bool first = true;        // DF: the first due head now, the others at the start of the next call
 #pragma unroll
       for (int g2 = 0; g2 < G; ++g2)
-        if (due[g2]) lqf::flush_head4<128, 128>(lds.fl, st, Q0, slot, hk * G + g2, qm);
+        if (due[g2]) {
+          if (!DF || first) lqf::flush_head4<128, 128>(lds.fl, st, Q0, slot, hk * G + g2, qm);
+          else if (tid == 0) note_due(st.ctl, dlist, n * HV + hk * G + g2);   // a standalone flush finds it
+          first = false;
+        }
     }
   }
 }
@@ -994,25 +1017,39 @@ extern "C" int lq_gdn_step_conv(const lq_state* st, const lq_step_io* io, const 
   return launch_gdn_dims<true>(st, io, *cv, nullptr, (hipStream_t)stream);
 }
 
-extern "C" int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0,
-                             void* stream) {
+static int gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0, bool deferred,
+                      hipStream_t s) {
   int rc = lq_check_step(st, io);
   if (rc) return rc;
   if (cv && (rc = check_conv(st, cv))) return rc;
   const float qmax = st->qmax > 0.f ? st->qmax : LQ_QMAX;
   if ((rc = lq_check_flush(st, Q0, io->idx, io->N, 0, qmax))) return rc;
   if (io->N == 0) return LQ_OK;
-  hipStream_t s = (hipStream_t)stream;
   if (st->K == 128 && st->V == 128 && st->HV == 2 * st->H && st->R <= 4) {   // one launch: the step flushes its own due heads
     const dim3 grid((unsigned)(io->N * st->H));
     const lq_conv none = {};
-    if (cv) gdn_step_kernel<128, 128, 2, true, true><<<grid, 256, 0, s>>>(*st, *io, *cv, nullptr, Q0);
-    else gdn_step_kernel<128, 128, 2, false, true><<<grid, 256, 0, s>>>(*st, *io, none, nullptr, Q0);
+    if (deferred) {
+      if (cv) gdn_step_kernel<128, 128, 2, true, true, 4, true><<<grid, 256, 0, s>>>(*st, *io, *cv, nullptr, Q0);
+      else gdn_step_kernel<128, 128, 2, false, true, 4, true><<<grid, 256, 0, s>>>(*st, *io, none, nullptr, Q0);
+    } else {
+      if (cv) gdn_step_kernel<128, 128, 2, true, true><<<grid, 256, 0, s>>>(*st, *io, *cv, nullptr, Q0);
+      else gdn_step_kernel<128, 128, 2, false, true><<<grid, 256, 0, s>>>(*st, *io, none, nullptr, Q0);
+    }
     return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
   }
   rc = cv ? launch_gdn_dims<true>(st, io, *cv, nullptr, s) : lq_launch_step(st, io, 0, 0.f, nullptr, s);
   if (rc) return rc;
   return lq_launch_flush(st, Q0, io->idx, io->N, 0, qmax, nullptr, s);
+}
+
+extern "C" int lq_gdn_decode(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0,
+                             void* stream) {
+  return gdn_decode(st, io, cv, Q0, false, (hipStream_t)stream);
+}
+
+extern "C" int lq_gdn_decode_deferred(const lq_state* st, const lq_step_io* io, const lq_conv* cv, const float* Q0,
+                                      void* stream) {
+  return gdn_decode(st, io, cv, Q0, true, (hipStream_t)stream);
 }
 
 extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream) {

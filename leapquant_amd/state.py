@@ -60,10 +60,15 @@ class LeapQuantState:
     kda=False: Gated DeltaNet (Qwen).  kda=True: Kimi Delta Attention (GLM), gate_lower_bound = GLM's bounded gate.
     nmax: the most rows one decode call can carry (accepted for parity; the HIP flush needs no work-list sizing).
     qmax: code range of the checkpoint (127: INT8; 31: 6-bit codes in the int8 container).
+    defer_flush (not in the reference): GDN decode through lq_gdn_decode_deferred -- of the two value heads of a key
+    head that a call fills, the second is flushed at the start of the next call that steps its slot (the outputs are
+    the same; a due row costs its call one head flush instead of two).  dequantize settles such heads first.
     """
 
-    def __init__(self, ssm, H, kda=False, gate_lower_bound=0.0, nmax=0, L=WINDOW, R=RANK, qmax=KN.QMAX):
+    def __init__(self, ssm, H, kda=False, gate_lower_bound=0.0, nmax=0, L=WINDOW, R=RANK, qmax=KN.QMAX,
+                 defer_flush=False):
         assert ssm.dtype == torch.float32, f"LeapQuant needs the fp32 recurrent state cache, got {ssm.dtype}"
+        self.defer_flush = bool(defer_flush) and not kda
         NS, HV, V, K = ssm.shape
         SS = ssm.stride(0)
         assert ssm.stride()[1:] == (V * K, K, 1), f"state inner dims must be packed, got strides {ssm.stride()}"
@@ -164,8 +169,8 @@ class LeapQuantState:
             _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 1, ctypes.c_float(self.qmax),
                                   stream), "lq_flush")
         else:                        # step + flush of the heads it fills (one launch for 128 x 128 heads, GQA 2)
-            _lib.check(L.lq_gdn_decode(ctypes.byref(st), ctypes.byref(io), None, KN._p(self.Q0), stream),
-                       "lq_gdn_decode")
+            fn = L.lq_gdn_decode_deferred if self.defer_flush else L.lq_gdn_decode
+            _lib.check(fn(ctypes.byref(st), ctypes.byref(io), None, KN._p(self.Q0), stream), "lq_gdn_decode")
 
     def decode_conv(self, ssm, x, conv_state, conv_weight, conv_bias, silu, a, b, A_log, dt_bias, idx, out):
         """GDN decode with the conv1d update fused into the step (lq_gdn_step_conv): x is the raw projection
@@ -203,8 +208,8 @@ class LeapQuantState:
         io = KN._step_io(x, a, b, A_log, dt_bias, idx, out, self.kstep_scale)
         cv = KN.conv_struct(conv_state, w, conv_bias, silu)
         stream = ctypes.c_void_p(torch.cuda.current_stream(x.device).cuda_stream)
-        _lib.check(self._lib.lq_gdn_decode(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), KN._p(self.Q0),
-                                           stream), "lq_gdn_decode")
+        fn = self._lib.lq_gdn_decode_deferred if self.defer_flush else self._lib.lq_gdn_decode
+        _lib.check(fn(ctypes.byref(st), ctypes.byref(io), ctypes.byref(cv), KN._p(self.Q0), stream), "lq_gdn_decode")
 
     def _check_gate(self, a, N, KA):
         """The raw gate `a` is read as bf16, N x HV (GDN) or N x HV x K (KDA) values (kernels.py:86, 738)."""
@@ -241,9 +246,12 @@ class LeapQuantState:
         if self.kda:                 # S = (Q U^T + deq) diag(exp(P)) + decayed window (state.py:118-128), HIP
             self._kda_round_trip(ssm, idx, "lq_kda_dequant")
             return
+        idx = idx.to(torch.int32).contiguous()
+        if self.defer_flush:         # a head left full by a deferred decode is flushed before its state is read
+            self.flush(ssm, idx)
         v = self.views(ssm)
         self.kdeq(ssm, v["Sq"], v["Sk"], v["Sv"], self.Kbuf, self.Ubuf, self.Wbuf, self.Pbuf, self.Gbuf, self.hcnt,
-                  v["uq"], idx.to(torch.int32).contiguous())
+                  v["uq"], idx)
 
     def quantize(self, ssm, idx):
         """Write the 8-bit checkpoint of the fp32 states in the slots idx and reset their windows (after a prefill)."""

@@ -14,7 +14,10 @@ from ..state import get_state
 
 
 def _state_of(layer, nmax):
-    return get_state(layer, layer.kv_cache[1], H=layer.num_k_heads // layer.tp_size, nmax=nmax[0])
+    # deferred flushes (lq_gdn_decode_deferred): under continuous batching rows reach the end of their window on
+    # different calls, and a row due on a call then costs it one head flush instead of two; the outputs are the same,
+    # and the prefill round trip (dequantize) flushes a slot's deferred head before it reads the state
+    return get_state(layer, layer.kv_cache[1], H=layer.num_k_heads // layer.tp_size, nmax=nmax[0], defer_flush=True)
 
 
 def _metadata(layer, get_forward_context):

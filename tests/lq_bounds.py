@@ -188,6 +188,16 @@ class CheckingLib:
         io = _arg(io)
         return self._per_slot("lq_gdn_decode flush", st, ctypes.c_void_p(io.idx), io.N, False, False, Q0=Q0)
 
+    def lq_gdn_decode_deferred(self, st, io, cv, Q0, stream):
+        """The same footprint as lq_gdn_decode: a deferred head is flushed by the next call that steps its slot, which
+        reads and writes the same (slot, head) bytes as the flush it replaces."""
+        cv_ = _arg(cv) if cv is not None else None
+        rc = self._step("lq_gdn_decode_deferred", st, io, False, cv_)
+        if rc:
+            return rc
+        io_ = _arg(io)
+        return self._per_slot("lq_gdn_decode_deferred flush", st, ctypes.c_void_p(io_.idx), io_.N, False, False, Q0=Q0)
+
     def _per_slot(self, name, st, idx, N, kda, block, Q0=None, need_buf=True):
         st = _arg(st)
         self.calls.append(name)

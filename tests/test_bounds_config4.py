@@ -41,19 +41,23 @@ def _stack(bf16_conv):
 
 
 @pytest.mark.parametrize("bf16_conv", [False, True])
-def test_config4_plugin_calls_stay_in_bounds(checked, bf16_conv):
+@pytest.mark.parametrize("deferred", [False, True])
+def test_config4_plugin_calls_stay_in_bounds(checked, bf16_conv, deferred):
+    """deferred: the states as the plugin builds them (defer_flush=True, lq_gdn_decode_deferred); otherwise built
+    beforehand with the reference's arguments (lq_gdn_decode)."""
     from leapquant_amd import state as S
     torch.manual_seed(0)
     stack, idx = _stack(bf16_conv)
     for l in stack:
-        S.get_state(l.attn, l.ssm, H=l.H).quantize(l.ssm, idx)
+        S.get_state(l.attn, l.ssm, H=l.H, defer_flush=deferred).quantize(l.ssm, idx)
     x = torch.randn(B, 2048).to(torch.bfloat16)
     with torch.no_grad():
         for _ in range(2):
             x = GS.run(stack, x)
+    name = "lq_gdn_decode_deferred" if deferred else "lq_gdn_decode"
     assert checked.calls.count("lq_quantize") == LAYERS
-    assert checked.calls.count("lq_gdn_decode") == 2 * LAYERS
-    assert checked.calls.count("lq_gdn_decode flush") == 2 * LAYERS
+    assert checked.calls.count(name) == 2 * LAYERS
+    assert checked.calls.count(name + " flush") == 2 * LAYERS
     # a mixed step on layer 0: 4 decode rows, prefill of slots 5..8 (the fp32 round trip around the engine's prefill)
     l = stack[0]
     md = FV.gdn_metadata(4, idx[:4], prefill_idx=idx[4:8], prefill_loc=torch.tensor([0, 2, 4, 6, 8]))

@@ -105,7 +105,7 @@ def test_gdn_decode_only_step_goes_to_leapquant(plugin):
     layer._forward_core(mixed_qkv, b, a, out)
     assert "vllm_core" not in FV.CALLS                                  # vLLM's decode path did not run
     st = plugin.rec[id(layer)]
-    assert st.kw == dict(H=H, nmax=512)
+    assert st.kw == dict(H=H, nmax=512, defer_flush=True)
     (name, c), = st.calls
     assert name == "decode"
     # the conv update of the first n rows, computed on a copy of the conv state
