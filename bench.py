@@ -35,8 +35,8 @@ if ROOT not in sys.path:
     sys.path.insert(0, ROOT)
 
 METRIC = "int8 GDN/KDA decode-step µs + achieved HBM GB/s at B=64,H=32,d=128"
-DECODE_KERNEL = "gdn_step_kernel<128, 128, 2, false, true, 4>"  # lq_gdn_decode at GQA 2: step + flush of its due heads
-STEP_KERNEL = "gdn_step_kernel<128, 128, 2, false, false, 4>"   # the step alone (lq_gdn_step)
+DECODE_KERNEL = "gdn_step_kernel<128, 128, 2, false, true, 4, false>"  # lq_gdn_decode at GQA 2: step + flush of its due heads
+STEP_KERNEL = "gdn_step_kernel<128, 128, 2, false, false, 4, false>"   # the step alone (lq_gdn_step)
 HBM_PEAK_GBPS = 8000.0
 
 
