@@ -14,7 +14,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "_build")
 LIB = os.path.join(OUT, "liblq.so")
-SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dense.hip", "lq_noalloc.hip")
+SOURCES = ("lq_step.hip", "lq_flush.hip", "lq_dequant.hip", "lq_dense.hip", "lq_noalloc.hip")
 PROBE_LIB = os.path.join(OUT, "liblq_probe.so")
 PROBE_SOURCES = ("lq_probe.hip",)
 ARCH = os.environ.get("LQ_OFFLOAD_ARCH", "gfx950")

@@ -246,6 +246,9 @@ __device__ __forceinline__ char* block_base(const lq_state& st, int slot, int hv
 __attribute__((visibility("hidden"))) int lq_check_step(const lq_state* st, const lq_step_io* io);
 __attribute__((visibility("hidden"))) int lq_check_flush(const lq_state* st, const float* Q0, const int* idx, int N,
                                                          int kda, float qmax);
+// the four-wave prefill dequant of GDN 128 x 128 heads at R <= 4 (lq_dequant.hip); arguments checked by lq_dequant
+__attribute__((visibility("hidden"))) int lq_launch_dequant4(const lq_state* st, const int* idx, int N, float qmax,
+                                                             hipStream_t s);
 // decode step of every row of io (GDN or KDA), due heads signalled through dlist when it is set (else st->ctl)
 __attribute__((visibility("hidden"))) int lq_launch_step(const lq_state* st, const lq_step_io* io, int kda, float glb,
                                                          int* dlist, hipStream_t s);

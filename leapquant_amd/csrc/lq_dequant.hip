@@ -1,0 +1,115 @@
+// Prefill dequant of GDN 128 x 128 heads at R <= 4 in the four-wave layout (gfx950).
+//
+// Semantics: /root/reference/leapquant/kernels.py:2041-2123 (dequant), as the eight-wave dequant_kernel of lq_flush.hip.
+// A translation unit of its own: in lq_flush.hip the extra kernel changed the register allocation of the flush kernels
+// (a 16-byte spill in the four-wave flush in place of 8, and a slower flush), although their code is unchanged.
+#include "lq_flush_core.h"
+
+namespace {
+
+using namespace lqf;
+
+// Four-wave prefill dequant of a GDN 128 x 128 head at R <= 4: dequant_kernel's arithmetic with the tile in the
+// four-wave layout of the flush (wave w owns key channels [32 w, 32 w + 32)) and the window staged in halves of 32
+// entries, so that the workgroup fits 40 KiB of LDS and four heads share a CU (the eight-wave layout holds the whole
+// window's operands, 60 KiB: two heads per CU).  The window's products are added half by half (hi, lo of the first
+// half, then of the second), an fp32 order the eight-wave kernel takes as hi, lo over the whole window.
+__global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
+void dequant4_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
+  __shared__ FlushShared4 sh;
+  const int HV = st.HV, L = st.L, R = st.R;
+  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  const int slot = idx[n];
+  if (slot <= 0 || slot >= st.NS) return;
+  const long long sh_ = (long long)slot * HV + hv;
+  const int tid = threadIdx.x, l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4;
+  char* base = block_base(st, slot, hv);
+  const int8_t* Sq = (const int8_t*)base;
+  const float* Sk = (const float*)(base + VD * KD);
+  const float* Sv = Sk + KD;
+  const f16_t* UQ = (const f16_t*)(Sv + VD);
+  const int h = __builtin_amdgcn_readfirstlane(min(st.hcnt[sh_], L));   // uniform: one word per head
+  const float P = st.Pbuf[sh_];
+  const int cv = tid & 127;
+  const bool colt = tid < KD;
+  const float scv = colt ? Sk[cv] : Sv[cv];
+  float uqv[4];
+#pragma unroll
+  for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
+  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
+  WinHalf win;
+  if (h > 0) load_half<KD, VD>(win, st, slot, hv, h, 0);   // an empty window loads, stages and multiplies nothing
+  uint32_t wds[2][8];
+  load_code_words4<KD, VD>(wds, Sq);
+  {
+    f32x4 fac;
+#pragma unroll
+    for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
+    if (colt) {
+      sh.skl[cv] = scv;
+      sh.uoc[cv] = fac;
+    } else {
+      sh.svr[cv] = scv;
+      sh.qov[cv] = fac;
+    }
+  }
+  if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
+  __syncthreads();
+  Tile4 t;
+  {
+    const float inv = 1.0f / qmax;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) {
+      const int c0 = 32 * w + 16 * g + 4 * q;
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt) {
+        const int v = 16 * nt + (l & 15);
+        const float rv = sh.svr[v];
+        const f32x4 qo = sh.qov[v];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int c = c0 + i;
+          const f32x4 uo = sh.uoc[c];
+          float x = (((float)(int)(int8_t)(wds[g][nt] >> (8 * i)) * inv) * sh.skl[c]) * rv;   // kernels.py:2107
+#pragma unroll
+          for (int a = 0; a < 4; ++a) x = fmaf(qo[a], uo[a], x);                              // kernels.py:2109-2111
+          t.a[g][nt][i] = x * P;                                                               // kernels.py:2113
+        }
+      }
+    }
+  }
+  if (h > 0) {                                        // + sum_{j<h} w_j u_j k_j^T (kernels.py:2115-2121)
+    store_half(sh, win, h, 0);
+    if (h > HALF) load_half<KD, VD>(win, st, slot, hv, h, 1);
+    __syncthreads();
+    rebuild_half4(t, sh.op[0], sh.op[1]);
+    rebuild_half4(t, sh.op[0], sh.op[2]);
+    if (h > HALF) {
+      __syncthreads();                                // every wave is past the first half's operands
+      store_half(sh, win, h, 1);
+      __syncthreads();
+      rebuild_half4(t, sh.op[0], sh.op[1]);
+      rebuild_half4(t, sh.op[0], sh.op[2]);
+    }
+  }
+  __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
+  float* S = (float*)base;                            // non-temporal: 64 KiB per head, written once
+#pragma unroll
+  for (int g = 0; g < 2; ++g)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      __builtin_nontemporal_store(t.a[g][nt], (f32x4*)(S + (16 * nt + (l & 15)) * KD + 32 * w + 16 * g + 4 * q));
+  if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
+  if (tid == 0) {
+    st.Pbuf[sh_] = 1.f;
+    st.hcnt[sh_] = 0;
+  }
+}
+
+}  // namespace
+
+// launched by lq_dequant for GDN 128 x 128 heads at R <= 4, arguments already checked
+int lq_launch_dequant4(const lq_state* st, const int* idx, int N, float qmax, hipStream_t s) {
+  dequant4_kernel<<<dim3((unsigned)(N * st->HV)), FT4, 0, s>>>(*st, idx, qmax);
+  return LQ_OK;
+}

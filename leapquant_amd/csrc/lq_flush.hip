@@ -1591,7 +1591,7 @@ extern "C" int lq_dequant(const lq_state* st, const int* idx, int N, float qmax,
   hipStream_t s = (hipStream_t)stream;
   if (st->K == KD && st->R > 8) dequant_kernel<KD, VD, 16><<<g, FT, 0, s>>>(*st, idx, qmax);
   else if (st->K == KD && st->R > 4) dequant_kernel<KD, VD, 8><<<g, FT, 0, s>>>(*st, idx, qmax);
-  else if (st->K == KD) dequant_kernel<><<<g, FT, 0, s>>>(*st, idx, qmax);
+  else if (st->K == KD) lq_launch_dequant4(st, idx, N, qmax, s);
   else if (st->V == VD) dequant_kernel<64, 128><<<g, FT, 0, s>>>(*st, idx, qmax);
   else dequant_kernel<64, 64><<<g, FT, 0, s>>>(*st, idx, qmax);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
