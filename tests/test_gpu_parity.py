@@ -435,6 +435,31 @@ def test_kda_round_trip_matches_oracle(L, steps):
     assert np.all(g["hcnt"][slots] == 0) and np.all(g["Pbuf"][slots] == 0)
 
 
+def test_kda_dequant_empty_and_partial_windows():
+    """One KDA prefill dequant over heads with an empty window (h == 0: no window loads, scan or products) and heads with
+    a partial one (past one 32-entry operand block), padding rows between them: every listed slot against the oracle's
+    rebuild, an unlisted slot's bytes untouched."""
+    rng = np.random.default_rng(902)
+    NS, HV, H = 6, 4, 4
+    st, S, Q0 = make_state(rng, NS, HV, H, L=64, kda=True)
+    A_log, dt_bias = gate_params(HV, 128, True)
+    for _ in range(37):                                 # slots 2 and 5 only: h = 37; slots 1, 3, 4 stay at h = 0
+        sl = np.array([2, 5])
+        mixed, a, b = make_inputs(rng, len(sl), HV, H, kda=True)
+        O.kda_step(st, mixed, a, b, A_log, dt_bias, sl)
+    assert np.all(st["hcnt"][[2, 5]] == 37) and np.all(st["hcnt"][[1, 3, 4]] == 0)
+    idx = np.array([1, 2, 0, 4, 5], np.int64)
+    ssm, lq = G.to_gpu(st)
+    before = ssm[3].view(torch.int32).clone()          # checkpoint bytes (as floats some are NaN)
+    reb = O.kda_rebuild(st, idx[idx > 0])
+    lq.dequantize(ssm, torch.from_numpy(idx).to(G.DEV))
+    torch.cuda.synchronize()
+    for s_ in (1, 2, 4, 5):
+        got = ssm[s_].cpu().numpy()
+        assert np.abs(got - reb[s_]).max() <= 1e-5 * np.abs(reb[s_]).max(), s_
+    assert torch.equal(ssm[3].view(torch.int32), before)
+
+
 @pytest.mark.parametrize("name", ["oracle_gdn_L16", "oracle_gdn_L64", "oracle_kda_L16", "oracle_kda_L64"])
 def test_decode_trajectory_matches_golden(name):
     """Full decode (step + flush every call) over the committed golden trajectories: every output within tolerance."""
