@@ -10,7 +10,9 @@ Measurement:
     replays of the decode loop.  The loop rotates NSET disjoint slot sets (> 1 GB of state) so the 256 MB MALL
     cannot hold the working set between uses of a set, and times whole rotations (every set's windows from empty
     through the all-due flush): --steps / --warmup are rounded up to rotations of 64 * NSET calls, and `steps` /
-    `warmup` report the calls actually run.  `achieved_gbps` divides the algorithmic bytes of those calls by their time.
+    `warmup` report the calls actually run (the warm-up, at least two rotations, is queued directly before the timed
+    calls so that the GPU does not idle between them).  `achieved_gbps` divides the algorithmic bytes of those calls by their time.
+    `value_spread`: the same figure for each of 9 further rotations (median, p10, p90, min, max).
   * `cpu_baseline`: the numpy oracle on config 0, its independent heads split over the host's cores (forked before the
     GPU is touched).
   * `roofline`: the timed region runs one kernel per call -- the GQA-2 step that also flushes the heads whose window it
@@ -641,32 +643,57 @@ def main():
     ROT = L * NSET
     gdec = capture(decode, CH)
     torch.cuda.synchronize()                                      # capturing executes nothing
-    warm_rot = max(1, -(-args.warmup // ROT))
+    # at least two rotations of warm-up: under continuous load the second rotation still ran ~1% slower than the third
+    # and later ones (16.61 against 16.45 us per call)
+    warm_rot = max(2, -(-args.warmup // ROT))
     timed_rot = max(1, -(-args.steps // ROT))
-    for _ in range(warm_rot * NSET):
-        gdec.replay()
+    tev = [torch.cuda.Event(enable_timing=True) for _ in range(timed_rot + 1)]   # between rotations: no gap added
     torch.cuda.synchronize()
-    assert int(lq.hcnt[1:].max()) == 0                           # every window back at the start of a rotation
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
-        e0.record(stream)
-        for _ in range(timed_rot * NSET):
+        # the warm-up replays are queued right before the timed ones, so the GPU goes from them into the timed region
+        # without idling (after an idle gap of ~1 ms the first timed rotation ran 2-3% slower: 16.83 against 16.45 us per
+        # call) and they keep it busy while the host enqueues the timed replays
+        for _ in range(warm_rot * NSET):
             gdec.replay()
-        e1.record(stream)
-    e1.synchronize()
+        tev[0].record(stream)
+        for k in range(timed_rot):
+            for _ in range(NSET):
+                gdec.replay()
+            tev[k + 1].record(stream)
+    tev[-1].synchronize()
     torch.cuda.synchronize()
-    ms_total = e0.elapsed_time(e1)
+    assert int(lq.hcnt[1:].max()) == 0                           # whole rotations: every window back at its start
+    ms_total = tev[0].elapsed_time(tev[-1])
     calls = timed_rot * ROT
     us_per_step = ms_total * 1e3 / calls
+    timed_rot_us = [round(tev[k].elapsed_time(tev[k + 1]) * 1e3 / ROT, 3) for k in range(timed_rot)]
     # bytes of exactly those calls: per set and window, the 64 steps at fills 0..63 and one all-due flush
     timed_bytes = timed_rot * NSET * (sum(step_bytes(B, HV, H, K, V, R, h) for h in range(L))
                                       + flush_bytes(B, HV, H, K, V, R, L))
 
     decode_gbps = timed_bytes / (ms_total * 1e-3) / 1e9
-    progress("decode loop: %.3f us per call over %d calls (%d whole rotations of %d sets)"
-             % (us_per_step, calls, timed_rot, NSET))
+    progress("decode loop: %.3f us per call over %d calls (%d whole rotations of %d sets; per rotation %s)"
+             % (us_per_step, calls, timed_rot, NSET, timed_rot_us))
+    # spread of the same figure: µs per call of each of SPREAD_ROT further whole rotations, events between them (no
+    # gap in the GPU's work), after an untimed rotation queued right before them as above; the windows are back at
+    # their start after every rotation
+    SPREAD_ROT = 9
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(SPREAD_ROT + 1)]
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream):
+        for _ in range(NSET):
+            gdec.replay()
+        evs[0].record(stream)
+        for k in range(SPREAD_ROT):
+            for _ in range(NSET):
+                gdec.replay()
+            evs[k + 1].record(stream)
+    torch.cuda.synchronize()
+    import numpy as np
+    rot_us = np.array([evs[k].elapsed_time(evs[k + 1]) * 1e3 / ROT for k in range(SPREAD_ROT)])
+    value_spread = {"rotations": SPREAD_ROT, "calls_each": ROT, "median": round(float(np.median(rot_us)), 3),
+                    "p10": round(float(np.percentile(rot_us, 10)), 3), "p90": round(float(np.percentile(rot_us, 90)), 3),
+                    "min": round(float(rot_us.min()), 3), "max": round(float(rot_us.max()), 3)}
     # ---- staggered windows (beside the BASELINE workload, not it): row n of every set starts at fill n % 64, so on
     # every call one row per set fills its window and is flushed, as in serving, where rows reach their flush at
     # different calls; the same decode graph over whole rotations ----
@@ -788,18 +815,17 @@ def main():
         KN.dense_step(Sd, mixed, a, b, A_log, dt_bias, sets[i % NSET], out, H)
 
     gd = capture(dense, CH)
-    gd.replay()
-    torch.cuda.synchronize()
     d0, d1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
+    torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
+        for _ in range(2 * NSET):                   # warm-up queued directly before the timed replays, as for the decode
+            gd.replay()
         d0.record(stream)
-        for _ in range(4):
+        for _ in range(2 * NSET):
             gd.replay()
         d1.record(stream)
     torch.cuda.synchronize()
-    bf16_us = d0.elapsed_time(d1) * 1e3 / (4 * CH)
+    bf16_us = d0.elapsed_time(d1) * 1e3 / (2 * NSET * CH)
     bf16_gbps = dense_bytes(B, HV, H, K, V) / (bf16_us * 1e-6) / 1e9
     rmw = dense_rmw_ceiling(torch, stream, Sd, B, HV, NSET, capture)
     del gd, Sd
@@ -879,7 +905,8 @@ def main():
         "metric": METRIC, "value": round(us_per_step, 3), "unit": "us/step", "n_gpus": 1, "steps": calls,
         "warmup": warm_rot * ROT, "steps_requested": args.steps, "warmup_requested": args.warmup,
         "steps_note": "decode calls timed: --steps rounded up to whole rotations of %d calls (every set's window "
-                      "from empty through its flush), so flushes are timed in their real proportion" % ROT,
+                      "from empty through its flush), so flushes are timed in their real proportion; warm-up: "
+                      "--warmup rounded up to whole rotations, at least 2, queued directly before the timed calls" % ROT,
         "ms_per_step": round(us_per_step / 1e3, 6), "higher_is_better": False, "scaling": "weak",
         "vs_baseline": None, "dtype": "int8", "data": "synthetic",
         "config": {"workload": "GDN decode, BASELINE config 1: B=64, HV=32 value / H=16 key heads, d=128, W=64, R=4, "
@@ -887,6 +914,7 @@ def main():
                                "64), whole windows of %d rotated slot sets" % NSET,
                    "batch": B, "value_heads": HV, "key_heads": H, "head_dim": K, "window": L, "rank": R},
         "achieved_gbps": round(decode_gbps, 1),
+        "value_spread": value_spread,
         "bf16_state_step_us": round(bf16_us, 3), "bf16_state_gbps": round(bf16_gbps, 1),
         "bf16_state_rmw_ceiling": rmw,
         "speedup_vs_bf16_step": round(bf16_us / us_per_step, 3),
