@@ -702,11 +702,10 @@ def main():
         lq.hcnt[sets[kk].long()] = fill0
     torch.cuda.synchronize()
     s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    for _ in range(NSET):
-        gdec.replay()
-    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
+    torch.cuda.synchronize()
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
+        for _ in range(2 * NSET):                   # warm-up queued directly before the timed replays
+            gdec.replay()
         s0.record(stream)
         for _ in range(NSET):
             gdec.replay()
@@ -724,11 +723,9 @@ def main():
         flush_only(i % NSET)
     gsf = capture(step_then_flush, CH)
     torch.cuda.synchronize()
-    for _ in range(NSET):
-        gsf.replay()
-    torch.cuda.synchronize()                                  # warm-up replays (default stream) done
     with torch.cuda.stream(stream):
-        torch.cuda._sleep(2_000_000)                # keeps the GPU busy while the host enqueues
+        for _ in range(2 * NSET):                   # warm-up queued directly before the timed replays
+            gsf.replay()
         s0.record(stream)
         for _ in range(NSET):
             gsf.replay()
@@ -751,11 +748,9 @@ def main():
             for kk in range(NSET):
                 lqd.hcnt[sets[kk].long()] = fill0
         torch.cuda.synchronize()
-        for _ in range(NSET):
-            gdd.replay()
-        torch.cuda.synchronize()                                  # warm-up replays (default stream) done
         with torch.cuda.stream(stream):
-            torch.cuda._sleep(2_000_000)            # keeps the GPU busy while the host enqueues
+            for _ in range(2 * NSET):                   # warm-up queued directly before the timed replays
+                gdd.replay()
             s0.record(stream)
             for _ in range(NSET):
                 gdd.replay()
