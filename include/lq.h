@@ -181,7 +181,9 @@ int lq_lowrank(const float* x, const float* Q0, float* U, float* Q, int n, int K
  * For callers that cannot allocate device memory: code under graph capture, tight serving loops, harnesses that forbid
  * hipMalloc.  Limit: N * HV <= LQ_DUE_MAX = 65536, else LQ_ERR_SIZE.  All calls on one GPU share the list: calls that
  * overlap on one GPU (concurrent streams, threads) race and must not be issued.  Results equal lq_gdn_step /
- * lq_kda_step followed by lq_flush on the same inputs. */
+ * lq_kda_step followed by lq_flush on the same inputs.  The list's device address is looked up on the first call on
+ * each device (also a call with N = 0, which launches nothing): a caller that captures its calls in a graph makes
+ * one such call on each device before the capture, so that the captured calls make no runtime query. */
 int lq_decode_noalloc(const lq_state* st, const lq_step_io* io, const float* Q0, int kda, float glb, void* stream);
 
 /* Baseline (no reference counterpart): the standalone conv1d update that lq_gdn_step_conv fuses into the step, same

@@ -6,6 +6,7 @@ probe that bench.py times as the memory system's ceiling; not part of the API).
 hipcc cross-compiles without a GPU.  Every HIP file gets `-Xclang -target-feature -Xclang -packed-fp32-ops` (no
 packed FP32 instructions in the device code).
 """
+import concurrent.futures
 import os
 import subprocess
 import sys
@@ -27,20 +28,24 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
+def _compile_one(cc, flags, s, verbose):
+    src = os.path.join(CSRC, s)
+    obj = os.path.join(OUT, s.replace(".hip", ".o"))
+    cmd = [cc] + flags + ["-c", src, "-o", obj]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("hipcc failed on %s:\n%s" % (s, r.stderr))
+    if verbose:
+        err = "\n".join(x for x in r.stderr.splitlines() if "packed-fp32-ops" not in x)
+        if err.strip():
+            print(err)
+    return obj
+
+
 def _compile_link(cc, flags, sources, lib, verbose):
-    objs = []
-    for s in sources:
-        src = os.path.join(CSRC, s)
-        obj = os.path.join(OUT, s.replace(".hip", ".o"))
-        cmd = [cc] + flags + ["-c", src, "-o", obj]
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError("hipcc failed on %s:\n%s" % (s, r.stderr))
-        if verbose:
-            err = "\n".join(x for x in r.stderr.splitlines() if "packed-fp32-ops" not in x)
-            if err.strip():
-                print(err)
-        objs.append(obj)
+    # one hipcc process per source file, run side by side (each is single-threaded)
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(len(sources), os.cpu_count() or 1)) as ex:
+        objs = list(ex.map(lambda s: _compile_one(cc, flags, s, verbose), sources))
     tmp = lib + ".tmp"
     cmd = [cc, "--offload-arch=%s" % ARCH, "-shared", "-fPIC", "-o", tmp] + objs
     r = subprocess.run(cmd, capture_output=True, text=True)

@@ -25,8 +25,9 @@ using namespace lqf;
 // With the due flag st.ctl[0] (set by the steps), a call in which no step made a head due reads one word and returns;
 // otherwise the last workgroup to finish (counted in st.ctl[1]) clears both for the next call.
 // With a due list (dlist, lq_decode_noalloc) the flush takes exactly the listed heads instead: workgroup b the entries
-// b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, so
-// an entry left by an interrupted call is skipped; the last workgroup to finish empties the list.
+// b, b + gridDim.x, ...  An entry is flushed only if it names a row of this call whose (slot, head) is still due, and
+// the workgroup claims the head first (hcnt L -> L + 1 by compare-and-swap), so an entry left by an interrupted call
+// is skipped or, if it names a head due again, flushed once; the last workgroup to finish empties the list.
 // `head(slot, hv0, mask, sched)` flushes the due heads hv0 + h (bit h of mask) of one unit with the whole workgroup
 // and, with sched set, leaves the workgroup's next candidate in `due`, a word of the workgroup's shared memory.
 template <int U>
@@ -121,7 +122,11 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
       long long take = -1;
       if (p >= 0 && p < N * HV) {
         const int n = p / HV, hv = p - n * HV, slot = idx[n];
-        if (slot > 0 && slot < st.NS && st.hcnt[(long long)slot * HV + hv] == L) take = (long long)slot * HV + hv;
+        // claimed by moving its fill from L to L + 1 (the flush writes 0 at its end): an entry that names the same
+        // head twice -- one left by a call whose flush launch failed, and this call's own -- is flushed once
+        if (slot > 0 && slot < st.NS &&
+            atomicCAS(st.hcnt + (long long)slot * HV + hv, L, L + 1) == L)
+          take = (long long)slot * HV + hv;
       }
       due = (unsigned long long)take;
     }

@@ -47,10 +47,12 @@ extern "C" int lq_decode_noalloc(const lq_state* st, const lq_step_io* io, const
   rc = lq_check_flush(st, Q0, io->idx, io->N, kda, qmax);
   if (rc) return rc;
   if ((long long)io->N * st->HV > LQ_DUE_MAX) return LQ_ERR_SIZE;   // more heads than the static due list holds
-  if (io->N == 0) return LQ_OK;
+  // the list's address first, also for N = 0: a call with no rows, made before a graph capture, sets the device up
+  // so that the captured calls make no runtime query
   int status = LQ_OK;
   int* dlist = scratch_on_current_device(&status);
   if (!dlist) return status;
+  if (io->N == 0) return LQ_OK;
   hipStream_t s = (hipStream_t)stream;
   rc = lq_launch_step(st, io, kda, glb, dlist, s);
   if (rc) return rc;

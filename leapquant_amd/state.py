@@ -106,6 +106,7 @@ class LeapQuantState:
         self._lib = _lib.lib()
         self._vkey = None
         self._skey = None
+        self._scan_src = None
         self._param_f32 = {}
 
     def _as_f32(self, t):
@@ -217,12 +218,24 @@ class LeapQuantState:
             raise ValueError("a: bf16 with N * HV%s = %d elements expected, got %s with %d"
                              % (" * K" if KA > 1 else "", N * self.HV * KA, a.dtype, a.numel()))
 
+    def _struct_scan(self, ssm):
+        """lq_state of this layer without the due flag: a flush through it checks hcnt of every listed row, and
+        leaves the flag as it is."""
+        st = self._struct(ssm)
+        if self._scan_src is not st:
+            self._st_scan = _lib.LqState.from_buffer_copy(st)
+            self._st_scan.ctl = None
+            self._scan_src = st
+        return self._st_scan
+
     def flush(self, ssm, idx):
-        """The end-of-window flush of the rows idx alone, as decode() runs it after its step (the due flag lets a
-        flush with nothing due return at once)."""
+        """The end-of-window flush of the due heads (hcnt == L) of the rows idx, as the reference's flush finds them
+        (kernels.py:1200).  It reads hcnt of every listed row rather than the due flag the decode steps raise: a head
+        that a deferred decode left full may sit in a slot that an earlier flush of other rows did not cover (that
+        flush cleared the flag), and it must still be flushed here."""
         idx = idx if idx.dtype == torch.int32 else idx.to(torch.int32)
         idx = idx.contiguous()
-        st = self._struct(ssm)
+        st = self._struct_scan(ssm)
         stream = ctypes.c_void_p(torch.cuda.current_stream(idx.device).cuda_stream)
         _lib.check(self._lib.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), idx.shape[0], 1 if self.kda else 0,
                                       ctypes.c_float(self.qmax), stream), "lq_flush")

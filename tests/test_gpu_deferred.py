@@ -88,3 +88,26 @@ def test_deferred_head_settled_by_dequantize():
     torch.cuda.synchronize()
     for s in (1, 3):
         assert _bytes_equal(pi[0][s], pd[0][s]), s
+
+
+@pytest.mark.parametrize("settle", ["dequantize", "flush"])
+def test_deferred_heads_settled_across_partial_calls(settle):
+    """Deferred heads in three slots, settled by two calls over different slots: the first call ([1, 3]) must not
+    leave slot 2's deferred head unflushed for the second ([2]).  Each slot's bytes equal the immediate decode's."""
+    NS, HV, H, L = 4, 4, 2, 16
+    rng, pi, pd = _pair(3300, NS, HV, H, L)
+    idx = np.arange(1, NS)
+    for t in range(L):                                   # the last call fills every window
+        oi, od = _decode_both(np.random.default_rng(200 + t), pi, pd, idx, HV, H)
+        assert torch.equal(oi, od)
+    assert int((pd[1].hcnt[2] == L).sum()) == HV // 2    # slot 2 holds deferred heads
+    for sl in ([1, 3], [2]):
+        t = torch.tensor(sl, dtype=torch.int32, device=G.DEV)
+        for ssm, lq in (pi, pd):
+            getattr(lq, settle)(ssm, t)
+    torch.cuda.synchronize()
+    assert int((pd[1].hcnt == L).sum()) == 0
+    for s in (1, 2, 3):
+        assert _bytes_equal(pi[0][s], pd[0][s]), s
+    for k in ("hcnt", "Wbuf", "Pbuf"):
+        assert torch.equal(getattr(pi[1], k), getattr(pd[1], k)), k

@@ -131,7 +131,9 @@ def test_full_head_left_by_a_flush_of_other_rows_is_recovered():
     io = KN._step_io(mg, ag.reshape(1, HV, 1), bg, Ag, dg, ig, out, lq.kstep_scale)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     _lib.check(_lib.lib().lq_gdn_step(ctypes.byref(lq._struct(ssm)), ctypes.byref(io), stream), "lq_gdn_step")
-    lq.flush(ssm, two)                                   # another row's flush: clears the flag, slot 1 stays full
+    # another row's flush as decode() launches it (through the flagged lq_state): it clears the flag, slot 1 stays full
+    _lib.check(_lib.lib().lq_flush(ctypes.byref(lq._struct(ssm)), KN._p(lq.Q0), KN._p(two), 1, 0,
+                                   ctypes.c_float(lq.qmax), stream), "lq_flush")
     torch.cuda.synchronize()
     assert int(lq.ctl[0]) == 0 and np.all(lq.hcnt[1].cpu().numpy() == L)
     before = G.from_gpu(ssm, lq)

@@ -102,3 +102,46 @@ def test_noalloc_rejects_more_heads_than_its_list_holds():
     with pytest.raises(RuntimeError, match="static due list"):
         _lib.check(-3, "lq_decode_noalloc")
     assert _noalloc(lq, ssm, mixed[:N - 1], a[:N - 1], b[:N - 1], A_log, dt_bias, idx[:N - 1], out[:N - 1]) == 0
+
+
+def test_noalloc_decode_under_graph_capture():
+    """lq_decode_noalloc captured in a graph (after one call with no rows, which sets the device up) and replayed over
+    a window end, each replay on new inputs copied into the captured buffers, against LeapQuantState.decode run eagerly
+    on the same inputs: outputs and state bytes equal after every replay (eager work and synchronisations between the
+    replays)."""
+    L, NS, HV, H = 16, 6, 4, 2
+    rng = np.random.default_rng(1700)
+    st, S, Q0 = make_state(rng, NS, HV, H, L=L)
+    _prestep(rng, st, Q0, False, steps=L // 2, NS=NS, HV=HV, H=H)
+    _to_full_minus_one(rng, st, (1, 2), False, L, HV, H)              # the first replay fills slots 1, 2
+    ssm_a, lq_a = G.to_gpu(st, H=H)
+    ssm_b, lq_b = G.to_gpu(st, H=H)
+    A_log, dt_bias = gate_params(HV)
+    idx = np.array([1, 2, 0, 4, 5, 3], np.int64)
+    mixed, a, b = make_inputs(rng, len(idx), HV, H)
+    mg, ag, bg, Ag, dg, ig = G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx)
+    out_b = torch.empty(len(idx), HV, 128, dtype=torch.bfloat16, device=G.DEV)
+    z = ig[:0]
+    assert _noalloc(lq_b, ssm_b, mg[:0], ag[:0], bg[:0], Ag, dg, z, out_b[:0]) == 0   # no rows: the device set-up
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        rc = _noalloc(lq_b, ssm_b, mg, ag, bg, Ag, dg, ig, out_b)
+    assert rc == 0
+    torch.cuda.synchronize()
+    for t in range(L + 2):                                            # slots 1, 2 fill on replay 0, the others later
+        mixed, a, b = make_inputs(rng, len(idx), HV, H)
+        m2, a2, b2, _, _, _ = G.inputs_gpu(mixed, a, b, A_log, dt_bias, idx)
+        for dst, src in ((mg, m2), (ag, a2), (bg, b2)):
+            dst.copy_(src)
+        out_a = torch.empty_like(out_b)
+        print("no-alloc decode under capture, replay %d" % t, flush=True)
+        lq_a.decode(ssm_a, mg, ag, bg, Ag, dg, ig, out_a)
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, out_b), t
+        assert torch.equal(ssm_a.view(torch.int32), ssm_b.view(torch.int32)), t
+        for key in ("hcnt", "Wbuf", "Pbuf", "Kbuf", "Ubuf"):
+            assert torch.equal(getattr(lq_a, key), getattr(lq_b, key)), (t, key)
+    assert int(lq_b.hcnt[1:].max()) < L
