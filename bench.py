@@ -301,8 +301,9 @@ def flush_quantize_bench(torch, dev, stream):
     slots = torch.arange(1, NS, device=dev, dtype=torch.int32)
     nheads = NSL * HV
     res = {"workload": "BASELINE config 3: 256 x 32 heads of 128 x 128 fp32 states, Student-t(3) x 0.02; flush with "
-                       "64 buffered entries on every head"}
-    for qmax, tag in ((127.0, "int8"), (31.0, "6bit")):
+                       "64 buffered entries on every head; value heads share a key head's window keys (GQA 2, "
+                       "H = 16) or each state has its own window (gqa1: H = 32, the survey's per-head byte count)"}
+    for qmax, tag, H in ((127.0, "int8", 16), (31.0, "6bit", 16), (127.0, "int8_gqa1", 32)):
         lq = LeapQuantState(ssm, H, L=L, R=R, qmax=qmax)
         vw = lq.views(ssm)
         quant = KN.make_quantize(NS, HV, K, V, L, ssm.stride(0), R=R, qmax=qmax)
@@ -311,11 +312,11 @@ def flush_quantize_bench(torch, dev, stream):
             quant(ssm, vw["Sq"], vw["Sk"], vw["Sv"], vw["uq"], lq.Wbuf, lq.Pbuf, lq.hcnt, lq.Q0, slots)
 
         ts = []
-        for r in range(3):
+        for r in range(3 if H == 16 else 1):         # gqa1: the same states, checkpointed for its flush only
             ssm.copy_(S0)                            # the quantize overwrites its input with the checkpoint
             torch.cuda.synchronize()
             ts.append(event_ms(torch, stream, qrun, 1))
-        q_us = sum(ts[1:]) / 2 * 1e3
+        q_us = sum(ts[1:]) / 2 * 1e3 if H == 16 else None
         if tag == "int8":
             # the prefill dequant of the same heads (window empty after the quantize): 19 KiB in, 64 KiB out per head;
             # then the checkpoints again for the flush below
@@ -347,9 +348,11 @@ def flush_quantize_bench(torch, dev, stream):
             tf.append(event_ms(torch, stream, frun, 1))
         f_us = sum(tf[1:]) / 2 * 1e3
         fb = flush_bytes(NSL, HV, H, K, V, R, L)
-        res["quantize_%s_us" % tag] = round(q_us, 1)
-        res["quantize_%s_gbps" % tag] = round(quantize_bytes(nheads, K, V) / (q_us * 1e-6) / 1e9, 1)
+        if q_us is not None:
+            res["quantize_%s_us" % tag] = round(q_us, 1)
+            res["quantize_%s_gbps" % tag] = round(quantize_bytes(nheads, K, V) / (q_us * 1e-6) / 1e9, 1)
         res["flush_%s_us" % tag] = round(f_us, 1)
+        res["flush_%s_bytes" % tag] = fb
         res["flush_%s_gbps" % tag] = round(fb / (f_us * 1e-6) / 1e9, 1)
         del lq, vw
     del S0, ssm

@@ -405,10 +405,12 @@ def due_pairs(st, idx):
     return out
 
 
-def flush(st, Q0, idx, qmax=QMAX, return_debug=False, b_hook=None):
+def flush(st, Q0, idx, qmax=QMAX, return_debug=False, b_hook=None, factors=None):
     """Flush every due (slot, head) in place: rebuild B, one subspace iteration from Q0 with CholeskyQR2, new fp16
     factors, smoothed residual, INT8 (or qmax) codes, window reset.  b_hook (tests only): a function applied to the
-    rebuilt fp16 B [D,V,K] before the subspace step, to measure how the outputs respond to a change of B."""
+    rebuilt fp16 B [D,V,K] before the subspace step, to measure how the outputs respond to a change of B.
+    factors (tests only): fp16 factors (U16 [D,K,R], Q16 [D,V,R]) of the due pairs, in due_pairs order, used in place
+    of the subspace step's own, so that the residual stage can be checked on another implementation's factors."""
     NS, HV, H, K, V, L, R = _dims(st)
     G = HV // H
     kda = st["kda"]
@@ -465,14 +467,19 @@ def flush(st, Q0, idx, qmax=QMAX, return_debug=False, b_hook=None):
         M = np.einsum("dav,dvr->dar", QT, Qh)                                                    # Q_old^T Q
         return fp16(np.einsum("dvc,dvr->dcr", B, Qh) + p * np.einsum("dac,dar->dcr", Uold, M)).astype(np.float64)
 
-    P16 = p_step(Q16)                                                                            # kernels.py:1580-1658
-    M2 = np.einsum("dac,dcr->dar", Uold, P16)                                                    # U_old^T P16
-    Qf = r32(np.einsum("dvc,dcr->dvr", B, P16) + p * np.einsum("dav,dar->dvr", QT, M2))        # kernels.py:1660-1739
-    pr = Qf.astype(np.float64)
-    for _ in range(2):                                                                           # kernels.py:1780-1835
-        pr = cholqr_pass(pr)
-        Q16 = fp16(pr).astype(np.float64)
-    U16 = p_step(Q16)                                                                            # ITERS = 1: U = P16
+    if factors is None:
+        P16 = p_step(Q16)                                                                        # kernels.py:1580-1658
+        M2 = np.einsum("dac,dcr->dar", Uold, P16)                                                # U_old^T P16
+        Qf = r32(np.einsum("dvc,dcr->dvr", B, P16) + p * np.einsum("dav,dar->dvr", QT, M2))    # kernels.py:1660-1739
+        pr = Qf.astype(np.float64)
+        for _ in range(2):                                                                       # kernels.py:1780-1835
+            pr = cholqr_pass(pr)
+            Q16 = fp16(pr).astype(np.float64)
+        U16 = p_step(Q16)                                                                        # ITERS = 1: U = P16
+    else:
+        U16 = fp16(factors[0]).astype(np.float64)
+        Q16 = fp16(factors[1]).astype(np.float64)
+        P16 = Qf = None
     # residual E = fp16(pn (fp16(B)/pn + Q_old U_old^T) - Q U^T)   (kernels.py:1888-1928)
     c = (r32(B * rpn[:, None, None]).astype(np.float64) if not kda else B.copy())
     c = c + np.einsum("dav,dac->dvc", QT, Uold)

@@ -11,6 +11,8 @@
 The windows are synthetic but consistent with the state's meaning: unit-norm bf16 keys, bf16 values, GDN weights
 w_j = prod_{i>j} alpha_i with P = prod alpha_i; KDA per-channel step decays e_j = exp(g_j) (fp16) with P = sum g_j.
 """
+import warnings
+
 import numpy as np
 import pytest
 import torch
@@ -86,6 +88,9 @@ def _assert_checkpoints(g, r, slots, qmax=127.0, S=None):
     rel = lambda k: np.abs(gs[k].astype(np.float64) / rs[k] - 1.0).max(axis=-1)
     near = (d.max(axis=(-2, -1)) <= 1) & (rel("Sk") <= 2e-3) & (rel("Sv") <= 2e-3)     # [slot, head]
     assert (~near).sum() <= max(1, 1e-2 * near.size), (~near).sum()
+    if (~near).any():                                   # shown in the run's warnings summary
+        warnings.warn("checkpoints: %d of %d heads beyond 1 LSB / 2e-3 in scale, compared by materialised state"
+                      % (int((~near).sum()), near.size))
     if (~near).any():
         sel = lambda c: {k: v[~near][None] for k, v in c.items()}
         mg, qg, stg = _materialized(sel(gs), qmax)
@@ -104,6 +109,34 @@ def _assert_checkpoints(g, r, slots, qmax=127.0, S=None):
             assert dq.max() <= 1 and (dq > 0).mean() <= 1e-4, (i, dq.max(), (dq > 0).mean())
             np.testing.assert_allclose(sk, gs["Sk"].reshape(-1, K)[i:i + 1024], rtol=1e-5)
             np.testing.assert_allclose(sv, gs["Sv"].reshape((-1, gs["Sv"].shape[-1]))[i:i + 1024], rtol=1e-5)
+
+
+def _assert_flush_pinned(g, pre, Q0, idx, qmax=127.0):
+    """One flush of identical pre-flush states (`pre`, the oracle state before the flush; `g`, the GPU's after it),
+    checked stage by stage.  Factors (U^T | Q^T, fp16) within one fp16 rounding of the oracle's: |diff| <= 2e-3 |x| +
+    2e-4 max |x| per head (an fp32 sum of another order lands on the other side of an fp16 rounding boundary now and
+    then).  Residual stage: the oracle's flush run on the GPU's own factors gives the GPU's codes within 1 LSB on <=
+    0.1 % of the flushed codes and its scales within 1e-3; what remains there is the rebuilt B's own fp16 rounding
+    flips.  Returns the due pairs."""
+    pairs = O.due_pairs(pre, idx)
+    assert pairs
+    s = np.array([p[0] for p in pairs])
+    hv = np.array([p[1] for p in pairs])
+    K = pre["Sk"].shape[-1]
+    ref = O.copy_state(pre)
+    O.flush(ref, Q0, idx, qmax=qmax)
+    ug, ur = g["UQ"][s, hv].astype(np.float64), ref["UQ"][s, hv].astype(np.float64)
+    tol = 2e-3 * np.abs(ur) + 2e-4 * np.abs(ur).max(axis=(-2, -1), keepdims=True)
+    assert np.all(np.abs(ug - ur) <= tol), np.abs(ug - ur).max()
+    pin = O.copy_state(pre)
+    O.flush(pin, Q0, idx, qmax=qmax, factors=(ug[:, :, :K].transpose(0, 2, 1), ug[:, :, K:].transpose(0, 2, 1)))
+    d = np.abs(g["Sq"][s, hv].astype(np.int32) - pin["Sq"][s, hv].astype(np.int32))
+    assert d.max() <= 1 and (d > 0).mean() <= 1e-3, (d.max(), (d > 0).mean())
+    np.testing.assert_allclose(g["Sk"][s, hv], pin["Sk"][s, hv], rtol=1e-3)
+    np.testing.assert_allclose(g["Sv"][s, hv], pin["Sv"][s, hv], rtol=1e-3)
+    for k in ("hcnt", "Wbuf", "Pbuf"):
+        assert np.array_equal(g[k][s, hv], ref[k][s, hv]), k
+    return pairs
 
 
 @pytest.mark.parametrize("kda", [False, True])
@@ -145,24 +178,45 @@ def test_decode_at_full_size_matches_oracle(kda):
     assert np.array_equal(G.from_gpu(ssm, lq)["hcnt"], st["hcnt"])
 
 
+_C3 = {}
+
+
+def _config3(qmax):
+    """Config 3's fp32 states (seeded) and the oracle's checkpoint of them (cached: the GQA legs share it)."""
+    if qmax not in _C3:
+        rng = np.random.default_rng(1003)
+        NSL, HV = 256, 32
+        S = (0.02 * rng.standard_t(3, (NSL + 1, HV, 128, 128))).astype(np.float32)
+        st = O.new_state(NSL + 1, HV, 16, L=64)
+        print("config 3 (qmax %g): oracle quantize of %d heads" % (qmax, NSL * HV), flush=True)
+        O.quantize(st, S, O.make_q0(128, 4), np.arange(1, NSL + 1, dtype=np.int64), qmax=qmax)
+        _C3[qmax] = (S, st)
+    return _C3[qmax]
+
+
+@pytest.mark.parametrize("H", [16, 32])
 @pytest.mark.parametrize("qmax", [127.0, 31.0])
-def test_config3_quantize_and_flush_at_full_size(qmax):
+def test_config3_quantize_and_flush_at_full_size(qmax, H):
     """Config 3: 256 x 32 Student-t(3) x 0.02 heads, INT8 and 6-bit; quantize of every head vs the oracle; all-due
-    flush (64 buffered entries per head) vs the oracle on 512 heads and through properties of the codes on all 8192."""
-    rng = np.random.default_rng(1003)
-    NSL, HV, H, L = 256, 32, 16, 64
+    flush (64 buffered entries per head) vs the oracle on 512 heads and through properties of the codes on all 8192.
+    H = 32: every state has its own window of 64 entries (GQA 1: the decode steps, then the standalone persistent
+    flush takes the 8192 due heads); H = 16: two value heads share a key head's window keys (GQA 2: the one-launch
+    decode flushes them)."""
+    rng = np.random.default_rng(1003 + H)
+    NSL, HV, L = 256, 32, 64
     NS = NSL + 1
-    S = (0.02 * rng.standard_t(3, (NS, HV, 128, 128))).astype(np.float32)
+    S, st16 = _config3(qmax)
     st = O.new_state(NS, HV, H, L=L)
+    for k in ("Sq", "Sk", "Sv", "UQ"):
+        st[k] = st16[k].copy()
     Q0 = O.make_q0(128, 4)
     idx = np.arange(1, NS, dtype=np.int64)
-    print("config 3 (qmax %g): oracle quantize of %d heads" % (qmax, NSL * HV), flush=True)
-    O.quantize(st, S, Q0, idx, qmax=qmax)
     ssm, lq = G.to_gpu(st, qmax=qmax)
-    ssm.copy_(torch.from_numpy(S))
-    lq.quantize(ssm, torch.from_numpy(idx).to(G.DEV))
-    g = G.from_gpu(ssm, lq)
-    _assert_checkpoints(g, st, slice(1, NS), qmax=qmax, S=S[1:])
+    if H == 16:                                         # the quantize of every head (the same states at both H)
+        ssm.copy_(torch.from_numpy(S))
+        lq.quantize(ssm, torch.from_numpy(idx).to(G.DEV))
+        g = G.from_gpu(ssm, lq)
+        _assert_checkpoints(g, st, slice(1, NS), qmax=qmax, S=S[1:])
 
     # the flush of a full window on every head, from the oracle's checkpoint on both sides
     _fill_windows(rng, st, L - 1, kda=False)
@@ -170,7 +224,7 @@ def test_config3_quantize_and_flush_at_full_size(qmax):
     A_log, dt_bias = gate_params(HV)
     mixed, a, b = make_inputs(rng, NSL, HV, H)
     G.load_state(lq, ssm, st)
-    print("config 3 (qmax %g): oracle step + flush of %d heads" % (qmax, len(sub) * HV), flush=True)
+    print("config 3 (qmax %g, H %d): oracle step + flush of %d heads" % (qmax, H, len(sub) * HV), flush=True)
     O.gdn_step(st, mixed, a, b, A_log, dt_bias, idx, qmax=qmax)    # fills every window (64 entries)
     before = O.copy_state(st)
     O.flush(st, Q0, sub, qmax=qmax)

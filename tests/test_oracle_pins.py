@@ -417,6 +417,34 @@ def test_flush_fully_decayed_and_idle_heads():
     assert np.abs(O.materialize(st)[1] - S).max() < 1e-2 * np.abs(S).max()
 
 
+@pytest.mark.parametrize("kda", [False, True])
+def test_flush_on_given_factors(kda):
+    """flush(factors=...) -- the residual stage run on given fp16 factors, as the GPU tests run it on the GPU's --
+    reproduces the flush bit for bit when handed the flush's own factors, and with factors nudged by one fp16 ulp in one
+    entry the codes it gives differ (so the argument is used, not ignored)."""
+    rng = np.random.default_rng(31 + kda)
+    NS, HV, L = 4, 2, 16
+    H = HV if kda else 1
+    st, _, Q0 = make_state(rng, NS, HV, H, L=L, kda=kda)
+    A_log, dt_bias = gate_params(HV, 128, kda)
+    idx = np.array([1, 3])
+    for _ in range(L):
+        mixed, a, b = make_inputs(rng, len(idx), HV, H, kda=kda)
+        (O.kda_step if kda else O.gdn_step)(st, mixed, a, b, A_log, dt_bias, idx)
+    pre = O.copy_state(st)
+    a_ = O.copy_state(pre)
+    dbg = O.flush(a_, Q0, idx, return_debug=True)
+    b_ = O.copy_state(pre)
+    O.flush(b_, Q0, idx, factors=(dbg["U16"], dbg["Q16"]))
+    for k in ("Sq", "Sk", "Sv", "UQ", "Wbuf", "Pbuf", "hcnt"):
+        assert np.array_equal(a_[k], b_[k]), k
+    U2 = dbg["U16"].copy()
+    U2[0, 5, 0] = float(np.nextafter(np.float16(U2[0, 5, 0]), np.float16(np.inf)))
+    c_ = O.copy_state(pre)
+    O.flush(c_, Q0, idx, factors=(U2, dbg["Q16"]))
+    assert not np.array_equal(c_["UQ"], a_["UQ"])
+
+
 # ------------------------------------------------------------------------------------------------ quantize / lowrank
 QUANT_CASES = [(q, h, d, 4) for q in (127.0, 31.0) for h in (False, True) for d in GDN_DIMS] + \
     [(127.0, False, (128, 128), 8), (127.0, True, (128, 128), 16)]          # ranks a step can read (kernels.py:63)
