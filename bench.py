@@ -771,7 +771,15 @@ def main():
     reset_windows(lq)                                             # every window back to h = 0
     gsteps = capture(lambda i: step_only(i, i % NSET), CH)
     gflush = [capture(lambda i, kk=kk: flush_only(kk), 1) for kk in range(NSET)]
-    gidle = capture(lambda i: lq.flush(ssm, sets[0]), CH)         # 64 flush launches with no head due, as decode runs them
+    def idle_flush(i):                 # lq_flush through the layer's flagged lq_state, as a two-launch decode runs it
+        import ctypes
+        from leapquant_amd import _lib, kernels as KN
+        st_ = lq._struct(ssm)
+        _lib.check(_lib.lib().lq_flush(ctypes.byref(st_), KN._p(lq.Q0), KN._p(sets[0]), B, 0,
+                                       ctypes.c_float(lq.qmax),
+                                       ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)), "lq_flush")
+
+    gidle = capture(idle_flush, CH)                               # 64 flush launches with no head due
     torch.cuda.synchronize()
     rounds = 3
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(NSET + 2)] for _ in range(rounds)]

@@ -26,7 +26,7 @@
 extern "C" {
 #endif
 
-#define LQ_ABI_VERSION 4
+#define LQ_ABI_VERSION 5
 #define LQ_SCHED_INTS 512   /* ints of lq_state.sched: eight counters, 256 bytes apart */
 
 enum lq_status {
@@ -132,6 +132,14 @@ int lq_gdn_decode_deferred(const lq_state* st, const lq_step_io* io, const lq_co
  * idx, o) (kernels.py:694-1075, launched at state.py:108-109).  Same limits as lq_gdn_step, with K = V = 128 and
  * R <= 4 only (kernels.py:727, 1036). */
 int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, void* stream);
+
+/* KDA decode call: the step of every row (gate as lq_kda_step), then the end-of-window flush of the heads whose window
+ * it filled (codes in [-qmax, qmax], qmax = st->qmax, 0 meaning 127) -- what lq_kda_step followed by lq_flush (kda = 1)
+ * computes, in one call.  Replaces make_kda_step(...)(...) followed by make_flush(..., KDA=True)(...) as
+ * LeapQuantState.decode launches them (/root/reference/leapquant/state.py:99-116; kernels.py:694-1075, 1077-2033).
+ * Two launches (the step, then the persistent flush, which returns at once when no step raised the due flag st->ctl):
+ * one C call per layer and decode call, as lq_gdn_decode.  Same limits as lq_kda_step and lq_flush. */
+int lq_kda_decode(const lq_state* st, const lq_step_io* io, float glb, const float* Q0, void* stream);
 
 /* End-of-window flush of every (idx[n] > 0, hv) head whose window is full (hcnt == L): rebuild, one subspace
  * iteration from Q0 [V][R] with CholeskyQR2, fp16 factors, smoothed residual requantised to codes in [-qmax, qmax]

@@ -5,7 +5,7 @@ import os
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "_build", "liblq.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 SCHED_INTS = 512           # include/lq.h: LQ_SCHED_INTS
 
 c_void_p, c_int, c_float, c_ll = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_longlong
@@ -34,6 +34,7 @@ SIGNATURES = {
     "lq_gdn_step": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_void_p]),
     "lq_gdn_step_conv": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv), c_void_p]),
     "lq_kda_step": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_float, c_void_p]),
+    "lq_kda_decode": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), c_float, c_void_p, c_void_p]),
     "lq_gdn_decode": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv), c_void_p,
                               c_void_p]),
     "lq_gdn_decode_deferred": (c_int, [ctypes.POINTER(LqState), ctypes.POINTER(LqStepIO), ctypes.POINTER(LqConv),

@@ -10,6 +10,8 @@
 // fixed grid is graph-capture safe.
 #include "lq_flush_core.h"
 
+#include <type_traits>
+
 namespace {
 
 using namespace lqf;
@@ -38,14 +40,16 @@ __device__ __forceinline__ unsigned unit_mask(const lq_state& st, int slot, int 
   return m;
 }
 
-template <int U = 1, class Head>
+// DYN: the dynamic schedule (the launch has checked flush_dynamic: counters given, more candidates than workgroups);
+// otherwise the static one.  Each is its own kernel instance.
+template <int U = 1, bool DYN = false, class Head>
 __device__ void flush_scan(unsigned long long& due, const lq_state& st, const int* __restrict__ idx, int N,
                            Head head) {
   const int NU = st.HV / U;                           // units per row
   const int total = N * NU;
   const int stride = gridDim.x;
   if (st.ctl && __hip_atomic_load(st.ctl, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0) return;   // uniform: nothing due
-  if (st.sched && total > stride && total < (1 << lqf::SCHED_BITS)) {
+  if constexpr (DYN) {
     // dynamic schedule: candidate b first, then whichever the workgroup's counter hands out (each head takes the next
     // one near its end and leaves it in `due`); a candidate that is not due takes the next at once
     if (threadIdx.x == 0) due = blockIdx.x;
@@ -87,11 +91,14 @@ __device__ void flush_scan(unsigned long long& due, const lq_state& st, const in
         if (threadIdx.x == 0) due = m;
       }
       __syncthreads();
-      unsigned long long m = due;
-      __syncthreads();
-      while (m) {
+      // the pass's due mask stays in the shared word (the static schedule passes no counters, so no head writes it):
+      // nothing of the pass is held in registers across a head
+      for (;;) {
+        const unsigned long long m = due;
+        __syncthreads();                              // every thread has the mask before thread 0 rewrites it
+        if (!m) break;
         const int b = __ffsll((long long)m) - 1;
-        m &= m - 1;
+        if (threadIdx.x == 0) due = m & (m - 1);      // read again after the head's last barrier
         const int p = base + stride * b;
         const int n = p / NU, u = p - n * NU;
         const int slot = idx[n];
@@ -146,7 +153,12 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
   }
 }
 
-template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
+// MODE: how the workgroups find their heads -- FS_STATIC / FS_DYNAMIC (flush_scan with the static or the dynamic
+// schedule) or FS_LISTED (the due list of lq_decode_noalloc, flush_listed).  Each is its own kernel instance, so that
+// no path's registers weigh on another's (one kernel holding all three spilled up to 64 bytes per lane more).
+enum { FS_STATIC = 0, FS_DYNAMIC = 1, FS_LISTED = 2 };
+
+template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4, int MODE = FS_STATIC>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
@@ -154,18 +166,18 @@ void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restri
   auto head = [&](int slot, int hv, unsigned, int* sched) {
     flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax, sched);
   };
-  if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
-  else flush_scan(sh.due, st, idx, N, head);
+  if constexpr (MODE == FS_LISTED) flush_listed(sh.due, st, idx, N, dlist, head);
+  else flush_scan<1, MODE == FS_DYNAMIC>(sh.due, st, idx, N, head);
 }
 
-template <int K_ = KD, int V_ = VD>
+template <int K_ = KD, int V_ = VD, int MODE = FS_STATIC>
 __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush4_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                    int* dlist) {
   __shared__ FlushShared4 sh;
   auto head = [&](int slot, int hv, unsigned, int* sched) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax, sched); };
-  if (dlist) flush_listed(sh.due, st, idx, N, dlist, head);
-  else flush_scan(sh.due, st, idx, N, head);
+  if constexpr (MODE == FS_LISTED) flush_listed(sh.due, st, idx, N, dlist, head);
+  else flush_scan<1, MODE == FS_DYNAMIC>(sh.due, st, idx, N, head);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -656,7 +668,7 @@ __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float*
   __syncthreads();                                    // LDS reuse by the next unit of this workgroup
 }
 
-template <int V_, int HP>
+template <int V_, int HP, int MODE = FS_STATIC>
 __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush64_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                     int* dlist) {
@@ -664,8 +676,8 @@ void flush64_kernel(lq_state st, const float* __restrict__ Q0, const int* __rest
   auto head = [&](int slot, int hv0, unsigned mask, int* sched) {
     flush_head64<V_, HP>(sh, st, Q0, slot, hv0, mask, qmax, sched);
   };
-  if (dlist) flush_listed<HP>(sh.due, st, idx, N, dlist, head);
-  else flush_scan<HP>(sh.due, st, idx, N, head);
+  if constexpr (MODE == FS_LISTED) flush_listed<HP>(sh.due, st, idx, N, dlist, head);
+  else flush_scan<HP, MODE == FS_DYNAMIC>(sh.due, st, idx, N, head);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1534,20 +1546,48 @@ int lq_check_flush(const lq_state* st, const float* Q0, const int* idx, int N, i
   return LQ_OK;
 }
 
+// the kernel instance of a flush of `units` candidates on `grid` workgroups: listed, or the dynamic schedule when
+// the counters are given and there are more candidates than workgroups (each workgroup then takes more than its
+// first), else the static one
+template <class F>
+static void with_mode(const lq_state* st, const int* dlist, int units, unsigned grid, F&& launch) {
+  if (dlist) launch(std::integral_constant<int, FS_LISTED>{});
+  else if (st->sched && units > (int)grid && units < (1 << SCHED_BITS)) launch(std::integral_constant<int, FS_DYNAMIC>{});
+  else launch(std::integral_constant<int, FS_STATIC>{});
+}
+
 int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, int kda, float qmax, int* dlist,
                     hipStream_t s) {
   if (N == 0) return LQ_OK;
   const int total = N * st->HV;
   const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
   const dim3 g4((unsigned)(total < 4 * num_cus() ? total : 4 * num_cus()));  // four-wave flush: four per CU
-  if (kda) flush_kernel<true><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if (st->K == KD && st->R > 4) flush_kernel<false, KD, VD, 8><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if (st->K == KD) flush4_kernel<><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if (st->V == VD) flush64_kernel<128, 1><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  else if ((st->HV / st->H) % 2 == 0) {               // two heads of one key head per workgroup (kernels.py:1095-1097)
+  if (kda) {
+    with_mode(st, dlist, total, g.x, [&](auto m) {
+      flush_kernel<true, KD, VD, 4, decltype(m)::value><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  } else if (st->K == KD && st->R > 4) {
+    with_mode(st, dlist, total, g.x, [&](auto m) {
+      flush_kernel<false, KD, VD, 8, decltype(m)::value><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  } else if (st->K == KD) {
+    with_mode(st, dlist, total, g4.x, [&](auto m) {
+      flush4_kernel<KD, VD, decltype(m)::value><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  } else if (st->V == VD) {
+    with_mode(st, dlist, total, g4.x, [&](auto m) {
+      flush64_kernel<128, 1, decltype(m)::value><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  } else if ((st->HV / st->H) % 2 == 0) {             // two heads of one key head per workgroup (kernels.py:1095-1097)
     const dim3 gp((unsigned)(total / 2 < 4 * num_cus() ? total / 2 : 4 * num_cus()));
-    flush64_kernel<64, 2><<<gp, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
-  } else flush64_kernel<64, 1><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    with_mode(st, dlist, total / 2, gp.x, [&](auto m) {
+      flush64_kernel<64, 2, decltype(m)::value><<<gp, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  } else {
+    with_mode(st, dlist, total, g4.x, [&](auto m) {
+      flush64_kernel<64, 1, decltype(m)::value><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    });
+  }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

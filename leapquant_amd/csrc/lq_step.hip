@@ -1059,4 +1059,16 @@ extern "C" int lq_kda_step(const lq_state* st, const lq_step_io* io, float glb, 
   return lq_launch_step(st, io, 1, glb, nullptr, (hipStream_t)stream);
 }
 
+extern "C" int lq_kda_decode(const lq_state* st, const lq_step_io* io, float glb, const float* Q0, void* stream) {
+  int rc = lq_check_step(st, io);
+  if (rc) return rc;
+  if (!st->Gbuf || st->K != KD || st->V != VD || st->R > 4) return LQ_ERR_ARG;
+  const float qmax = st->qmax > 0.f ? st->qmax : LQ_QMAX;
+  if ((rc = lq_check_flush(st, Q0, io->idx, io->N, 1, qmax))) return rc;
+  if (io->N == 0) return LQ_OK;
+  hipStream_t s = (hipStream_t)stream;
+  if ((rc = lq_launch_step(st, io, 1, glb, nullptr, s))) return rc;
+  return lq_launch_flush(st, Q0, io->idx, io->N, 1, qmax, nullptr, s);
+}
+
 extern "C" int lq_abi_version(void) { return LQ_ABI_VERSION; }

@@ -139,8 +139,8 @@ class LeapQuantState:
         return self._st
 
     def decode(self, ssm, mixed, a, b, A_log, dt_bias, idx, out):
-        """One decode token per row, then the end-of-window flush of the heads whose window became full (GDN: one
-        lq_gdn_decode call; KDA: the step, then the flush).
+        """One decode token per row, then the end-of-window flush of the heads whose window became full (one C call:
+        lq_gdn_decode, or lq_kda_decode).
         a: GDN (N, HV) | KDA (N, HV, K) raw gate;  dt_bias: GDN (HV,) | KDA (HV*K,)."""
         A_log = self._as_f32(A_log)
         dt_bias = self._as_f32(dt_bias)
@@ -164,11 +164,9 @@ class LeapQuantState:
         io = KN._step_io(mixed, a, b, A_log, dt_bias, idx, out, self.kstep_scale)
         stream = ctypes.c_void_p(torch.cuda.current_stream(mixed.device).cuda_stream)
         L = self._lib
-        if self.kda:
-            _lib.check(L.lq_kda_step(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(self.glb), stream),
-                       "lq_kda_step")
-            _lib.check(L.lq_flush(ctypes.byref(st), KN._p(self.Q0), KN._p(idx), N, 1, ctypes.c_float(self.qmax),
-                                  stream), "lq_flush")
+        if self.kda:                 # the step, then the flush of the heads it fills
+            _lib.check(L.lq_kda_decode(ctypes.byref(st), ctypes.byref(io), ctypes.c_float(self.glb), KN._p(self.Q0),
+                                       stream), "lq_kda_decode")
         else:                        # step + flush of the heads it fills (one launch for 128 x 128 heads, GQA 2)
             fn = L.lq_gdn_decode_deferred if self.defer_flush else L.lq_gdn_decode
             _lib.check(fn(ctypes.byref(st), ctypes.byref(io), None, KN._p(self.Q0), stream), "lq_gdn_decode")

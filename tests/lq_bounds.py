@@ -70,7 +70,7 @@ def _arg(x):
 class CheckingLib:
     """Drop-in for the ctypes handle of liblq.so: checks the footprint of every call, launches nothing."""
 
-    ABI = 4
+    ABI = 5
 
     def __init__(self):
         self.storages = Storages()
@@ -187,6 +187,16 @@ class CheckingLib:
             return rc
         io = _arg(io)
         return self._per_slot("lq_gdn_decode flush", st, ctypes.c_void_p(io.idx), io.N, False, False, Q0=Q0)
+
+    def lq_kda_decode(self, st, io, glb, Q0, stream):
+        """The KDA step, then the flush of the rows of the call."""
+        rc = self._step("lq_kda_decode", st, io, True)
+        if rc:
+            return rc
+        st_, io_ = _arg(st), _arg(io)
+        if st_.R > 4:
+            return -1
+        return self._per_slot("lq_kda_decode flush", st, ctypes.c_void_p(io_.idx), io_.N, True, False, Q0=Q0)
 
     def lq_gdn_decode_deferred(self, st, io, cv, Q0, stream):
         """The same footprint as lq_gdn_decode: a deferred head is flushed by the next call that steps its slot, which
