@@ -40,7 +40,7 @@ enum lq_status {
 typedef struct lq_state {
   void* ssm;              /* fp32 [NS][HV][V][K] at slot 0 (the tensor's data pointer, storage offset included) */
   long long slot_stride;  /* SS: floats between consecutive slots (>= HV*V*K) */
-  void* Kbuf;             /* bf16 [NS][H][L][K] */
+  void* Kbuf;             /* bf16 [NS][H][L][K]   (Kbuf, Ubuf, Gbuf: 16-byte aligned, read by whole-row 16-byte loads) */
   void* Ubuf;             /* bf16 [NS][HV][L][V] */
   float* Wbuf;            /* [NS][HV][L] */
   float* Pbuf;            /* [NS][HV][KA] */
@@ -201,7 +201,7 @@ int lq_conv_update(const lq_conv* cv, const void* x, void* out, const int* idx, 
 
 /* Baseline for the measurements (no reference counterpart): the same GDN decode step on a dense state S
  * [NS][HV][V][K] stored as bf16 (state_dtype 0) or fp32 (state_dtype 1), updated in place:
- * S' = alpha S + u k^T, u = beta (v - alpha S k), o = S' q. */
+ * S' = alpha S + u k^T, u = beta (v - alpha S k), o = S' q.  S and io->mixed 16-byte aligned. */
 int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, int K, int V, const lq_step_io* io, void* stream);
 
 #ifdef __cplusplus

@@ -233,6 +233,13 @@ __device__ __forceinline__ void note_due(int* ctl, int* dlist, int p) {
   }
 }
 
+// The window buffers are read by 16-byte loads and direct-to-LDS loads of whole rows: their bases must be 16-byte
+// aligned (rows are K or V bf16 long, multiples of 16 bytes).  torch's allocations are; a view at an odd offset is not.
+__host__ __device__ inline bool buffers_aligned(const lq_state* st) {
+  const uintptr_t m = (uintptr_t)st->Kbuf | (uintptr_t)st->Ubuf | (uintptr_t)st->Gbuf;
+  return (m & 15) == 0;
+}
+
 // code range of the stored checkpoint (lq_state.qmax; 0: INT8)
 __device__ __forceinline__ float code_range(const lq_state& st) { return st.qmax > 0.f ? st.qmax : LQ_QMAX; }
 

@@ -155,6 +155,8 @@ extern "C" int lq_dense_step(void* S, int state_dtype, int NS, int HV, int H, in
   if (!S || !io || K != KD || V != VD || H <= 0 || HV <= 0 || HV % H != 0 || NS <= 0 || io->N < 0) return LQ_ERR_ARG;
   if (state_dtype != 0 && state_dtype != 1) return LQ_ERR_ARG;
   if (io->N == 0) return LQ_OK;
+  // q, k and the state rows are read by 16-byte loads: 16-byte aligned bases (the rows are multiples of 16 bytes)
+  if (((uintptr_t)S & 15) || ((uintptr_t)io->mixed & 15)) return LQ_ERR_ARG;
   const int G = HV / H;
   dim3 grid((unsigned)(io->N * H));
   hipStream_t s = (hipStream_t)stream;

@@ -1534,6 +1534,7 @@ int check_block_state(const lq_state* st, bool need_buf, bool kda, int rmax) {
   if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3)) return LQ_ERR_ARG;
   if (((uintptr_t)st->ssm & 15) != 0) return LQ_ERR_ARG;
   if (need_buf && (!st->Kbuf || !st->Ubuf)) return LQ_ERR_ARG;
+  if (!buffers_aligned(st)) return LQ_ERR_ARG;
   return LQ_OK;
 }
 

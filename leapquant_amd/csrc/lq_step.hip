@@ -955,6 +955,7 @@ int lq_check_step(const lq_state* st, const lq_step_io* io) {
   // 16-byte loads of the int8 rows and of the scale / factor block need a 16-byte aligned block start
   if (st->slot_stride < (long long)st->HV * st->V * st->K || (st->slot_stride & 3) || ((uintptr_t)st->ssm & 15))
     return LQ_ERR_ARG;
+  if (!buffers_aligned(st)) return LQ_ERR_ARG;
   if (!(st->qmax == 0.f || (st->qmax >= 1.f && st->qmax <= 127.f))) return LQ_ERR_ARG;
   if (io->N > 0 && (!io->mixed || !io->a || !io->b || !io->A_log || !io->dt_bias || !io->idx || !io->out))
     return LQ_ERR_ARG;

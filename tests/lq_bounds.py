@@ -75,6 +75,7 @@ class CheckingLib:
     def __init__(self):
         self.storages = Storages()
         self.calls = []
+        self.alignments = []                 # byte address of every pointer a state / step call was given
 
     # ---- helpers --------------------------------------------------------------------------------------------------
     def _state_ok(self, st, need_buf=True, kda=False):
@@ -86,6 +87,8 @@ class CheckingLib:
         if st.slot_stride < st.HV * st.V * st.K or st.slot_stride % 4 or not st.ssm or st.ssm % 16:
             return False
         if not st.hcnt or not st.Wbuf or not st.Pbuf or (need_buf and (not st.Kbuf or not st.Ubuf)):
+            return False
+        if ((st.Kbuf or 0) | (st.Ubuf or 0) | (st.Gbuf or 0)) % 16:      # 16-byte row loads and LDS DMA
             return False
         return True
 
@@ -153,6 +156,7 @@ class CheckingLib:
     def _step(self, name, st, io, kda, cv=None):
         st, io = _arg(st), _arg(io)
         self.calls.append(name)
+        self.alignments += [p for p in (st.ssm, st.Kbuf, st.Ubuf, st.Gbuf, io.mixed, io.out) if p]
         if not self._state_ok(st, kda=kda) or not (st.qmax == 0 or 1 <= st.qmax <= 127) or io.N < 0:
             return -1
         if kda and (not st.Gbuf or (st.K, st.V) != (128, 128)):
@@ -286,6 +290,8 @@ class CheckingLib:
         if io.N == 0:
             return 0
         base = _arg(S_).value if hasattr(_arg(S_), "value") else _arg(S_)
+        if base % 16 or io.mixed % 16:                 # 16-byte loads of the state rows and of q, k
+            return -1
         esz = 2 if dtype == 0 else 4
         S = self.storages
         MIX = 2 * H * K + HV * V

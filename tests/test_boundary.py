@@ -62,7 +62,8 @@ def _io(**kw):
 
 BAD_STATES = [dict(K=96), dict(V=64), dict(K=32, V=32), dict(L=0), dict(L=65), dict(R=0), dict(R=17), dict(H=0), dict(HV=3),
               dict(NS=0), dict(slot_stride=100), dict(slot_stride=4 * 128 * 128 + 1), dict(ssm=8), dict(ssm=None),
-              dict(hcnt=None), dict(Wbuf=None)]
+              dict(hcnt=None), dict(Wbuf=None), dict(Kbuf=40), dict(Ubuf=56), dict(Gbuf=104)]   # last three: not
+# 16-byte aligned (the window rows are read by 16-byte and direct-to-LDS loads)
 BAD_STEP_STATES = [dict(qmax=0.5), dict(qmax=128.0), dict(qmax=-31.0), dict(qmax=float("nan"))]
 
 
@@ -205,6 +206,9 @@ def test_other_argument_errors(lib):
     assert lib.lq_dense_step(p, 2, 8, 4, 2, 128, 128, ctypes.byref(io), z) == -1
     assert lib.lq_dense_step(None, 0, 8, 4, 2, 128, 128, ctypes.byref(io), z) == -1
     assert lib.lq_dense_step(p, 0, 8, 4, 2, 128, 128, ctypes.byref(io), z) == 0
+    # 16-byte loads of q, k and the state rows: misaligned bases are refused before any launch
+    assert lib.lq_dense_step(p, 0, 8, 4, 2, 128, 128, ctypes.byref(_io(N=1, mixed=24)), z) == -1
+    assert lib.lq_dense_step(ctypes.c_void_p(8), 0, 8, 4, 2, 128, 128, ctypes.byref(_io(N=1)), z) == -1
 
 
 def _conv(**kw):

@@ -92,3 +92,55 @@ def test_checking_lib_catches_an_out_of_range_call(checked):
     import ctypes
     with pytest.raises(lq_bounds.OutOfBounds, match="ssm block"):
         checked.lq_flush(ctypes.byref(bad), KN._p(st.Q0), KN._p(idx), 1, 0, ctypes.c_float(127.0), None)
+
+
+def _op_signatures(layers, B, deferred=True):
+    """The aten ops of one decode step of the stack (through the plugin, after its checkpoints are written), each as
+    (op, per tensor operand: dtype, contiguous, a transposed 2-D view, byte offset of the view modulo 16), and the
+    liblq calls of that step with the byte alignment of every pointer they were handed."""
+    from torch.utils import _pytree as pytree
+    from torch.utils._python_dispatch import TorchDispatchMode
+    from leapquant_amd import state as S
+
+    class Rec(TorchDispatchMode):
+        def __init__(self):
+            super().__init__()
+            self.ops = []
+
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            kwargs = kwargs or {}
+            ts = [a for a in pytree.tree_leaves((args, kwargs)) if isinstance(a, torch.Tensor)]
+            self.ops.append((str(func), tuple(
+                (str(t.dtype), t.is_contiguous(), t.dim() == 2 and t.stride(0) == 1 and t.shape[0] > 1,
+                 (t.storage_offset() * t.element_size()) % 16) for t in ts)))
+            return func(*args, **kwargs)
+
+    torch.manual_seed(0)
+    stack, idx = GS.build(layers, B=B, device="cpu")
+    for l in stack:
+        S.get_state(l.attn, l.ssm, H=l.H, defer_flush=deferred).quantize(l.ssm, idx)
+    x = torch.randn(B, 2048).to(torch.bfloat16)
+    rec = Rec()
+    with torch.no_grad(), rec:
+        GS.run(stack, x)
+    return rec.ops
+
+
+def test_config4_step_differs_from_the_passing_stack_only_in_sizes(checked):
+    """One decode step of BASELINE config 4 (24 layers, B = 64) against the stack that runs on the GPU in
+    tests/test_gpu_config4.py (4 layers, B = 8): the same aten ops in the same order per layer, with the same dtypes,
+    layouts (no transposed operand, in particular no bf16 product with a transposed right operand) and view offsets,
+    and the same liblq entry points with 16-byte aligned pointers.  What config 4 adds is sizes: the batch of the
+    projections' bf16 GEMMs (M = 64), of the conv update and of the two liblq calls per layer."""
+    big = _op_signatures(24, 64)
+    n_big = len(checked.calls)
+    small = _op_signatures(4, 8)
+    per_layer = lambda ops, L: ops[: len(ops) // L]
+    assert len(big) % 24 == 0 and len(small) % 4 == 0
+    assert per_layer(big, 24) == per_layer(small, 4)
+    assert big == per_layer(big, 24) * 24
+    mm = [o for o in big if "mm" in o[0]]
+    assert mm and all(not any(t[2] for t in o[1]) for o in mm)          # no transposed GEMM operand
+    calls = checked.calls[n_big - 48:n_big]                            # one step of 24 layers: decode + its flush
+    assert calls == ["lq_gdn_decode_deferred", "lq_gdn_decode_deferred flush"] * 24
+    assert all(a % 16 == 0 for a in checked.alignments), sorted(set(a % 256 for a in checked.alignments))
