@@ -57,8 +57,12 @@ def _compile_link(cc, flags, sources, lib, verbose):
 def build(verbose=False):
     os.makedirs(OUT, exist_ok=True)
     cc = hipcc()
+    # -amdgpu-atomic-optimizer-strategy=None: every atomic of the library is issued by one lane, so the optimizer's
+    # wave-wide rewrite buys nothing, and its result broadcast (a readfirstlane right after the atomic) makes the wave
+    # wait for the atomic's return at once -- the flush's schedule take would then hold wave 0 for its round trip
     flags = ["--offload-arch=%s" % ARCH, "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function", "-Wno-inline-asm",
-             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+             "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+             "-mllvm", "-amdgpu-atomic-optimizer-strategy=None"]
     _compile_link(cc, flags, SOURCES, LIB, verbose)
     _compile_link(cc, flags, PROBE_SOURCES, PROBE_LIB, verbose)
     return LIB

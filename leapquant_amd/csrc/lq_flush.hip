@@ -607,7 +607,7 @@ __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float*
     for (int i = 0; i < 4; ++i) rsk[1][i] = rsk[0][i];
   }
   int next = 0;                                       // dynamic schedule: this workgroup's next candidate
-  if (sched && tid == 0) next = sched_next(sched);
+  if (sched && tid == 0) next = sched_take(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
@@ -664,7 +664,7 @@ __device__ void flush_head64(FlushShared64& sh, const lq_state& st, const float*
       }
     }
   }
-  if (sched && tid == 0) sh.due = (unsigned long long)next;
+  if (sched && tid == 0) sh.due = (unsigned long long)sched_candidate(take_result(next));
   __syncthreads();                                    // LDS reuse by the next unit of this workgroup
 }
 

@@ -616,10 +616,21 @@ static_assert(SCHED_GROUPS * SCHED_STRIDE == LQ_SCHED_INTS, "counters of lq_stat
 __device__ __forceinline__ int* sched_counter(int* sched) {
   return sched + SCHED_STRIDE * (int)(blockIdx.x % SCHED_GROUPS);
 }
-__device__ __forceinline__ int sched_next(int* sched) {
-  const int g = __hip_atomic_fetch_add(sched_counter(sched), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
-                ((1 << SCHED_BITS) - 1);
-  return (int)gridDim.x + SCHED_GROUPS * g + (int)(blockIdx.x % SCHED_GROUPS);
+// A take (the counter's old value) and the candidate it stands for are two steps, so that a head can issue its take
+// early and turn it into a candidate only where it stores it: the atomic's round trip then overlaps the head's last
+// stages instead of holding wave 0 right after the take (a use of the result right away waits for it there).
+__device__ __forceinline__ int sched_take(int* sched) {
+  return __hip_atomic_fetch_add(sched_counter(sched), 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int sched_candidate(int take) {
+  return (int)gridDim.x + SCHED_GROUPS * (take & ((1 << SCHED_BITS) - 1)) + (int)(blockIdx.x % SCHED_GROUPS);
+}
+__device__ __forceinline__ int sched_next(int* sched) { return sched_candidate(sched_take(sched)); }
+// the take's value where it is used: an opaque copy, so that nothing computed from it moves up to the take (and with it
+// the wait for the atomic's return)
+__device__ __forceinline__ int take_result(int take) {
+  asm volatile("" : "+v"(take));
+  return take;
 }
 
 template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
@@ -890,7 +901,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
     rsk[3] = dpp<0xff>(rs);
   }
   int next = 0;                                       // dynamic schedule: this workgroup's next candidate
-  if (sched && tid == 0) next = sched_next(sched);
+  if (sched && tid == 0) next = sched_take(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
   Tile t;                                             // E rsk, fp32
 #pragma unroll
@@ -960,7 +971,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   if (tid == 0) {
     if (!KDA) st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
-    if (sched) sh.due = (unsigned long long)next;
+    if (sched) sh.due = (unsigned long long)sched_candidate(take_result(next));
   }
   __syncthreads();                                    // LDS reuse by the next head of this workgroup
 }
@@ -978,21 +989,31 @@ constexpr int FT4 = 256;             // threads per workgroup
 constexpr int NW4 = FT4 / 64;        // waves
 constexpr int HALF = 32;             // window entries staged at once
 constexpr int OPS4 = HALF + 8;       // operand row stride (bf16): 80 B rows, 16-byte aligned, conflict-free b128 reads
+// CF (conflict-free layout): the factor tables [4][128] fp16 are read by the four lane rows of a 16-lane group at once
+// (row l & 3, same column), and rows of 128 halfs all start in the same bank, so each row is padded by 16 halfs (rows
+// then start 8 banks apart); the row-maximum table [16][128] fp32 is written by the four lane groups at once (row
+// 4 w + q, same column), padded by 16 floats (16 banks apart); store_half rotates the odd lane groups' columns.  The
+// standalone flush and the prefill dequant use it (the flush's LDS bank conflicts fall by three quarters, LDS-active
+// cycles by a third); the one-launch decode's flush does not: there the padded addressing costs the fused-conv kernel
+// registers (20 bytes per lane spilled), and the conflicts are not on its critical path.
+constexpr int FTP = 16, RMP = 16;
 
 struct Tile4 {
   f32x4 a[2][8];
 };
 
-struct FlushShared4 {
+template <bool CF>
+struct FlushShared4T {
+  static constexpr int FP = CF ? FTP : 0, RP = CF ? RMP : 0;
   union {
     bf16_t op[3][KD][OPS4];    // rebuild operands of one window half [c or v][j]
     struct {                   // after the rebuild
       f32x4 qpart[NW4][VD];    // per-wave partial Q rows
-      float rmx[4 * NW4][VD];  // per-(wave, lane group) row maxima of the scaled residual
+      float rmx[4 * NW4][VD + RP];    // per-(wave, lane group) row maxima of the scaled residual
       float rq[VD];            // qmax / row scale
-      f16_t ppT[4][KD];        // P16^T
-      f16_t uoT[4][KD];        // old U^T, fp16 (MFMA operand)
-      f16_t qoT[4][VD];        // old Q^T, fp16
+      f16_t ppT[4][KD + FP];   // P16^T
+      f16_t uoT[4][KD + FP];   // old U^T, fp16 (MFMA operand)
+      f16_t qoT[4][VD + FP];   // old Q^T, fp16
       f16x4 qo16[VD];          // old Q rows [v][a], fp16 (residual B operand)
       f16x4 qn16[VD];          // Q16 rows [v][r] (residual B operand)
     } r;
@@ -1002,11 +1023,13 @@ struct FlushShared4 {
   float w[LPMAX];
   f32x4 uoc[KD];               // old U rows [c][a], a >= R zero
   f32x4 qov[VD];               // old Q rows [v][a], a >= R zero
-  f16_t qT[4][VD];             // Q^T operand of the P steps: fp16-rounded Q0, then Q16
+  f16_t qT[4][VD + FP];        // Q^T operand of the P steps: fp16-rounded Q0, then Q16
   f32x4 qv[VD];                // Q rows: fp32 before CholeskyQR, then Q16
   unsigned long long due;      // persistent flush: due mask of the current candidate chunk / listed head
 };
-static_assert(sizeof(FlushShared4) <= 40960, "four workgroups per CU: 160 KiB of LDS");
+using FlushShared4 = FlushShared4T<true>;
+static_assert(sizeof(FlushShared4T<true>) <= 40960 && sizeof(FlushShared4T<false>) <= 40960,
+              "four workgroups per CU: 160 KiB of LDS");
 
 // One window half's rows in registers: thread t takes entries 2 (t % 16), 2 (t % 16) + 1 of the half, columns
 // 8 (t / 16) .. 8 (t / 16) + 7 (16 x 16 = 256 threads).  Rows >= h read row 0 (in bounds; their weight is zero).
@@ -1030,11 +1053,15 @@ __device__ __forceinline__ void load_half(WinHalf& r, const lq_state& st, int sl
   }
 }
 // Transposed into the rebuild operands [c or v][j - HALF hf], two entries per 32-bit LDS write: op0 = K_j[c],
-// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.
-__device__ __forceinline__ void store_half(FlushShared4& sh, const WinHalf& r, int h, int hf) {
+// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.  Write e of a lane writes
+// column c8 + e, but the odd 16-lane groups (columns c8 = 8 (t / 16), 8 rows past the even group's) write c8 + (e + 4)
+// mod 8: rows 8 + 4 or 8 - 4 apart are 80 or 240 dwords apart, 16 banks off, so the two groups of a half-wave write
+// disjoint banks (rows exactly 8 apart, 160 dwords, share all 16).  Without CF no rotation (the same bytes either way).
+template <bool CF>
+__device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf& r, int h, int hf) {
   // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
 #pragma clang fp contract(off)
-  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8;
+  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8, ro = CF ? 4 * ((t / 16) & 1) : 0;
   const int j0 = HALF * hf + jl;
   const bool v0 = j0 < h, v1 = j0 + 1 < h;
   const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
@@ -1042,15 +1069,18 @@ __device__ __forceinline__ void store_half(FlushShared4& sh, const WinHalf& r, i
   const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int x = e >> 1;
-    const bool odd = e & 1;
-    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
-    *(uint32_t*)&sh.op[0][c8 + e][jl] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
-    const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
-    const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
+    const int x = e >> 1, xr = ((e + 4) & 7) >> 1;     // the word of column e, and of column e + 4 (odd groups)
+    const bool rot = ro != 0, odd = e & 1;
+    const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of the column
+    const int c = c8 + ((e + ro) & 7);
+    const uint32_t kax = rot ? ka[xr] : ka[x], kbx = rot ? kb[xr] : kb[x];
+    const uint32_t uax = rot ? ua[xr] : ua[x], ubx = rot ? ub[xr] : ub[x];
+    *(uint32_t*)&sh.op[0][c][jl] = __builtin_amdgcn_perm(kbx, kax, sel);
+    const float wu0 = w0 * (odd ? bf_hi(uax) : bf_lo(uax));
+    const float wu1 = w1 * (odd ? bf_hi(ubx) : bf_lo(ubx));
     const uint32_t hi = pk_bf16_kept(wu0, wu1);
-    *(uint32_t*)&sh.op[1][c8 + e][jl] = hi;
-    *(uint32_t*)&sh.op[2][c8 + e][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+    *(uint32_t*)&sh.op[1][c][jl] = hi;
+    *(uint32_t*)&sh.op[2][c][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
   }
 }
 // acc[c][v] += sum_j A[c][j] B[v][j] over one staged half (bf16 operands, fp32 accumulate)
@@ -1132,7 +1162,8 @@ __device__ __forceinline__ void tile_add_words4(Tile4& t, const uint32_t wds[2][
   }
 }
 // M[a][r] = sum_v Q_old[v][a] Q[v][r] (Q from sh.qT): every lane gets all 16 entries
-__device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4]) {
+template <bool CF>
+__device__ __forceinline__ void gram_qold_q(const FlushShared4T<CF>& sh, float M[4][4]) {
   const int l = lane_id(), q = l >> 4, l16 = l & 15;
   f32x4 macc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -1151,8 +1182,8 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4& sh, float M[4][4
 // v, so each block of B is transposed (one exact MFMA against the identity: lane l then holds
 // B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]); the first call (TR) forms the transposed blocks into bt, the
 // second (the U step) reads them from there.
-template <bool TR>
-__device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh)[2][8], f16x4 (&bt)[2][8], float pn,
+template <bool TR, bool CF>
+__device__ __forceinline__ void p_step4(const FlushShared4T<CF>& sh, const f16x4 (&bh)[2][8], f16x4 (&bt)[2][8], float pn,
                                         int R, f32x4 p[2]) {
   const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
   float M[4][4];
@@ -1181,8 +1212,8 @@ __device__ __forceinline__ void p_step4(const FlushShared4& sh, const f16x4 (&bh
   }
 }
 
-template <int K_ = KD, int V_ = VD>
-__device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
+template <int K_ = KD, int V_ = VD, bool CF = true>
+__device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                             float qmax, int* sched = nullptr) {
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
@@ -1407,7 +1438,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
     rsk[g][3] = dpp<0xff>(rs);
   }
   int next = 0;                                       // dynamic schedule: this workgroup's next candidate
-  if (sched && tid == 0) next = sched_next(sched);
+  if (sched && tid == 0) next = sched_take(sched);
   // ---- stage 6: row scales and codes (kernels.py:1974-2009) ----
   Tile4 t;                                            // E rsk, fp32
 #pragma unroll
@@ -1486,7 +1517,7 @@ __device__ void flush_head4(FlushShared4& sh, const lq_state& st, const float* _
   if (tid == 0) {
     st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
-    if (sched) sh.due = (unsigned long long)next;
+    if (sched) sh.due = (unsigned long long)sched_candidate(take_result(next));
   }
   __syncthreads();                                    // LDS reuse by the next head of this workgroup
 }
