@@ -82,14 +82,12 @@ void dequant4_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
     store_half(sh, win, h, 0);
     if (h > HALF) load_half<KD, VD>(win, st, slot, hv, h, 1);
     __syncthreads();
-    rebuild_half4(t, sh.op[0], sh.op[1]);
-    rebuild_half4(t, sh.op[0], sh.op[2]);
+    rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
     if (h > HALF) {
       __syncthreads();                                // every wave is past the first half's operands
       store_half(sh, win, h, 1);
       __syncthreads();
-      rebuild_half4(t, sh.op[0], sh.op[1]);
-      rebuild_half4(t, sh.op[0], sh.op[2]);
+      rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
     }
   }
   __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them

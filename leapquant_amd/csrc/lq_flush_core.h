@@ -1083,21 +1083,35 @@ __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf&
     *(uint32_t*)&sh.op[2][c][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
   }
 }
-// acc[c][v] += sum_j A[c][j] B[v][j] over one staged half (bf16 operands, fp32 accumulate)
-__device__ __forceinline__ void rebuild_half4(Tile4& t, const bf16_t (*A)[OPS4], const bf16_t (*B)[OPS4]) {
+// acc[c][v] += sum_j A[c][j] (B1[v][j] + B2[v][j]) over one staged half (bf16 operands, fp32 accumulate): the hi and lo
+// passes with the A fragments loaded once and the next pair of B fragments requested before the current pair's MFMAs
+// (each accumulator takes its hi term, then its lo term; 124 -> 112 VGPRs in the one-launch decode, flush 194 -> 191
+// us at config 3)
+__device__ __forceinline__ void rebuild_half4x2(Tile4& t, const bf16_t (*A)[OPS4], const bf16_t (*B1)[OPS4],
+                                                const bf16_t (*B2)[OPS4]) {
   const int l = lane_id(), w = wave_id(), q = l >> 4;
   bf16x8 af[2];
 #pragma unroll
   for (int g = 0; g < 2; ++g) af[g] = *(const bf16x8*)&A[32 * w + 16 * g + (l & 15)][8 * q];
+  auto ld = [&](int it, bf16x8& b0, bf16x8& b1) {
+    const bf16_t (*B)[OPS4] = (it & 1) ? B2 : B1;
+    const int n2 = 2 * (it >> 1);
+    b0 = *(const bf16x8*)&B[16 * n2 + (l & 15)][8 * q];
+    b1 = *(const bf16x8*)&B[16 * n2 + 16 + (l & 15)][8 * q];
+  };
+  bf16x8 c0, c1;
+  ld(0, c0, c1);
 #pragma unroll
-  for (int n2 = 0; n2 < 8; n2 += 2) {                 // two B fragments in flight at a time (register pressure)
-    const bf16x8 b0 = *(const bf16x8*)&B[16 * n2 + (l & 15)][8 * q];
-    const bf16x8 b1 = *(const bf16x8*)&B[16 * n2 + 16 + (l & 15)][8 * q];
+  for (int it = 0; it < 8; ++it) {
+    bf16x8 n0, n1;
+    if (it + 1 < 8) ld(it + 1, n0, n1);
+    const int n2 = 2 * (it >> 1);
 #pragma unroll
-    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b0, t.a[g][n2], 0, 0, 0);
+    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], c0, t.a[g][n2], 0, 0, 0);
 #pragma unroll
-    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b1, t.a[g][n2 + 1], 0, 0, 0);
+    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], c1, t.a[g][n2 + 1], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < 8) { c0 = n0; c1 = n1; }
   }
 }
 // the 16 code words of the lane's tile entries, wds[g][nt] = Sq[16 nt + l16][32 w + 16 g + 4 q .. + 3] (zero past a
@@ -1281,15 +1295,13 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
     // as well would take the registers past 128)
     if (two) load_half<K_, V_>(win, st, slot, hv, L, 1);
     __syncthreads();
-    rebuild_half4(t, sh.op[0], sh.op[1]);
-    rebuild_half4(t, sh.op[0], sh.op[2]);
+    rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
     load_code_words4<K_, V_>(wds, Sq);
     if (two) {
       __syncthreads();                                // every wave is past the first half's operands
       store_half(sh, win, L, 1);
       __syncthreads();
-      rebuild_half4(t, sh.op[0], sh.op[1]);
-      rebuild_half4(t, sh.op[0], sh.op[2]);
+      rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
     }
     tile_add_words4(t, wds, sh.svr, sh.skl);
 #pragma unroll
