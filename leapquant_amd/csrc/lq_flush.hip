@@ -158,24 +158,24 @@ __device__ void flush_listed(unsigned long long& due, const lq_state& st, const 
 // no path's registers weigh on another's (one kernel holding all three spilled up to 64 bytes per lane more).
 enum { FS_STATIC = 0, FS_DYNAMIC = 1, FS_LISTED = 2 };
 
-template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4, int MODE = FS_STATIC>
+template <int K_ = KD, int V_ = VD, int RA = 4, int MODE = FS_STATIC>
 __global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(4)))
 void flush_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                   int* dlist) {
   __shared__ FlushShared<RA> sh;
-  auto head = [&](int slot, int hv, unsigned, int* sched) {
-    flush_head<KDA, K_, V_, RA>(sh, st, Q0, slot, hv, qmax, sched);
-  };
+  auto head = [&](int slot, int hv, unsigned, int* sched) { flush_head<K_, V_, RA>(sh, st, Q0, slot, hv, qmax, sched); };
   if constexpr (MODE == FS_LISTED) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan<1, MODE == FS_DYNAMIC>(sh.due, st, idx, N, head);
 }
 
-template <int K_ = KD, int V_ = VD, int MODE = FS_STATIC>
+template <int K_ = KD, int V_ = VD, int MODE = FS_STATIC, bool KDA = false>
 __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void flush4_kernel(lq_state st, const float* __restrict__ Q0, const int* __restrict__ idx, int N, float qmax,
                    int* dlist) {
   __shared__ FlushShared4 sh;
-  auto head = [&](int slot, int hv, unsigned, int* sched) { flush_head4<K_, V_>(sh, st, Q0, slot, hv, qmax, sched); };
+  auto head = [&](int slot, int hv, unsigned, int* sched) {
+    flush_head4<K_, V_, true, KDA>(sh, st, Q0, slot, hv, qmax, sched);
+  };
   if constexpr (MODE == FS_LISTED) flush_listed(sh.due, st, idx, N, dlist, head);
   else flush_scan<1, MODE == FS_DYNAMIC>(sh.due, st, idx, N, head);
 }
@@ -1564,12 +1564,12 @@ int lq_launch_flush(const lq_state* st, const float* Q0, const int* idx, int N, 
   const dim3 g((unsigned)(total < 2 * num_cus() ? total : 2 * num_cus()));   // persistent: two workgroups per CU at most
   const dim3 g4((unsigned)(total < 4 * num_cus() ? total : 4 * num_cus()));  // four-wave flush: four per CU
   if (kda) {
-    with_mode(st, dlist, total, g.x, [&](auto m) {
-      flush_kernel<true, KD, VD, 4, decltype(m)::value><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+    with_mode(st, dlist, total, g4.x, [&](auto m) {
+      flush4_kernel<KD, VD, decltype(m)::value, true><<<g4, FT4, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
     });
   } else if (st->K == KD && st->R > 4) {
     with_mode(st, dlist, total, g.x, [&](auto m) {
-      flush_kernel<false, KD, VD, 8, decltype(m)::value><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
+      flush_kernel<KD, VD, 8, decltype(m)::value><<<g, FT, 0, s>>>(*st, Q0, idx, N, qmax, dlist);
     });
   } else if (st->K == KD) {
     with_mode(st, dlist, total, g4.x, [&](auto m) {

@@ -633,11 +633,10 @@ __device__ __forceinline__ int take_result(int take) {
   return take;
 }
 
-template <bool KDA, int K_ = KD, int V_ = VD, int RA = 4>
+template <int K_ = KD, int V_ = VD, int RA = 4>
 __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                            float qmax, int* sched = nullptr) {
-  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
-  static_assert(RA == 4 || (RA == 8 && !KDA && K_ == KD && V_ == VD), "R = 8: GDN 128 x 128 heads");
+  static_assert(RA == 4 || (RA == 8 && K_ == KD && V_ == VD), "R = 8: 128 x 128 heads");
   constexpr int NB = RA / 4;
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
@@ -651,11 +650,8 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   const int LP = (L + 31) & ~31;
 
   // ---- stage 1: every load of the head up front (scalars, scales, factors, window rows, code words) ----
-  float pn = 1.f, rpn = 1.f;
-  if (!KDA) {
-    pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);               // kernels.py:1471
-    rpn = 1.0f / pn;                                  // kernels.py:1477
-  }
+  const float pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);     // kernels.py:1471
+  const float rpn = 1.0f / pn;                        // kernels.py:1477
   const int cv = tid & 127;                           // column (tid < 128) or row (128 <= tid < 256) of the stage-1 loads
   const bool colt = tid < KD;
   const int nc = colt ? K_ : V_;                      // this thread's column / row count
@@ -671,18 +667,15 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
     const float y = Q0[vq * R + min(a, R - 1)];
     q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
   }
-  const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window<KDA, K_, V_>(win, st, slot, hv, L, LP);
+  load_window<false, K_, V_>(win, st, slot, hv, L, LP);
   uint32_t wds[8];
   load_code_words<K_, V_>(wds, Sq);
 
   if (tid < KD) {
     const int c = cv;
-    float pcv = 1.f;
-    if (KDA) pcv = expf(pbc);                                                          // kernels.py:1451
-    sh.skl[c] = KDA ? scv * pcv : scv;                                                // kernels.py:1519
+    sh.skl[c] = scv;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       f32x4 u;
@@ -690,14 +683,13 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
       for (int i = 0; i < 4; ++i) {
         const int a = 4 * b + i;
         u[i] = a < R ? uqv[a] : 0.f;
-        if (KDA) u[i] = hround(u[i] * pcv);                                           // kernels.py:1464-1465
         sh.uoT[a][c] = f2h(u[i]);
       }
       sh.uoc[b][c] = u;
     }
   } else if (tid < KD + VD) {
     const int v = cv;
-    sh.svr[v] = KDA ? scv * (1.0f / qmax) : scv * (pn / qmax);                       // kernels.py:1468, 1483
+    sh.svr[v] = scv * (pn / qmax);                                                    // kernels.py:1483
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       f32x4 o;
@@ -713,26 +705,17 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   }
   if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
   __syncthreads();
-  store_window<KDA>(sh, win, L, LP);
+  store_window<false>(sh, win, L, LP);
   __syncthreads();
-  if (KDA) {
-    kda_key_scan<2>(sh.op, sh.w, L, LP);
-    __syncthreads();
-  }
 
-  // ---- stage 2: B = deq(S0) (+ decay) + window, fp16 (kernels.py:1483-1571) ----
+  // ---- stage 2: B = deq(S0) pn + window, fp16 (kernels.py:1483-1571) ----
   f16x4 bh[8], bt[8];                                 // B packed: k = c (tile layout) and k = v (transposed)
   {
     Tile t;
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) t.a[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (!KDA) {
-      rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
-      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
-    } else {
-      rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
-      rebuild_mfma(t, sh.op[1], sh.op[2], LP / 32);
-    }
+    rebuild_mfma(t, sh.op[0], sh.op[1], LP / 32);
+    rebuild_mfma(t, sh.op[0], sh.op[2], LP / 32);
     tile_add_words(t, wds, sh.svr, sh.skl);
     f16x4 ident;
 #pragma unroll
@@ -866,9 +849,9 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
       const f16x4 bqo = sh.r.qo16[qb][v];
       const f16x4 bqn = sh.r.qn16[qb][v];
       const f16x4 b = bh[nt];
-      f32x4 e = KDA ? from_h4(b) : f32x4{h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
+      f32x4 e = {h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
       e = mma16(auo, bqo, e);
-      if (!KDA) e *= pn;
+      e *= pn;
       e = mma16(aun, bqn, e);
       bh[nt] = to_h4(e);                                                            // E, fp16
     }
@@ -962,14 +945,9 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   if (tid < V_) {
     for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[r >> 2][tid][r & 3]);
   }
-  if (KDA) {
-    if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
-    uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
-    for (int i = tid; i < L * KD / 8; i += FT) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
-  }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {
-    if (!KDA) st.Pbuf[sh_] = 1.f;
+    st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
     if (sched) sh.due = (unsigned long long)sched_candidate(take_result(next));
   }
@@ -977,13 +955,15 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Four-wave GDN flush: one due head per workgroup of 256 threads, <= 40 KiB LDS and <= 128 VGPRs, so that four heads
-// share a CU (the eight-wave flush above fits two).  The flush is latency-bound -- each head is a chain of dependent,
-// barrier-separated phases -- so heads in flight per CU set its rate.  Same arithmetic, in the same order, as
-// flush_head; only the distribution over the lanes differs: wave w owns key channels [32 w, 32 w + 32) as two groups
-// g of 16, and lane l holds
+// Four-wave flush (GDN with R <= 4, and KDA): one due head per workgroup of 256 threads, <= 40 KiB LDS and <= 128
+// VGPRs, so that four heads share a CU (the eight-wave flush above fits two).  The flush is latency-bound -- each head
+// is a chain of dependent, barrier-separated phases -- so heads in flight per CU set its rate.  Same arithmetic, in the
+// same order, as flush_head; only the distribution over the lanes differs: wave w owns key channels [32 w, 32 w + 32)
+// as two groups g of 16, and lane l holds
 //     a[g][nt][i] = M[c][v],   c = 32 w + 16 g + 4 (l >> 4) + i,   v = 16 nt + (l & 15).
-// The window is staged and multiplied in halves of 32 entries.
+// The window is staged and multiplied in halves of 32 entries.  KDA (kernels.py:1443-1471, 1519): pn = 1, the
+// per-channel decay exp(Pbuf[c]) folds into the column factor Sk and the old U rows, and the window's keys enter as
+// decayed hi / lo operands (kda_key_scan4), the halves staged newest first.
 // ------------------------------------------------------------------------------------------------------------------
 constexpr int FT4 = 256;             // threads per workgroup
 constexpr int NW4 = FT4 / 64;        // waves
@@ -1032,15 +1012,17 @@ static_assert(sizeof(FlushShared4T<true>) <= 40960 && sizeof(FlushShared4T<false
               "four workgroups per CU: 160 KiB of LDS");
 
 // One window half's rows in registers: thread t takes entries 2 (t % 16), 2 (t % 16) + 1 of the half, columns
-// 8 (t / 16) .. 8 (t / 16) + 7 (16 x 16 = 256 threads).  Rows >= h read row 0 (in bounds; their weight is zero).
+// 8 (t / 16) .. 8 (t / 16) + 7 (16 x 16 = 256 threads).  Rows >= h read row 0 (in bounds; their weight is zero).  KDA
+// also takes the entries' per-channel decays (Gbuf, the keys' [j][c] layout).
 struct WinHalf {
-  uint4 k[2], u[2];
+  uint4 k[2], u[2], g[2];
 };
-template <int K_, int V_>
+template <int K_, int V_, bool KDA = false>
 __device__ __forceinline__ void load_half(WinHalf& r, const lq_state& st, int slot, int hv, int h, int hf) {
   const int G = st.HV / st.H, hk = hv / G, L = st.L;
   const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
   const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
+  const f16_t* Gb = KDA ? (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD : nullptr;
   const int t = opaque_tid(), jp = t % 16, c8 = (t / 16) * 8;
   const uint4 z = make_uint4(0u, 0u, 0u, 0u);        // columns past a K_ / V_ < 128 head: zero operands
 #pragma unroll
@@ -1050,14 +1032,17 @@ __device__ __forceinline__ void load_half(WinHalf& r, const lq_state& st, int sl
     const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
     r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
     r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
+    if constexpr (KDA) r.g[k] = *(const uint4*)(Gb + (long long)jr * KD + c8);
   }
 }
-// Transposed into the rebuild operands [c or v][j - HALF hf], two entries per 32-bit LDS write: op0 = K_j[c],
-// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.  Write e of a lane writes
-// column c8 + e, but the odd 16-lane groups (columns c8 = 8 (t / 16), 8 rows past the even group's) write c8 + (e + 4)
-// mod 8: rows 8 + 4 or 8 - 4 apart are 80 or 240 dwords apart, 16 banks off, so the two groups of a half-wave write
-// disjoint banks (rows exactly 8 apart, 160 dwords, share all 16).  Without CF no rotation (the same bytes either way).
-template <bool CF>
+// Transposed into the rebuild operands [c or v][j - HALF hf], two entries per 32-bit LDS write.  GDN: op0 = K_j[c],
+// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511); rows j >= h carry zero values.  KDA: op0 / op1 = raw K_j[c] /
+// e_j[c] (turned into the decayed key operands by kda_key_scan4), op2 = u_j[v]; rows j >= h carry zero values and
+// decay 1.  Write e of a lane writes column c8 + e, but the odd 16-lane groups (columns c8 = 8 (t / 16), 8 rows past
+// the even group's) write c8 + (e + 4) mod 8: rows 8 + 4 or 8 - 4 apart are 80 or 240 dwords apart, 16 banks off, so
+// the two groups of a half-wave write disjoint banks (rows exactly 8 apart, 160 dwords, share all 16).  Without CF no
+// rotation (the same bytes either way).
+template <bool KDA = false, bool CF>
 __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf& r, int h, int hf) {
   // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
 #pragma clang fp contract(off)
@@ -1067,6 +1052,8 @@ __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf&
   const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
   const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
   const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
+  const uint32_t ga[4] = {r.g[0].x, r.g[0].y, r.g[0].z, r.g[0].w}, gb[4] = {r.g[1].x, r.g[1].y, r.g[1].z, r.g[1].w};
+  const uint32_t keep = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int x = e >> 1, xr = ((e + 4) & 7) >> 1;     // the word of column e, and of column e + 4 (odd groups)
@@ -1076,12 +1063,67 @@ __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf&
     const uint32_t kax = rot ? ka[xr] : ka[x], kbx = rot ? kb[xr] : kb[x];
     const uint32_t uax = rot ? ua[xr] : ua[x], ubx = rot ? ub[xr] : ub[x];
     *(uint32_t*)&sh.op[0][c][jl] = __builtin_amdgcn_perm(kbx, kax, sel);
-    const float wu0 = w0 * (odd ? bf_hi(uax) : bf_lo(uax));
-    const float wu1 = w1 * (odd ? bf_hi(ubx) : bf_lo(ubx));
-    const uint32_t hi = pk_bf16_kept(wu0, wu1);
-    *(uint32_t*)&sh.op[1][c][jl] = hi;
-    *(uint32_t*)&sh.op[2][c][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+    if constexpr (!KDA) {
+      const float wu0 = w0 * (odd ? bf_hi(uax) : bf_lo(uax));
+      const float wu1 = w1 * (odd ? bf_hi(ubx) : bf_lo(ubx));
+      const uint32_t hi = pk_bf16_kept(wu0, wu1);
+      *(uint32_t*)&sh.op[1][c][jl] = hi;
+      *(uint32_t*)&sh.op[2][c][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
+    } else {
+      const uint32_t gax = rot ? ga[xr] : ga[x], gbx = rot ? gb[xr] : gb[x];
+      *(uint32_t*)&sh.op[1][c][jl] = (__builtin_amdgcn_perm(gbx, gax, sel) & keep) | (0x3c003c00u & ~keep);
+      *(uint32_t*)&sh.op[2][c][jl] = __builtin_amdgcn_perm(ubx, uax, sel) & keep;
+    }
   }
+}
+// KDA key operands of one staged half, in place over its raw keys op[0] and decays op[1] ([c][j - HALF hf]): op[0] /
+// op[1] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, as kda_key_scan).  The
+// halves are staged newest first: dcar is D at the top of this half (the product of every later decay; 1 for the
+// newest half), and the return value is the carry for the next, older half.  Two lanes per channel (c = t / 2): lane s
+// takes entries 16 s .. 16 s + 15 and walks them backwards; lane 0 first multiplies through lane 1's decays (handed
+// over by DPP), so that every D_j is the sequential walk's own product, one rounding per factor in the reference's
+// order (a regrouped product rounds differently, and the key operands' cancellation in the rebuild turns such last-bit
+// differences into fp16 flips of B).  Each lane reads and writes its own 16 entries only.
+template <bool CF>
+__device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar, int h, int hf) {
+  // the split is of the fp32-rounded product (kernels.py:1456-1463): no fusing into the first subtraction
+#pragma clang fp contract(off)
+  const int t = opaque_tid(), c = t >> 1, s = t & 1, jb = 16 * s, j0 = HALF * hf + jb;
+  uint32_t ku[8], eu[8];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    const uint4 kr = *(const uint4*)&sh.op[0][c][jb + 8 * x];
+    const uint4 er = *(const uint4*)&sh.op[1][c][jb + 8 * x];
+    ku[4 * x] = kr.x; ku[4 * x + 1] = kr.y; ku[4 * x + 2] = kr.z; ku[4 * x + 3] = kr.w;
+    eu[4 * x] = er.x; eu[4 * x + 1] = er.y; eu[4 * x + 2] = er.z; eu[4 * x + 3] = er.w;
+  }
+  float d = dcar, dn = dcar;                          // lane 0: dcar times lane 1's 16 decays, last first
+#pragma unroll
+  for (int x = 7; x >= 0; --x) {
+    const uint32_t en = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)eu[x], 0xf5, 0xf, 0xf, false);  // quad_perm [1,1,3,3]
+    dn = dn * h2f((f16_t)(en >> 16));
+    dn = dn * h2f((f16_t)(en & 0xffffu));
+  }
+  if (s == 0) d = dn;
+  uint32_t hw[8] = {}, lw[8] = {};
+#pragma unroll
+  for (int e = 15; e >= 0; --e) {
+    if (j0 + e < h) {                                 // rows >= h: zero operands, decay 1
+      float r = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j0 + e] * d);
+      const bf16_t bh_ = f2bf(r);
+      r = r - bf2f(bh_);
+      const bf16_t bl_ = f2bf(r);
+      hw[e >> 1] |= (uint32_t)bh_ << (16 * (e & 1));
+      lw[e >> 1] |= (uint32_t)bl_ << (16 * (e & 1));
+      d = d * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
+    }
+  }
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+    *(uint4*)&sh.op[0][c][jb + 8 * x] = make_uint4(hw[4 * x], hw[4 * x + 1], hw[4 * x + 2], hw[4 * x + 3]);
+    *(uint4*)&sh.op[1][c][jb + 8 * x] = make_uint4(lw[4 * x], lw[4 * x + 1], lw[4 * x + 2], lw[4 * x + 3]);
+  }
+  return dpp<0xa0>(d);                                // quad_perm [0,0,2,2]: lane 0's D below its entries, to both
 }
 // acc[c][v] += sum_j A[c][j] (B1[v][j] + B2[v][j]) over one staged half (bf16 operands, fp32 accumulate): the hi and lo
 // passes with the A fragments loaded once and the next pair of B fragments requested before the current pair's MFMAs
@@ -1112,6 +1154,41 @@ __device__ __forceinline__ void rebuild_half4x2(Tile4& t, const bf16_t (*A)[OPS4
     for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], c1, t.a[g][n2 + 1], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < 8) { c0 = n0; c1 = n1; }
+  }
+}
+// KDA: acc[c][v] += sum_j (A1[c][j] + A2[c][j]) B[v][j] over one staged half (the hi / lo decayed key operands
+// against u): both A fragments loaded once, each B pair once, the next pair requested before the current MFMAs; each
+// accumulator takes its hi term, then its lo term
+__device__ __forceinline__ void rebuild_half4x2a(Tile4& t, const bf16_t (*A1)[OPS4], const bf16_t (*A2)[OPS4],
+                                                 const bf16_t (*B)[OPS4]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  bf16x8 a1[2], a2[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) {
+    a1[g] = *(const bf16x8*)&A1[32 * w + 16 * g + (l & 15)][8 * q];
+    a2[g] = *(const bf16x8*)&A2[32 * w + 16 * g + (l & 15)][8 * q];
+  }
+  auto ld = [&](int n2, bf16x8& b0, bf16x8& b1) {
+    b0 = *(const bf16x8*)&B[16 * n2 + (l & 15)][8 * q];
+    b1 = *(const bf16x8*)&B[16 * n2 + 16 + (l & 15)][8 * q];
+  };
+  bf16x8 c0, c1;
+  ld(0, c0, c1);
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    bf16x8 n0, n1;
+    if (it + 1 < 4) ld(2 * it + 2, n0, n1);
+    const int n2 = 2 * it;
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[g], c0, t.a[g][n2], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a1[g], c1, t.a[g][n2 + 1], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[g], c0, t.a[g][n2], 0, 0, 0);
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[g], c1, t.a[g][n2 + 1], 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (it + 1 < 4) { c0 = n0; c1 = n1; }
   }
 }
 // the 16 code words of the lane's tile entries, wds[g][nt] = Sq[16 nt + l16][32 w + 16 g + 4 q .. + 3] (zero past a
@@ -1226,9 +1303,10 @@ __device__ __forceinline__ void p_step4(const FlushShared4T<CF>& sh, const f16x4
   }
 }
 
-template <int K_ = KD, int V_ = VD, bool CF = true>
+template <int K_ = KD, int V_ = VD, bool CF = true, bool KDA = false>
 __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const float* __restrict__ Q0, int slot, int hv,
                             float qmax, int* sched = nullptr) {
+  static_assert(!KDA || (K_ == KD && V_ == VD), "KDA heads are 128 x 128");
   const int HV = st.HV, L = st.L, R = st.R;
   const long long sh_ = (long long)slot * HV + hv;
   const int tid = opaque_tid(), l = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6), q = l >> 4, l16 = l & 15;
@@ -1238,10 +1316,15 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
   float* Sv = Sk + K_;
   f16_t* UQ = (f16_t*)(Sv + V_);
   const bool two = L > HALF;                          // window halves
+  // the half staged first: KDA stages the newest half first (its decayed keys carry the later decays down)
+  const int hA = KDA && two ? 1 : 0;
 
   // ---- stage 1: every load of the head up front ----
-  const float pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);     // kernels.py:1471
-  const float rpn = 1.0f / pn;                        // kernels.py:1477
+  float pn = 1.f, rpn = 1.f;                          // KDA: the decay lives in Pbuf per channel, pn = 1
+  if constexpr (!KDA) {
+    pn = fmaxf(st.Pbuf[sh_], LQ_PNMIN);               // kernels.py:1471
+    rpn = 1.0f / pn;                                  // kernels.py:1477
+  }
   const int cv = tid & 127;                           // column (tid < 128) or row of the stage-1 loads
   const bool colt = tid < KD;
   const int nc = colt ? K_ : V_;
@@ -1257,16 +1340,18 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
     const float y = Q0[vq * R + min(a, R - 1)];
     q0v[a] = (V_ == VD || cv < V_) ? y : 0.f;
   }
+  const float pbc = KDA ? st.Pbuf[sh_ * KD + cv] : 0.f;
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinHalf win;
-  load_half<K_, V_>(win, st, slot, hv, L, 0);
+  load_half<K_, V_, KDA>(win, st, slot, hv, L, hA);
   uint32_t wds[2][8];                                 // loaded after the first window half's products
 
   if (colt) {
-    sh.skl[cv] = scv;
+    const float pcv = KDA ? expf(pbc) : 1.f;                                           // kernels.py:1451
+    sh.skl[cv] = KDA ? scv * pcv : scv;                                               // kernels.py:1519
     f32x4 u;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) u[a] = a < R ? uqv[a] : 0.f;
+    for (int a = 0; a < 4; ++a) u[a] = a < R ? (KDA ? hround(uqv[a] * pcv) : uqv[a]) : 0.f;   // kernels.py:1464-1465
     sh.uoc[cv] = u;
   } else {
     sh.svr[cv] = scv * (pn / qmax);                                                   // kernels.py:1483
@@ -1289,19 +1374,29 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
     for (int g = 0; g < 2; ++g)
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) t.a[g][nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-    store_half(sh, win, L, 0);
+    float dcar = 1.f;                                 // KDA: the decay product carried down from the newer half
+    auto rebuild = [&](int hf) {
+      if constexpr (KDA) {
+        dcar = kda_key_scan4(sh, dcar, L, hf);
+        __syncthreads();
+        rebuild_half4x2a(t, sh.op[0], sh.op[1], sh.op[2]);
+      } else {
+        rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
+      }
+    };
+    store_half<KDA>(sh, win, L, hA);
     // the second half's rows are requested as soon as the first half's are in LDS, and the code words after the first
     // half's products, so that each load's latency overlaps a half's products (holding the code words from stage 1
     // as well would take the registers past 128)
-    if (two) load_half<K_, V_>(win, st, slot, hv, L, 1);
+    if (two) load_half<K_, V_, KDA>(win, st, slot, hv, L, 1 - hA);
     __syncthreads();
-    rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
+    rebuild(hA);
     load_code_words4<K_, V_>(wds, Sq);
     if (two) {
       __syncthreads();                                // every wave is past the first half's operands
-      store_half(sh, win, L, 1);
+      store_half<KDA>(sh, win, L, 1 - hA);
       __syncthreads();
-      rebuild_half4x2(t, sh.op[0], sh.op[1], sh.op[2]);
+      rebuild(1 - hA);
     }
     tile_add_words4(t, wds, sh.svr, sh.skl);
 #pragma unroll
@@ -1412,9 +1507,9 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
 #pragma unroll
       for (int g = 0; g < 2; ++g) {
         const f16x4 b = bh[g][nt];
-        f32x4 e = {h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
+        f32x4 e = KDA ? from_h4(b) : f32x4{h4mul<0>(b, rpn), h4mul<1>(b, rpn), h4mul<2>(b, rpn), h4mul<3>(b, rpn)};
         e = mma16(auo[g], bqo, e);
-        e *= pn;
+        if constexpr (!KDA) e *= pn;
         e = mma16(aun[g], bqn, e);
         bh[g][nt] = to_h4(e);                                                       // E, fp16
       }
@@ -1525,9 +1620,14 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
   if (tid < V_) {
     for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
   }
+  if constexpr (KDA) {
+    if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
+    uint4* Gb = (uint4*)((f16_t*)st.Gbuf + sh_ * L * KD);                             // fp16 1.0 over the window
+    for (int i = tid; i < L * KD / 8; i += FT4) Gb[i] = make_uint4(0x3c003c00u, 0x3c003c00u, 0x3c003c00u, 0x3c003c00u);
+  }
   if (tid < L) st.Wbuf[sh_ * L + tid] = 0.f;
   if (tid == 0) {
-    st.Pbuf[sh_] = 1.f;
+    if constexpr (!KDA) st.Pbuf[sh_] = 1.f;
     st.hcnt[sh_] = 0;
     if (sched) sh.due = (unsigned long long)sched_candidate(take_result(next));
   }

@@ -6,8 +6,9 @@ gfx950 code objects, tests/lq_codeobj.py).
     were allocated for;
   * its static LDS fits a workgroup on a CU (160 KiB), and the workgroups per CU that LDS and registers allow are at
     least one, so every launch can make progress;
-  * the kernels of the benchmark's hot path (the one-launch GDN decode, the four-wave flush, the KDA step) keep the
-    residency they are tuned for (four workgroups per CU for the 256-thread ones, eight for the KDA step).
+  * the kernels of the benchmark's hot path (the one-launch GDN decode, the four-wave GDN and KDA flushes, the KDA
+    step) keep the residency they are tuned for (four workgroups per CU for the 256-thread ones, eight for the KDA
+    step).
 """
 import os
 import shutil
@@ -59,7 +60,9 @@ def test_hot_kernels_keep_their_residency(kernels):
         hit = [k for k in kernels if pattern in k["name"]]
         assert hit, pattern
         return hit
-    for k in find("gdn_step_kernel<128, 128, 2, false, true, 4, false>") + find("flush4_kernel<128, 128, 1>"):
+    for k in find("gdn_step_kernel<128, 128, 2, false, true, 4, false>") + find("flush4_kernel<128, 128, 1, false>"):
         assert _per_cu(k) >= 4 and k["scratch"] <= 8, (k["name"], _per_cu(k), k["scratch"])
+    for k in find("flush4_kernel<128, 128, 1, true>"):        # KDA: a few loop-invariant values spilled per head
+        assert _per_cu(k) >= 4 and k["scratch"] <= 64, (k["name"], _per_cu(k), k["scratch"])
     for k in find("kda_step_kernel"):
         assert _per_cu(k) >= 8 and k["scratch"] == 0, (k["name"], _per_cu(k), k["scratch"])
