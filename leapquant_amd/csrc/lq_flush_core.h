@@ -1105,18 +1105,28 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
     dn = dn * h2f((f16_t)(en & 0xffffu));
   }
   if (s == 0) d = dn;
-  uint32_t hw[8] = {}, lw[8] = {};
+  float wj[16];                                       // the entries' weights, read before the walk
+#pragma unroll
+  for (int x = 0; x < 4; ++x) {
+    const float4 w4 = *(const float4*)&sh.w[j0 + 4 * x];
+    wj[4 * x] = w4.x; wj[4 * x + 1] = w4.y; wj[4 * x + 2] = w4.z; wj[4 * x + 3] = w4.w;
+  }
+  uint32_t hw[8], lw[8];
+  // no branch per entry: rows >= h hold decay 1 (d passes unchanged) and take zero operands
 #pragma unroll
   for (int e = 15; e >= 0; --e) {
-    if (j0 + e < h) {                                 // rows >= h: zero operands, decay 1
-      float r = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (sh.w[j0 + e] * d);
-      const bf16_t bh_ = f2bf(r);
-      r = r - bf2f(bh_);
-      const bf16_t bl_ = f2bf(r);
-      hw[e >> 1] |= (uint32_t)bh_ << (16 * (e & 1));
-      lw[e >> 1] |= (uint32_t)bl_ << (16 * (e & 1));
-      d = d * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
+    const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (wj[e] * d);
+    const float r = j0 + e < h ? kd : 0.f;
+    const bf16_t bh_ = f2bf(r);
+    const bf16_t bl_ = f2bf(r - bf2f(bh_));
+    if (e & 1) {
+      hw[e >> 1] = (uint32_t)bh_ << 16;
+      lw[e >> 1] = (uint32_t)bl_ << 16;
+    } else {
+      hw[e >> 1] |= (uint32_t)bh_;
+      lw[e >> 1] |= (uint32_t)bl_;
     }
+    d = d * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
