@@ -889,7 +889,7 @@ def main():
     del conv, xconv
 
     # ---- 8 copies of 64 MiB: the known-size kernel that calibrates the FETCH_SIZE / WRITE_SIZE counters when this
-    # same command runs under rocprofv3 --pmc (bytes per launch of the step: profiles/gdn_step_B64_traffic.json) ----
+    # same command runs under rocprofv3 --pmc (bytes per launch of the step: profiles/hbm_traffic.json) ----
     src = torch.empty(64 * 2 ** 20 // 4, device=dev)
     dst = torch.empty_like(src)
     for _ in range(8):
