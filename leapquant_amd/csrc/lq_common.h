@@ -256,6 +256,9 @@ __attribute__((visibility("hidden"))) int lq_check_flush(const lq_state* st, con
 // the four-wave prefill dequant of GDN 128 x 128 heads at R <= 4 (lq_dequant.hip); arguments checked by lq_dequant
 __attribute__((visibility("hidden"))) int lq_launch_dequant4(const lq_state* st, const int* idx, int N, float qmax,
                                                              hipStream_t s);
+// the four-wave prefill dequant of KDA heads (lq_dequant.hip); arguments checked by lq_kda_dequant
+__attribute__((visibility("hidden"))) int lq_launch_kda_dequant4(const lq_state* st, const int* idx, int N, float qmax,
+                                                                 hipStream_t s);
 // decode step of every row of io (GDN or KDA), due heads signalled through dlist when it is set (else st->ctl)
 __attribute__((visibility("hidden"))) int lq_launch_step(const lq_state* st, const lq_step_io* io, int kda, float glb,
                                                          int* dlist, hipStream_t s);

@@ -1220,122 +1220,6 @@ void quantize64_kernel(lq_state st, const float* __restrict__ Q0, const int* __r
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// prefill dequant, KDA (state.py:118-128): S = diag(exp(P)) applied to S0 = Q U^T + deq(Sq) over the key channels,
-// plus sum_{j<h} w_j u_j (K_j * D_j)^T with D_j = prod_{j<i<h} e_i, written in place as fp32.  The window is left as
-// it is (the checkpoint after the engine's prefill resets it).  w_j K_j D_j goes into the rank-h MFMA as three bf16
-// terms (hi, mid, lo: 24 significant bits), so the window part keeps fp32 accuracy.
-// ------------------------------------------------------------------------------------------------------------------
-struct KdaDeqShared {
-  bf16_t op[4][KD][OPS];       // [0..2] hi / mid / lo of w_j K_j[c] D_j[c] ([c][j]), [3] u_j[v] ([v][j])
-  float skl[KD];               // Sk / qmax
-  float svr[VD];               // Sv
-  float pcs[KD];               // exp(P)
-  float w[LPMAX];
-  f32x4 uoc[KD];               // U rows [c][r]
-  f32x4 qov[VD];               // Q rows [v][r]
-};
-
-__global__ __launch_bounds__(FT) __attribute__((amdgpu_waves_per_eu(2)))
-void kda_dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
-  __shared__ KdaDeqShared sh;
-  const int HV = st.HV, L = st.L, R = st.R;
-  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
-  const int slot = idx[n];
-  if (slot <= 0 || slot >= st.NS) return;
-  const long long sh_ = (long long)slot * HV + hv;
-  const int tid = threadIdx.x, l = lane_id(), w = wave_id(), q = l >> 4;
-  char* base = block_base(st, slot, hv);
-  const int8_t* Sq = (const int8_t*)base;
-  const float* Sk = (const float*)(base + VD * KD);
-  const float* Sv = Sk + KD;
-  const f16_t* UQ = (const f16_t*)(Sv + VD);
-  const int h = __builtin_amdgcn_readfirstlane(min(st.hcnt[sh_], L));   // uniform: one word per head
-  const int LP = h > 0 ? ((h + 31) & ~31) : 32;
-  const int cv = tid & 127;
-  const bool colt = tid < KD;
-  const float scv = colt ? Sk[cv] : Sv[cv];
-  float uqv[4];
-#pragma unroll
-  for (int a = 0; a < 4; ++a) uqv[a] = h2f(UQ[min(a, R - 1) * (KD + VD) + (colt ? 0 : KD) + cv]);
-  const float pbc = st.Pbuf[sh_ * KD + cv];
-  const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
-  // an empty window (h == 0, uniform: a slot just checkpointed) skips the window's loads, staging, scan and products
-  WinRegs win;
-  if (h > 0) load_window<true>(win, st, slot, hv, h, LP);
-  uint32_t wds[8];
-  load_code_words(wds, Sq);
-  f32x4 fac;
-#pragma unroll
-  for (int a = 0; a < 4; ++a) fac[a] = a < R ? uqv[a] : 0.f;
-  if (tid < KD) {
-    sh.skl[cv] = scv / qmax;
-    sh.pcs[cv] = expf(pbc);                                                           // state.py:128
-    sh.uoc[cv] = fac;
-  } else if (tid < KD + VD) {
-    sh.svr[cv] = scv;
-    sh.qov[cv] = fac;
-  }
-  if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
-  __syncthreads();
-  // window: raw keys / decays into op0 / op1, values into op3 (rows >= h: zero values)
-  if (h > 0) {
-    const int ch = win_chunk(LP);
-    if (ch < 16) {
-      const int j0 = 2 * win_pair(LP), c8 = ch * 8;
-      const uint32_t keep = (j0 < h ? 0x0000ffffu : 0u) | (j0 + 1 < h ? 0xffff0000u : 0u);
-      const uint32_t ka[4] = {win.k[0].x, win.k[0].y, win.k[0].z, win.k[0].w}, kb[4] = {win.k[1].x, win.k[1].y, win.k[1].z, win.k[1].w};
-      const uint32_t ua[4] = {win.u[0].x, win.u[0].y, win.u[0].z, win.u[0].w}, ub[4] = {win.u[1].x, win.u[1].y, win.u[1].z, win.u[1].w};
-      const uint32_t ga[4] = {win.g[0].x, win.g[0].y, win.g[0].z, win.g[0].w}, gb[4] = {win.g[1].x, win.g[1].y, win.g[1].z, win.g[1].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int x = e >> 1;
-        const uint32_t sel = (e & 1) ? 0x07060302u : 0x05040100u;
-        *(uint32_t*)&sh.op[0][c8 + e][j0] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
-        *(uint32_t*)&sh.op[1][c8 + e][j0] = (__builtin_amdgcn_perm(gb[x], ga[x], sel) & keep) | (0x3c003c00u & ~keep);
-        *(uint32_t*)&sh.op[3][c8 + e][j0] = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
-      }
-    }
-  }
-  if (h > 0) {
-    __syncthreads();
-    kda_key_scan<3>(sh.op, sh.w, h, LP);              // decayed keys, hi / mid / lo (state.py:124-127)
-  }
-  // S0 pc in the tile layout: (code Sk / qmax) Sv + sum_r Q[v][r] U[c][r], times exp(P[c]) (state.py:121-122, 128)
-  Tile t;
-  {
-    const int c0 = 16 * w + 4 * q;
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt) {
-      const int v = 16 * nt + (l & 15);
-      const float rv = sh.svr[v];
-      const f32x4 qo = sh.qov[v];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int c = c0 + i;
-        const f32x4 uo = sh.uoc[c];
-        float x = ((float)(int)(int8_t)(wds[nt] >> (8 * i)) * sh.skl[c]) * rv;
-#pragma unroll
-        for (int a = 0; a < 4; ++a) x = fmaf(qo[a], uo[a], x);
-        t.a[nt][i] = sh.pcs[c] * x;
-      }
-    }
-  }
-  if (h > 0) {
-    __syncthreads();                                  // decayed keys staged
-    rebuild_mfma(t, sh.op[0], sh.op[3], LP / 32);
-    rebuild_mfma(t, sh.op[1], sh.op[3], LP / 32);
-    rebuild_mfma(t, sh.op[2], sh.op[3], LP / 32);
-  }
-  __syncthreads();                                    // every wave has read its codes: the fp32 state may overwrite them
-  float* S = (float*)base;                            // plain stores: non-temporal ones measured slower here (113 -> 120 us)
-#pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    const int v = 16 * nt + (l & 15);
-    *(float4*)(S + v * KD + 16 * w + 4 * q) = make_float4(t.a[nt][0], t.a[nt][1], t.a[nt][2], t.a[nt][3]);
-  }
-}
-
-// ------------------------------------------------------------------------------------------------------------------
 // prefill dequant, GDN (kernels.py:2041-2123): S = P (deq(Sq) + Q U^T) + sum_{j<h} w_j u_j k_j^T, in place.  A head
 // of K_ x V_ < 128 x 128 runs zero-padded in the tile (see flush_head) and writes its own rows / columns only.
 // ------------------------------------------------------------------------------------------------------------------
@@ -1385,7 +1269,7 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   // an empty window (h == 0, uniform: the prefill of a slot just checkpointed) skips the window's loads, staging and
   // products
   WinRegs win;
-  if (h > 0) load_window<false, K_, V_>(win, st, slot, hv, h, LP);
+  if (h > 0) load_window<K_, V_>(win, st, slot, hv, h, LP);
   uint32_t wds[8];
   load_code_words<K_, V_>(wds, Sq);
   if (tid < KD + VD) {
@@ -1400,7 +1284,7 @@ void dequant_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   }
   if (tid < LPMAX) sh.w[tid] = tid < h ? wv : 0.f;
   __syncthreads();
-  if (h > 0) store_window<false>(sh, win, h, LP);
+  if (h > 0) store_window(sh, win, h, LP);
   Tile t;
   {
     const float inv = 1.0f / qmax;
@@ -1629,7 +1513,7 @@ extern "C" int lq_kda_dequant(const lq_state* st, const int* idx, int N, float q
   if (rc) return rc;
   if (N < 0 || (N > 0 && !idx) || !(qmax >= 1.f && qmax <= 127.f) || !st->Gbuf) return LQ_ERR_ARG;
   if (N == 0) return LQ_OK;
-  kda_dequant_kernel<<<dim3((unsigned)(N * st->HV)), FT, 0, (hipStream_t)stream>>>(*st, idx, qmax);
+  lq_launch_kda_dequant4(st, idx, N, qmax, (hipStream_t)stream);
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;
 }
 

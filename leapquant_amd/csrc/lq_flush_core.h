@@ -397,19 +397,17 @@ __device__ __forceinline__ void rebuild_mfma(Tile& t, const bf16_t (*A)[OPS], co
 
 // Window rows of one head, loaded up front (unconditional, clamped addresses; rows >= h and the padding to LP carry
 // zero weight).  Thread t takes the row pair (2 jp, 2 jp + 1), jp = t % (LP / 2), in the 8-column chunk t / (LP / 2)
-// (16 chunks; LP = 64 keeps every thread busy), so that each LDS write below holds two entries.  KDA also takes the
-// window's per-channel decays (Gbuf, same [j][c] layout as the keys).
+// (16 chunks; LP = 64 keeps every thread busy), so that each LDS write below holds two entries.
 struct WinRegs {
-  uint4 k[2], u[2], g[2];
+  uint4 k[2], u[2];
 };
 __device__ __forceinline__ int win_pair(int LP) { return opaque_tid() % (LP / 2); }
 __device__ __forceinline__ int win_chunk(int LP) { return opaque_tid() / (LP / 2); }
-template <bool KDA, int K_ = KD, int V_ = VD>
+template <int K_ = KD, int V_ = VD>
 __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int slot, int hv, int h, int LP) {
   const int G = st.HV / st.H, hk = hv / G, L = st.L;
   const bf16_t* Kb = (const bf16_t*)st.Kbuf + ((long long)slot * st.H + hk) * L * K_;
   const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv) * L * V_;
-  const f16_t* Gb = KDA ? (const f16_t*)st.Gbuf + ((long long)slot * st.HV + hv) * L * KD : nullptr;
   const int jp = win_pair(LP), c8 = min(win_chunk(LP), 15) * 8;
   const uint4 z = make_uint4(0u, 0u, 0u, 0u);       // columns past a K_ / V_ < 128 head: zero operands
 #pragma unroll
@@ -419,13 +417,11 @@ __device__ __forceinline__ void load_window(WinRegs& r, const lq_state& st, int 
     const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_ + (V_ == VD ? c8 : min(c8, V_ - 8)));
     r.k[k] = (K_ == KD || c8 < K_) ? kx : z;
     r.u[k] = (V_ == VD || c8 < V_) ? ux : z;
-    if (KDA) r.g[k] = *(const uint4*)(Gb + (long long)jr * KD + c8);
   }
 }
-// Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write.  GDN: op0 =
-// K_j[c], op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  KDA: op0 / op1 = raw K_j[c] / e_j[c] (turned
-// into the decayed key operands by kda_key_scan), op2 = u_j[v].  Rows j >= h carry zero values and, for KDA, decay 1.
-template <bool KDA, class SH>
+// Transposed into the rebuild operands [c or v][j], two entries (rows j0, j0 + 1) per 32-bit LDS write: op0 = K_j[c],
+// op1 / op2 = hi / lo of w_j u_j[v] (kernels.py:1501-1511).  Rows j >= h carry zero values.
+template <class SH>
 __device__ __forceinline__ void store_window(SH& sh, const WinRegs& r, int h, int LP) {
   const int ch = win_chunk(LP);
   if (ch >= 16) return;
@@ -434,98 +430,23 @@ __device__ __forceinline__ void store_window(SH& sh, const WinRegs& r, int h, in
   const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
   const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
   const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
-  const uint32_t ga[4] = {r.g[0].x, r.g[0].y, r.g[0].z, r.g[0].w}, gb[4] = {r.g[1].x, r.g[1].y, r.g[1].z, r.g[1].w};
-  const uint32_t keep = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const int x = e >> 1;
     const bool odd = e & 1;
     const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of column c8 + e
-    uint32_t* o0 = (uint32_t*)&sh.op[0][c8 + e][j0];
-    uint32_t* o1 = (uint32_t*)&sh.op[1][c8 + e][j0];
-    uint32_t* o2 = (uint32_t*)&sh.op[2][c8 + e][j0];
-    *o0 = __builtin_amdgcn_perm(kb[x], ka[x], sel);
-    if (!KDA) {
+    *(uint32_t*)&sh.op[0][c8 + e][j0] = __builtin_amdgcn_perm(kb[x], ka[x], sel);
+    {
       // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
 #pragma clang fp contract(off)
       const float wu0 = w0 * (odd ? bf_hi(ua[x]) : bf_lo(ua[x]));
       const float wu1 = w1 * (odd ? bf_hi(ub[x]) : bf_lo(ub[x]));
       const uint32_t hi = pk_bf16_kept(wu0, wu1);
-      *o1 = hi;
-      *o2 = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
-    } else {
-      *o1 = (__builtin_amdgcn_perm(gb[x], ga[x], sel) & keep) | (0x3c003c00u & ~keep);   // rows >= h: decay 1
-      *o2 = __builtin_amdgcn_perm(ub[x], ua[x], sel) & keep;
+      *(uint32_t*)&sh.op[1][c8 + e][j0] = hi;
+      *(uint32_t*)&sh.op[2][c8 + e][j0] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
     }
   }
 }
-// KDA key operands, in place over the raw keys op[0] and decays op[1] ([c][j]): op[0..NT-1] = the NT-term bf16 split
-// (hi, [mid,] lo) of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, state.py:124-127).
-// Four lanes per channel: lane s of a quad takes the s-th quarter of the window (LP / 4 = 8 or 16 entries, held in
-// registers) and walks it backwards.  The decay product it starts from, D at the top of its quarter, is the running
-// product of the later decays taken in the reference's own order (from the window's end down, one rounding per factor),
-// so every D_j is bit-identical to the sequential walk's: a product regrouped by quarters rounds differently, and the
-// key operands' cancellation in the rebuild turns those last-bit differences into fp16 flips of B.  The prefix costs a
-// lane up to 3 LP / 4 dependent multiplies; the per-entry split work stays divided four ways.  FT = 4 KD threads.
-template <int NT>
-__device__ __forceinline__ void kda_key_scan(bf16_t (*op)[KD][OPS], const float* wj, int h, int LP) {
-  static_assert(FT == 4 * KD, "one quad of lanes per channel");
-  const int tid = opaque_tid(), c = tid >> 2, s = tid & 3, seg = LP >> 2, jb = s * seg;
-  uint32_t ku[2][4], eu[2][4];
-#pragma unroll
-  for (int x = 1; x >= 0; --x) {
-    if (8 * x < seg) {
-      const uint4 kr = *(const uint4*)&op[0][c][jb + 8 * x];
-      const uint4 er = *(const uint4*)&op[1][c][jb + 8 * x];
-      ku[x][0] = kr.x; ku[x][1] = kr.y; ku[x][2] = kr.z; ku[x][3] = kr.w;
-      eu[x][0] = er.x; eu[x][1] = er.y; eu[x][2] = er.z; eu[x][3] = er.w;
-    }
-  }
-  float dcur = 1.0f;
-#pragma unroll
-  for (int sq = 3; sq >= 1; --sq) {                   // the later quarters, last first
-    const int q0 = sq * seg;
-    if (q0 < h) {                                     // rows >= h hold decay 1 (exact factors)
-      float t = dcur;
-#pragma unroll
-      for (int x = 1; x >= 0; --x) {
-        if (8 * x < seg) {
-          const uint4 er = *(const uint4*)&op[1][c][q0 + 8 * x];
-          const uint32_t ew[4] = {er.x, er.y, er.z, er.w};
-#pragma unroll
-          for (int e = 7; e >= 0; --e) t = t * h2f((f16_t)(ew[e >> 1] >> (16 * (e & 1))));
-        }
-      }
-      dcur = s < sq ? t : dcur;
-    }
-  }
-#pragma unroll
-  for (int x = 1; x >= 0; --x) {
-    if (8 * x < seg) {
-      const int j0 = jb + 8 * x;
-      uint32_t tw[NT][4] = {};
-#pragma unroll
-      for (int e = 7; e >= 0; --e) {
-        const int j = j0 + e;
-        if (j < h) {
-          // the split is of the fp32-rounded product (kernels.py:1456-1463): no fusing into the first subtraction
-#pragma clang fp contract(off)
-          float r = bf2f((bf16_t)(ku[x][e >> 1] >> (16 * (e & 1)))) * (wj[j] * dcur);
-#pragma unroll
-          for (int t = 0; t < NT; ++t) {
-            const bf16_t b = f2bf(r);
-            tw[t][e >> 1] |= (uint32_t)b << (16 * (e & 1));
-            r = r - bf2f(b);
-          }
-          dcur = dcur * h2f((f16_t)(eu[x][e >> 1] >> (16 * (e & 1))));
-        }
-      }
-#pragma unroll
-      for (int t = 0; t < NT; ++t) *(uint4*)&op[t][c][j0] = make_uint4(tw[t][0], tw[t][1], tw[t][2], tw[t][3]);
-    }
-  }
-}
-
 // per-wave partial sums of the row reductions -> the full sum for row v (threads v < 128)
 __device__ __forceinline__ f32x4 sum_parts(const f32x4 (*part)[VD], int v) {
   f32x4 s = part[0][v];
@@ -669,7 +590,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   }
   const float wv = st.Wbuf[sh_ * L + min(tid, L - 1)];
   WinRegs win;
-  load_window<false, K_, V_>(win, st, slot, hv, L, LP);
+  load_window<K_, V_>(win, st, slot, hv, L, LP);
   uint32_t wds[8];
   load_code_words<K_, V_>(wds, Sq);
 
@@ -705,7 +626,7 @@ __device__ void flush_head(FlushShared<RA>& sh, const lq_state& st, const float*
   }
   if (tid < LPMAX) sh.w[tid] = tid < L ? wv : 0.f;
   __syncthreads();
-  store_window<false>(sh, win, L, LP);
+  store_window(sh, win, L, LP);
   __syncthreads();
 
   // ---- stage 2: B = deq(S0) pn + window, fp16 (kernels.py:1483-1571) ----
@@ -1077,17 +998,21 @@ __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf&
   }
 }
 // KDA key operands of one staged half, in place over its raw keys op[0] and decays op[1] ([c][j - HALF hf]): op[0] /
-// op[1] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463, as kda_key_scan).  The
+// op[1] = hi / lo of K_j[c] w_j D_j[c], D_j = prod_{j < i < h} e_i[c] (kernels.py:1453-1463).  The
 // halves are staged newest first: dcar is D at the top of this half (the product of every later decay; 1 for the
 // newest half), and the return value is the carry for the next, older half.  Two lanes per channel (c = t / 2): lane s
 // takes entries 16 s .. 16 s + 15 and walks them backwards; lane 0 first multiplies through lane 1's decays (handed
 // over by DPP), so that every D_j is the sequential walk's own product, one rounding per factor in the reference's
 // order (a regrouped product rounds differently, and the key operands' cancellation in the rebuild turns such last-bit
-// differences into fp16 flips of B).  Each lane reads and writes its own 16 entries only.
-template <bool CF>
-__device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar, int h, int hf) {
+// differences into fp16 flips of B).  Each lane reads and writes its own 16 entries only.  NT = 3 (the prefill dequant,
+// state.py:124-127): the split is hi / mid / lo, op[0] / op[1] take hi / mid and lo3 the lane's lo words ([c][j] as
+// the LDS rows: word x holds entries jb + 2 x, jb + 2 x + 1 of channel c).
+template <int NT = 2, bool CF>
+__device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar, int h, int hf,
+                                               uint32_t* lo3 = nullptr) {
   // the split is of the fp32-rounded product (kernels.py:1456-1463): no fusing into the first subtraction
 #pragma clang fp contract(off)
+  static_assert(NT == 2 || NT == 3, "two or three bf16 terms");
   const int t = opaque_tid(), c = t >> 1, s = t & 1, jb = 16 * s, j0 = HALF * hf + jb;
   uint32_t ku[8], eu[8];
 #pragma unroll
@@ -1111,22 +1036,30 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
     const float4 w4 = *(const float4*)&sh.w[j0 + 4 * x];
     wj[4 * x] = w4.x; wj[4 * x + 1] = w4.y; wj[4 * x + 2] = w4.z; wj[4 * x + 3] = w4.w;
   }
-  uint32_t hw[8], lw[8];
+  uint32_t hw[8], lw[8], tw[8];                       // hi, second and (NT = 3) third terms
   // no branch per entry: rows >= h hold decay 1 (d passes unchanged) and take zero operands
 #pragma unroll
   for (int e = 15; e >= 0; --e) {
     const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (wj[e] * d);
     const float r = j0 + e < h ? kd : 0.f;
     const bf16_t bh_ = f2bf(r);
-    const bf16_t bl_ = f2bf(r - bf2f(bh_));
+    const float r1 = r - bf2f(bh_);
+    const bf16_t bl_ = f2bf(r1);
+    const bf16_t bt_ = NT == 3 ? f2bf(r1 - bf2f(bl_)) : (bf16_t)0;
     if (e & 1) {
       hw[e >> 1] = (uint32_t)bh_ << 16;
       lw[e >> 1] = (uint32_t)bl_ << 16;
+      tw[e >> 1] = (uint32_t)bt_ << 16;
     } else {
       hw[e >> 1] |= (uint32_t)bh_;
       lw[e >> 1] |= (uint32_t)bl_;
+      tw[e >> 1] |= (uint32_t)bt_;
     }
     d = d * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
+  }
+  if constexpr (NT == 3) {
+#pragma unroll
+    for (int x = 0; x < 8; ++x) lo3[x] = tw[x];
   }
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
@@ -1199,6 +1132,19 @@ __device__ __forceinline__ void rebuild_half4x2a(Tile4& t, const bf16_t (*A1)[OP
     for (int g = 0; g < 2; ++g) t.a[g][n2 + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a2[g], c1, t.a[g][n2 + 1], 0, 0, 0);
     __builtin_amdgcn_sched_barrier(0);
     if (it + 1 < 4) { c0 = n0; c1 = n1; }
+  }
+}
+// acc[c][v] += sum_j A[c][j] B[v][j] over one staged half, one bf16 term (the prefill dequant's third key term)
+__device__ __forceinline__ void rebuild_half4x1(Tile4& t, const bf16_t (*A)[OPS4], const bf16_t (*B)[OPS4]) {
+  const int l = lane_id(), w = wave_id(), q = l >> 4;
+  bf16x8 af[2];
+#pragma unroll
+  for (int g = 0; g < 2; ++g) af[g] = *(const bf16x8*)&A[32 * w + 16 * g + (l & 15)][8 * q];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) {
+    const bf16x8 b = *(const bf16x8*)&B[16 * nt + (l & 15)][8 * q];
+#pragma unroll
+    for (int g = 0; g < 2; ++g) t.a[g][nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af[g], b, t.a[g][nt], 0, 0, 0);
   }
 }
 // the 16 code words of the lane's tile entries, wds[g][nt] = Sq[16 nt + l16][32 w + 16 g + 4 q .. + 3] (zero past a

@@ -89,7 +89,7 @@ LAUNCH_BLOCK = {
     "quantize_kernel": lambda t: 256,
     "quantize64_kernel": lambda t: 256,
     "dequant_kernel": lambda t: 512,
-    "kda_dequant_kernel": lambda t: 512,
+    "kda_dequant4_kernel": lambda t: 256,
     "lowrank_kernel": lambda t: 512,
 }
 
