@@ -36,6 +36,12 @@ __device__ __forceinline__ uint32_t pk_bf16_kept(float lo, float hi) {
   return w;
 }
 // bf16 halves of a word as fp32
+// x, or zero where !ok, word by word: a select of whole uint4 values can be lowered through a private array indexed
+// at run time (scratch memory), which a mask on each word never is
+__device__ __forceinline__ uint4 keep4(uint4 x, bool ok) {
+  const uint32_t m = ok ? 0xffffffffu : 0u;
+  return make_uint4(x.x & m, x.y & m, x.z & m, x.w & m);
+}
 __device__ __forceinline__ float bf_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 __device__ __forceinline__ float bfround(float f) { return bf2f(f2bf(f)); }

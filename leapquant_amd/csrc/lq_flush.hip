@@ -231,14 +231,13 @@ __device__ __forceinline__ void load_half64(WinHalf& r, const lq_state& st, int 
   const int hh = min(c8 / V_, HP - 1), v = c8 - hh * V_;
   const bool uok = c8 < HP * V_ && ((mask >> hh) & 1);
   const bf16_t* Ub = (const bf16_t*)st.Ubuf + ((long long)slot * st.HV + hv0 + hh) * L * V_ + (c8 < HP * V_ ? v : 0);
-  const uint4 z = make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
   for (int k = 0; k < 2; ++k) {
     const int j = HALF * hf + 2 * jp + k, jr = j < L ? j : 0;
     const uint4 kx = *(const uint4*)(Kb + (long long)jr * K64 + min(c8, K64 - 8));
     const uint4 ux = *(const uint4*)(Ub + (long long)jr * V_);
-    r.k[k] = c8 < K64 ? kx : z;
-    r.u[k] = uok ? ux : z;
+    r.k[k] = keep4(kx, c8 < K64);
+    r.u[k] = keep4(ux, uok);
   }
 }
 template <int V_, int HP>
