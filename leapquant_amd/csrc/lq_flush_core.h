@@ -1442,6 +1442,14 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
   __syncthreads();
   f32x4 u16[2];
   p_step4<false>(sh, bh, bt, pn, R, u16);             // U16 = P step with Q16 (lanes < 16)
+  if constexpr (K_ == KD && V_ == VD) {               // U16^T to LDS (P16^T is read no more) for the factor stores
+    if (q == 0) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 16 * g + l16] = f2h(u16[g][r]);
+    }
+  }
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
   // E is kept packed (fp16, in B's registers: B is dead after the U step); the products B / pn, E rsk and the |E| sums
@@ -1565,16 +1573,27 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
     }
   }
   // ---- stage 7: factors, window reset (kernels.py:1836-1842, 2014-2025) ----
-  if (q == 0) {
-#pragma unroll
-    for (int g = 0; g < 2; ++g) {
-      const int c = 32 * w + 16 * g + l16;
-      if (K_ == KD || c < K_)
-        for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16[g][r]);
+  if constexpr (K_ == KD && V_ == VD) {
+    // the factor rows [U_r | Q_r] from their fp16 tables (U16^T above, Q16^T from the CholeskyQR): thread t writes
+    // halfs 4 (t % 64) .. + 3 of row t / 64, one 8-byte store each, where per-lane 2-byte stores took twelve
+    // instructions a wave
+    const int r = tid >> 6, c4 = 4 * (tid & 63);
+    if (r < R) {
+      const uint2 x = c4 < KD ? *(const uint2*)&sh.r.ppT[r][c4] : *(const uint2*)&sh.qT[r][c4 - KD];
+      *(uint2*)&UQ[r * (KD + VD) + c4] = x;
     }
-  }
-  if (tid < V_) {
-    for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+  } else {
+    if (q == 0) {
+#pragma unroll
+      for (int g = 0; g < 2; ++g) {
+        const int c = 32 * w + 16 * g + l16;
+        if (c < K_)
+          for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16[g][r]);
+      }
+    }
+    if (tid < V_) {
+      for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
+    }
   }
   if constexpr (KDA) {
     if (tid < KD) st.Pbuf[sh_ * KD + tid] = 0.f;
