@@ -209,7 +209,7 @@ def _flush_case(rng, kda, L, qmax=127.0, NS=6, HV=4, H=2):
 
 
 @pytest.mark.parametrize("kda", [False, True])
-@pytest.mark.parametrize("L", [16, 64])
+@pytest.mark.parametrize("L", [16, 48, 64])       # 48: the second window half (KDA: staged first) holds 16 entries
 def test_flush_matches_oracle(kda, L):
     rng = np.random.default_rng(200 + L + 7 * kda)
     st, Q0 = _flush_case(rng, kda, L)
