@@ -436,18 +436,18 @@ def test_kda_round_trip_matches_oracle(L, steps):
 
 
 def test_kda_dequant_empty_and_partial_windows():
-    """One KDA prefill dequant over heads with an empty window (h == 0: no window loads, scan or products) and heads with
-    a partial one (past one 32-entry operand block), padding rows between them: every listed slot against the oracle's
-    rebuild, an unlisted slot's bytes untouched."""
+    """One KDA prefill dequant over heads with an empty window (h == 0: no window loads, scan or products), a partial
+    one (h = 37: the newer 32-entry half holds 5 entries) and a full one (h = 64: both halves), padding rows between
+    them: every listed slot against the oracle's rebuild, an unlisted slot's bytes untouched."""
     rng = np.random.default_rng(902)
     NS, HV, H = 6, 4, 4
     st, S, Q0 = make_state(rng, NS, HV, H, L=64, kda=True)
     A_log, dt_bias = gate_params(HV, 128, True)
-    for _ in range(37):                                 # slots 2 and 5 only: h = 37; slots 1, 3, 4 stay at h = 0
-        sl = np.array([2, 5])
+    for t in range(64):                                 # slots 2, 5: h = 37; slot 4: h = 64; slots 1, 3 stay at 0
+        sl = np.array([2, 4, 5]) if t < 37 else np.array([4])
         mixed, a, b = make_inputs(rng, len(sl), HV, H, kda=True)
         O.kda_step(st, mixed, a, b, A_log, dt_bias, sl)
-    assert np.all(st["hcnt"][[2, 5]] == 37) and np.all(st["hcnt"][[1, 3, 4]] == 0)
+    assert np.all(st["hcnt"][[2, 5]] == 37) and np.all(st["hcnt"][4] == 64) and np.all(st["hcnt"][[1, 3]] == 0)
     idx = np.array([1, 2, 0, 4, 5], np.int64)
     ssm, lq = G.to_gpu(st)
     before = ssm[3].view(torch.int32).clone()          # checkpoint bytes (as floats some are NaN)
