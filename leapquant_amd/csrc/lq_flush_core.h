@@ -191,18 +191,22 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
 }
 
 // CholeskyQR pass with the reference's pivot floors (kernels.py:1778-1835): 1 / L factors of the 4 x 4 Gram (packed
-// lower triangle), then the rows times L^-T
+// lower triangle), then the rows times L^-T.  The reciprocal square roots are the hardware's (v_rsq_f32, about 1 ulp),
+// as the reference's are approximate (T.rsqrt): the four of them are the serial spine of the factorisation on wave 0,
+// and the correctly rounded 1 / sqrtf in their place cost the flush 3.5% (config 3, 188.4 -> 181.8 us with these) and
+// the KDA flush 6% (125.8 -> 118.7 us).  The factors round to fp16 afterwards, and the oracle factorises in fp64, so
+// the parity bars see no difference (every GPU test unchanged).
 __device__ __forceinline__ void chol4(const float gg[10], float ll[10]) {
-  ll[0] = rsqrtf_rn(fmaxf(gg[0], 1e-30f));
+  ll[0] = __builtin_amdgcn_rsqf(fmaxf(gg[0], 1e-30f));
   ll[1] = gg[1] * ll[0];
-  ll[2] = rsqrtf_rn(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
+  ll[2] = __builtin_amdgcn_rsqf(fmaxf(fmaxf(gg[2] - ll[1] * ll[1], 1e-6f * gg[2]), 1e-30f));
   ll[3] = gg[3] * ll[0];
   ll[4] = (gg[4] - ll[3] * ll[1]) * ll[2];
-  ll[5] = rsqrtf_rn(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
+  ll[5] = __builtin_amdgcn_rsqf(fmaxf(fmaxf(gg[5] - ll[3] * ll[3] - ll[4] * ll[4], 1e-6f * gg[5]), 1e-30f));
   ll[6] = gg[6] * ll[0];
   ll[7] = (gg[7] - ll[6] * ll[1]) * ll[2];
   ll[8] = (gg[8] - ll[6] * ll[3] - ll[7] * ll[4]) * ll[5];
-  ll[9] = rsqrtf_rn(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
+  ll[9] = __builtin_amdgcn_rsqf(fmaxf(fmaxf(gg[9] - ll[6] * ll[6] - ll[7] * ll[7] - ll[8] * ll[8], 1e-6f * gg[9]), 1e-30f));
 }
 __device__ __forceinline__ void chol4_solve(const float ll[10], f32x4& p) {
   p[0] = p[0] * ll[0];
