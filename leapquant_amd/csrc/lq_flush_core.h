@@ -214,26 +214,61 @@ __device__ __forceinline__ void chol4_solve(const float ll[10], f32x4& p) {
   p[2] = (p[2] - p[0] * ll[3] - p[1] * ll[4]) * ll[5];
   p[3] = (p[3] - p[0] * ll[6] - p[1] * ll[7] - p[2] * ll[8]) * ll[9];
 }
+// The 10 entries of a 4 x 4 Gram from the lanes' partial sums x[k], summed over the wave.  The ten sums share their
+// lane exchanges: a swap32 round adds the lane rows r, r + 2 of entry pairs (k, k + 5), a swap16 round adds rows r,
+// r + 1 of the results, after which each 16-lane row of three registers holds a different entry summed over the four
+// rows; one DPP pass sums within the rows and each entry is read from its row (~50 instructions where ten wave
+// all-reductions take ~110, on wave 0's serial chain).
+__device__ __forceinline__ void gram_sum10(const float x[10], float g[10]) {
+  float y[5];
+#pragma unroll
+  for (int i = 0; i < 5; ++i) {                       // rows 0-1: entry i; rows 2-3: entry i + 5
+    uint32_t a = __float_as_uint(x[i]), b = __float_as_uint(x[i + 5]);
+    swap32(a, b);
+    y[i] = __uint_as_float(a) + __uint_as_float(b);
+  }
+  float z[3];
+  {
+    uint32_t a = __float_as_uint(y[0]), b = __float_as_uint(y[1]);
+    swap16(a, b);
+    z[0] = sum16(__uint_as_float(a) + __uint_as_float(b));   // rows: entries 0, 1, 5, 6
+  }
+  {
+    uint32_t a = __float_as_uint(y[2]), b = __float_as_uint(y[3]);
+    swap16(a, b);
+    z[1] = sum16(__uint_as_float(a) + __uint_as_float(b));   // rows: entries 2, 3, 7, 8
+  }
+  {
+    uint32_t a = __float_as_uint(y[4]), b = a;
+    swap16(a, b);
+    z[2] = sum16(__uint_as_float(a) + __uint_as_float(b));   // rows: entries 4, 4, 9, 9
+  }
+  g[0] = rl(z[0], 0);  g[1] = rl(z[0], 16); g[5] = rl(z[0], 32); g[6] = rl(z[0], 48);
+  g[2] = rl(z[1], 0);  g[3] = rl(z[1], 16); g[7] = rl(z[1], 32); g[8] = rl(z[1], 48);
+  g[4] = rl(z[2], 0);  g[9] = rl(z[2], 32);
+}
 // on the 2 rows (l, l + 64) a lane of wave 0 holds: the Gram over all 128 rows
 __device__ __forceinline__ void cholqr_pass(f32x4& p0, f32x4& p1) {
-  float gg[10], ll[10];
+  float gx[10], gg[10], ll[10];
   int k = 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(fmaf(p0[r], p0[c], p1[r] * p1[c]));
+    for (int c = 0; c <= r; ++c) gx[k++] = fmaf(p0[r], p0[c], p1[r] * p1[c]);
+  gram_sum10(gx, gg);
   chol4(gg, ll);
   chol4_solve(ll, p0);
   chol4_solve(ll, p1);
 }
 // on the one row a lane holds: the Gram over the wave's 64 rows (one head of a pair, K = 64 flush)
 __device__ __forceinline__ void cholqr_pass1(f32x4& p) {
-  float gg[10], ll[10];
+  float gx[10], gg[10], ll[10];
   int k = 0;
 #pragma unroll
   for (int r = 0; r < 4; ++r)
 #pragma unroll
-    for (int c = 0; c <= r; ++c) gg[k++] = sum64u(p[r] * p[c]);
+    for (int c = 0; c <= r; ++c) gx[k++] = p[r] * p[c];
+  gram_sum10(gx, gg);
   chol4(gg, ll);
   chol4_solve(ll, p);
 }
