@@ -51,9 +51,11 @@ __device__ __forceinline__ f16_t f2h(float f) { return __builtin_bit_cast(f16_t,
 __device__ __forceinline__ float hround(float f) { return (float)(_Float16)f; }
 
 // ---- wave64 lane exchange (DPP: fused into the consuming VALU op, no LDS traffic) -------------------------------
+// Every pattern used here (quad_perm, row_mirror, row_half_mirror) reads a lane of the same row, so every lane has a
+// source: bound_ctrl only tells the compiler that no old value is needed (no move to initialise the destination).
 template <int CTRL>
 __device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
 }
 #define DPP_XOR1 0xb1          // quad_perm [1,0,3,2]
 #define DPP_XOR2 0x4e          // quad_perm [2,3,0,1]

@@ -1008,22 +1008,38 @@ template <bool KDA = false, bool CF>
 __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf& r, int h, int hf) {
   // the split is of the fp32-rounded product: no fusing of w u into the lo subtraction (kernels.py:1509-1511)
 #pragma clang fp contract(off)
-  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8, ro = CF ? 4 * ((t / 16) & 1) : 0;
+  const int t = opaque_tid(), jl = 2 * (t % 16), c8 = (t / 16) * 8;
+  const bool rot = CF && ((t / 16) & 1);
   const int j0 = HALF * hf + jl;
   const bool v0 = j0 < h, v1 = j0 + 1 < h;
   const float w0 = v0 ? sh.w[j0] : 0.f, w1 = v1 ? sh.w[j0 + 1] : 0.f;
-  const uint32_t ka[4] = {r.k[0].x, r.k[0].y, r.k[0].z, r.k[0].w}, kb[4] = {r.k[1].x, r.k[1].y, r.k[1].z, r.k[1].w};
-  const uint32_t ua[4] = {r.u[0].x, r.u[0].y, r.u[0].z, r.u[0].w}, ub[4] = {r.u[1].x, r.u[1].y, r.u[1].z, r.u[1].w};
-  const uint32_t ga[4] = {r.g[0].x, r.g[0].y, r.g[0].z, r.g[0].w}, gb[4] = {r.g[1].x, r.g[1].y, r.g[1].z, r.g[1].w};
+  // the words of the lane's columns in the order it writes them: a rotated lane group's write e takes column
+  // (e + 4) mod 8, i.e. word (x + 2) mod 4, so its words are permuted once here (one select each) instead of per write
+  auto words = [&](const uint4& v, uint32_t (&o)[4]) {
+    o[0] = rot ? v.z : v.x;
+    o[1] = rot ? v.w : v.y;
+    o[2] = rot ? v.x : v.z;
+    o[3] = rot ? v.y : v.w;
+  };
+  uint32_t ka[4], kb[4], ua[4], ub[4], ga[4], gb[4];
+  words(r.k[0], ka);
+  words(r.k[1], kb);
+  words(r.u[0], ua);
+  words(r.u[1], ub);
+  if constexpr (KDA) {
+    words(r.g[0], ga);
+    words(r.g[1], gb);
+  }
   const uint32_t keep = (v0 ? 0x0000ffffu : 0u) | (v1 ? 0xffff0000u : 0u);
+  // column of write e: c8 + (e + 4 rot) mod 8 = cA + e for e < 4, cB + e for e >= 4 (two bases, constant offsets)
+  const int cA = c8 + (rot ? 4 : 0), cB = c8 - (rot ? 4 : 0);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int x = e >> 1, xr = ((e + 4) & 7) >> 1;     // the word of column e, and of column e + 4 (odd groups)
-    const bool rot = ro != 0, odd = e & 1;
+    const int x = e >> 1;
+    const bool odd = e & 1;
     const uint32_t sel = odd ? 0x07060302u : 0x05040100u;   // the two rows' halves of the column
-    const int c = c8 + ((e + ro) & 7);
-    const uint32_t kax = rot ? ka[xr] : ka[x], kbx = rot ? kb[xr] : kb[x];
-    const uint32_t uax = rot ? ua[xr] : ua[x], ubx = rot ? ub[xr] : ub[x];
+    const int c = (e < 4 ? cA : cB) + e;
+    const uint32_t kax = ka[x], kbx = kb[x], uax = ua[x], ubx = ub[x];
     *(uint32_t*)&sh.op[0][c][jl] = __builtin_amdgcn_perm(kbx, kax, sel);
     if constexpr (!KDA) {
       const float wu0 = w0 * (odd ? bf_hi(uax) : bf_lo(uax));
@@ -1032,7 +1048,7 @@ __device__ __forceinline__ void store_half(FlushShared4T<CF>& sh, const WinHalf&
       *(uint32_t*)&sh.op[1][c][jl] = hi;
       *(uint32_t*)&sh.op[2][c][jl] = pk_bf16(wu0 - bf_lo(hi), wu1 - bf_hi(hi));
     } else {
-      const uint32_t gax = rot ? ga[xr] : ga[x], gbx = rot ? gb[xr] : gb[x];
+      const uint32_t gax = ga[x], gbx = gb[x];
       *(uint32_t*)&sh.op[1][c][jl] = (__builtin_amdgcn_perm(gbx, gax, sel) & keep) | (0x3c003c00u & ~keep);
       *(uint32_t*)&sh.op[2][c][jl] = __builtin_amdgcn_perm(ubx, uax, sel) & keep;
     }
