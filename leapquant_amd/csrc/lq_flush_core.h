@@ -1281,14 +1281,16 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4T<CF>& sh, float M
 #pragma unroll
     for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
 }
-// P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lanes
-// l < 16 return P[32 w + 16 g + l][0..3] (zero for r >= R) in p[g]; the other lanes zeros.  The contraction runs over
-// v, so each block of B is transposed (one exact MFMA against the identity: lane l then holds
+// P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lane
+// (q, l16) returns P[32 w + 16 g + l16][0..3] for g = q >> 1 (zero for r >= R).  The contraction runs over v, so each
+// block of B is transposed (one exact MFMA against the identity: lane l then holds
 // B[32 w + 16 g + (l & 15)][16 nt + 4 (l >> 4) + i]); the first call (TR) forms the transposed blocks into bt, the
-// second (the U step) reads them from there.
+// second (the U step) reads them from there.  The A operand's rows m >= 4 repeat rows m mod 4, so every lane group
+// holds the same rows of P^T: the lane groups 0-1 finish channel group 0 and 2-3 group 1, each correction once per
+// lane instead of both groups in every lane (the same values).
 template <bool TR, bool CF>
 __device__ __forceinline__ void p_step4(const FlushShared4T<CF>& sh, const f16x4 (&bh)[2][8], f16x4 (&bt)[2][8], float pn,
-                                        int R, f32x4 p[2]) {
+                                        int R, f32x4& pg) {
   const int l = lane_id(), w = wave_id(), q = l >> 4, l16 = l & 15;
   float M[4][4];
   gram_qold_q(sh, M);
@@ -1305,14 +1307,13 @@ __device__ __forceinline__ void p_step4(const FlushShared4T<CF>& sh, const f16x4
       pacc[g] = mma16(aq, bt[g][nt], pacc[g]);
     }
   }
+  const bool g1 = q >= 2;
+  const f32x4 uo = sh.uoc[32 * w + 16 * (g1 ? 1 : 0) + l16];
 #pragma unroll
-  for (int g = 0; g < 2; ++g) {
-    const f32x4 uo = sh.uoc[32 * w + 16 * g + l16];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
-      p[g][r] = (q == 0 && r < R) ? hround(pacc[g][r] + pn * corr) : 0.f;
-    }
+  for (int r = 0; r < 4; ++r) {
+    const float pa = g1 ? pacc[1][r] : pacc[0][r];
+    const float corr = uo[0] * M[0][r] + uo[1] * M[1][r] + uo[2] * M[2][r] + uo[3] * M[3][r];
+    pg[r] = r < R ? hround(pa + pn * corr) : 0.f;
   }
 }
 
@@ -1429,14 +1430,12 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
   __syncthreads();
 
   // ---- stage 3: subspace iteration (ITERS = 1) with the algebraic rank-R corrections (kernels.py:1580-1842) ----
-  f32x4 p16[2];
+  f32x4 p16;
   f16x4 bt[2][8];                                     // B^T blocks, formed by the first P step
-  p_step4<true>(sh, bh, bt, pn, R, p16);              // P16 rows of this wave's channels (lanes < 16)
-  if (q == 0) {
+  p_step4<true>(sh, bh, bt, pn, R, p16);              // P16 rows of channel group q >> 1 of this wave's channels
+  if ((q & 1) == 0) {
 #pragma unroll
-    for (int g = 0; g < 2; ++g)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 16 * g + l16] = f2h(p16[g][r]);
+    for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 8 * q + l16] = f2h(p16[r]);
   }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
@@ -1497,15 +1496,23 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
     __builtin_amdgcn_s_setprio(0);
   }
   __syncthreads();
-  f32x4 u16[2];
-  p_step4<false>(sh, bh, bt, pn, R, u16);             // U16 = P step with Q16 (lanes < 16)
+  f32x4 u16g;
+  p_step4<false>(sh, bh, bt, pn, R, u16g);            // U16 = P step with Q16 (channel group q >> 1)
   if constexpr (K_ == KD && V_ == VD) {               // U16^T to LDS (P16^T is read no more) for the factor stores
-    if (q == 0) {
+    if ((q & 1) == 0) {
 #pragma unroll
-      for (int g = 0; g < 2; ++g)
-#pragma unroll
-        for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 16 * g + l16] = f2h(u16[g][r]);
+      for (int r = 0; r < 4; ++r) sh.r.ppT[r][32 * w + 8 * q + l16] = f2h(u16g[r]);
     }
+  }
+  // -U16 of both channel groups in the lanes l < 16 (the residual's A operand): group 1 from lane l + 32
+  f16x4 nu16[2];
+  {
+    const uint2 x = h4_words(to_h4(-u16g));
+    uint32_t a0 = x.x, b0 = x.x, a1 = x.y, b1 = x.y;
+    swap32(a0, b0);                                   // b0, b1 of lanes 0-31: the words of lanes 32-63
+    swap32(a1, b1);
+    nu16[0] = __builtin_bit_cast(f16x4, x);
+    nu16[1] = __builtin_bit_cast(f16x4, make_uint2(b0, b1));
   }
 
   // ---- stage 4: residual E = fp16(pn (B / pn + Q_old U_old^T) - Q U^T) (kernels.py:1888-1928) ----
@@ -1517,7 +1524,7 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
 #pragma unroll
     for (int g = 0; g < 2; ++g) {
       auo[g] = q == 0 ? to_h4(sh.uoc[32 * w + 16 * g + l16]) : z4;                  // A[c][a] = U_old
-      aun[g] = q == 0 ? to_h4(-u16[g]) : z4;                                        // A[c][r] = -U16
+      aun[g] = q == 0 ? nu16[g] : z4;                                               // A[c][r] = -U16
     }
 #pragma unroll
     for (int nt = 0; nt < 8; ++nt) {
@@ -1640,13 +1647,10 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
       *(uint2*)&UQ[r * (KD + VD) + c4] = x;
     }
   } else {
-    if (q == 0) {
-#pragma unroll
-      for (int g = 0; g < 2; ++g) {
-        const int c = 32 * w + 16 * g + l16;
-        if (c < K_)
-          for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16[g][r]);
-      }
+    if ((q & 1) == 0) {
+      const int c = 32 * w + 8 * q + l16;
+      if (c < K_)
+        for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + c] = f2h(u16g[r]);
     }
     if (tid < V_) {
       for (int r = 0; r < R; ++r) UQ[r * (K_ + V_) + K_ + tid] = f2h(sh.qv[tid][r]);
