@@ -703,6 +703,8 @@ struct QuantShared {
   f32x4 qpart[QW][VD];               // one block's per-wave partial rows at a time
   float rowmax[QW][VD];
   float sk[KD];
+  float rsk[KD];                     // 1 / Sk per column
+  float rsv[VD];                     // qmax / Sv per row
 };
 
 // column sums sum_v M[v][c] X[v][r] for this lane's channels: fn(cg, i, s) once per (group, channel) with the full sum
@@ -883,9 +885,9 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 32 * w + 16 * cg + 4 * q + i;
-      f32x4 unc[NB];
+      f32x4 nunc[NB];                                 // -U of the column, negated once (fma(q, -u, e) = fma(-q, u, e))
 #pragma unroll
-      for (int b = 0; b < NB; ++b) unc[b] = sh.pp[b][c];
+      for (int b = 0; b < NB; ++b) nunc[b] = -sh.pp[b][c];
       float s = 0.f;
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt) {
@@ -894,7 +896,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
         for (int b = 0; b < NB; ++b) {
           const f32x4 qnv = sh.qv[b][16 * nt + (l & 15)];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[b][r], e);
+          for (int r = 0; r < 4; ++r) e = fmaf(qnv[r], nunc[b][r], e);
         }
         t.a[cg][nt][i] = e;
         s += fabsf(e);
@@ -902,15 +904,25 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
       s = sum16(s);
       const float skc = fmaxf(sqrtf(s / (float)V_), LQ_EPS);      // kernels.py:2222
       if ((l & 15) == 0) sh.sk[c] = skc;
+      // one column at a time: without this the compiler requests the next columns' U rows early and the kernel
+      // spills (118 -> 128 VGPRs and 28 bytes of scratch per lane; the quantize then ran 18% slower)
+      __builtin_amdgcn_sched_barrier(0);
     }
   __syncthreads();
   // E / Sk and E / (Sk Sv) (kernels.py:2224-2229) as products with reciprocals taken once per column and once per row
-  // (within a few ulp of the quotients, below the codes' rounding step)
+  // (within a few ulp of the quotients, below the codes' rounding step).  Each reciprocal is formed by one lane and
+  // shared through LDS: lane l < 32 of wave w takes column 32 w + l (one division per lane, where each lane formed the
+  // reciprocals of its own eight columns, the same eight in all 16 lanes of its row)
+  if (l < 32) sh.rsk[32 * w + l] = 1.0f / sh.sk[32 * w + l];
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   float rsk[2][4];
 #pragma unroll
-  for (int cg = 0; cg < 2; ++cg)
+  for (int cg = 0; cg < 2; ++cg) {
+    const f32x4 r4 = *(const f32x4*)&sh.rsk[32 * w + 16 * cg + 4 * q];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) rsk[cg][i] = 1.0f / sh.sk[32 * w + 16 * cg + 4 * q + i];
+    for (int i = 0; i < 4; ++i) rsk[cg][i] = r4[i];
+  }
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     float m = 0.f;
@@ -927,6 +939,16 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   float* Sk = (float*)(base + V_ * K_);
   float* Sv = Sk + K_;
   f16_t* UQ = (f16_t*)(Sv + V_);
+  // row scales once per row (threads 0-127), then read by every lane for its eight rows
+  if (tid < VD) {
+    float rm = sh.rowmax[0][tid];
+#pragma unroll
+    for (int w2 = 1; w2 < QW; ++w2) rm = fmaxf(rm, sh.rowmax[w2][tid]);
+    const float svv = fmaxf(rm, LQ_EPS);
+    sh.rsv[tid] = qmax / svv;
+    if (V_ == VD || tid < V_) Sv[tid] = svv;
+  }
+  __syncthreads();
   // codes: |x| <= qmax (1 + 2^-22) since svv is the row's largest |E rsk| (or above it), so the rounding to the nearest
   // integer is the add of 1.5 2^23 (round to nearest even, as rintf) and the clamp to [-qmax, qmax] never binds for
   // a finite x; the code is the low byte of the sum
@@ -934,11 +956,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) {
     const int v = 16 * nt + (l & 15);
-    float rm = sh.rowmax[0][v];
-#pragma unroll
-    for (int w2 = 1; w2 < QW; ++w2) rm = fmaxf(rm, sh.rowmax[w2][v]);
-    const float svv = fmaxf(rm, LQ_EPS);
-    const float rsv = qmax / svv;
+    const float rsv = sh.rsv[v];
 #pragma unroll
     for (int cg = 0; cg < 2; ++cg) {
       uint32_t b[4];
@@ -951,7 +969,6 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
       const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
       cw[cg][nt] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
     }
-    if ((V_ == VD || v < V_) && w == 0 && q == 0) Sv[v] = svv;
   }
   if constexpr (K_ == KD && V_ == VD) {
     // the same lane layout as the four-wave flush's tile: four 16-byte stores per lane after its transpose
@@ -1146,14 +1163,14 @@ void quantize64_kernel(lq_state st, const float* __restrict__ Q0, const int* __r
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 16 * w + 4 * q + i;
-      const f32x4 unc = sh.pp[h][c];
+      const f32x4 nunc = -sh.pp[h][c];                // -U, negated once (fma(q, -u, e) = fma(-q, u, e))
       float sa = 0.f;
 #pragma unroll
       for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) {
         const f32x4 qnv = sh.qv[16 * nt + l16];
         float e = t.a[nt][i];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) e = fmaf(-qnv[r], unc[r], e);
+        for (int r = 0; r < 4; ++r) e = fmaf(qnv[r], nunc[r], e);
         t.a[nt][i] = e;
         sa += fabsf(e);
       }
