@@ -754,9 +754,7 @@ __device__ __forceinline__ void rowred_q(const QTile& t, const f32x4* Y, f32x4 (
 #pragma unroll
         for (int r = 0; r < 4; ++r) s[r] = fmaf(m, yc[cg][i][r], s[r]);
       }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = xor32_sum(xor16_sum(s[r]));
-    if (q == 0) part[w][16 * nt + (l & 15)] = s;
+    ((float*)&part[w][16 * nt + (l & 15)])[q] = sum4_scatter(s);
   }
 }
 
@@ -902,18 +900,22 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
         s += fabsf(e);
       }
       s = sum16(s);
-      const float skc = fmaxf(sqrtf(s / (float)V_), LQ_EPS);      // kernels.py:2222
-      if ((l & 15) == 0) sh.sk[c] = skc;
+      if ((l & 15) == 0) sh.sk[c] = s;                // the column's sum of |E|; its scale below, once per column
       // one column at a time: without this the compiler requests the next columns' U rows early and the kernel
       // spills (118 -> 128 VGPRs and 28 bytes of scratch per lane; the quantize then ran 18% slower)
       __builtin_amdgcn_sched_barrier(0);
     }
   __syncthreads();
   // E / Sk and E / (Sk Sv) (kernels.py:2224-2229) as products with reciprocals taken once per column and once per row
-  // (within a few ulp of the quotients, below the codes' rounding step).  Each reciprocal is formed by one lane and
-  // shared through LDS: lane l < 32 of wave w takes column 32 w + l (one division per lane, where each lane formed the
-  // reciprocals of its own eight columns, the same eight in all 16 lanes of its row)
-  if (l < 32) sh.rsk[32 * w + l] = 1.0f / sh.sk[32 * w + l];
+  // (within a few ulp of the quotients, below the codes' rounding step).  Each column's scale and its reciprocal are
+  // formed by one lane and shared through LDS: lane l < 32 of wave w takes column 32 w + l (one square root and one
+  // division per lane, where each lane formed those of its own eight columns, the same eight in all 16 lanes of its
+  // row).  E rsk is kept in the tile: the row maxima and the codes take the same product.
+  if (l < 32) {
+    const float skc = fmaxf(sqrtf(sh.sk[32 * w + l] / (float)V_), LQ_EPS);   // kernels.py:2222
+    sh.sk[32 * w + l] = skc;
+    sh.rsk[32 * w + l] = 1.0f / skc;
+  }
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
   float rsk[2][4];
@@ -929,7 +931,10 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
     for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) m = fmaxf(m, fabsf(t.a[cg][nt][i] * rsk[cg][i]));   // kernels.py:2224-2227
+      for (int i = 0; i < 4; ++i) {
+        t.a[cg][nt][i] = t.a[cg][nt][i] * rsk[cg][i];                           // kernels.py:2224-2227
+        m = fmaxf(m, fabsf(t.a[cg][nt][i]));
+      }
     m = xor32_max(xor16_max(m));
     if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
   }
@@ -963,7 +968,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
 #pragma clang fp contract(off)
-        const float x = (t.a[cg][nt][i] * rsk[cg][i]) * rsv;     // kernels.py:2229 (rounded before the add)
+        const float x = t.a[cg][nt][i] * rsv;                    // kernels.py:2229 (rounded before the add)
         b[i] = __float_as_uint(x + 12582912.0f);
       }
       const uint32_t lo = __builtin_amdgcn_perm(b[1], b[0], 0x0c0c0400u), hi = __builtin_amdgcn_perm(b[3], b[2], 0x0c0c0400u);
@@ -1118,9 +1123,7 @@ void quantize64_kernel(lq_state st, const float* __restrict__ Q0, const int* __r
 #pragma unroll
       for (int r = 0; r < 4; ++r) s[r] = fmaf(t.a[nt][i], y[r], s[r]);
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) s[r] = xor32_sum(xor16_sum(s[r]));
-    if (q == 0) sh.qpart[w][16 * nt + l16] = s;
+    ((float*)&sh.qpart[w][16 * nt + l16])[q] = sum4_scatter(s);
   }
   __syncthreads();
   if (w == 0) {

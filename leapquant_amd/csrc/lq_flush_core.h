@@ -85,6 +85,18 @@ __device__ __forceinline__ void swap16(uint32_t& a, uint32_t& b) {
   a = r[0];
   b = r[1];
 }
+// s[r] summed over the four 16-lane groups as xor32_sum(xor16_sum(s[r])) sums it, ((group 0 + group 1) + (group 2 +
+// group 3)), as a reduce-scatter: lane group q returns the total of s[q] (three exchanges and three adds where the four
+// all-reductions take eight exchanges, eight copies and eight adds; the same sums, so the same bits)
+__device__ __forceinline__ float sum4_scatter(const f32x4& s) {
+  uint32_t a0 = __float_as_uint(s[0]), b0 = __float_as_uint(s[1]), a1 = __float_as_uint(s[2]), b1 = __float_as_uint(s[3]);
+  swap16(a0, b0);
+  swap16(a1, b1);
+  uint32_t x = __float_as_uint(__uint_as_float(a0) + __uint_as_float(b0));   // rows: s0, s1, s0, s1 over groups 0+1 / 2+3
+  uint32_t y = __float_as_uint(__uint_as_float(a1) + __uint_as_float(b1));   // rows: s2, s3, s2, s3
+  swap32(x, y);
+  return __uint_as_float(x) + __uint_as_float(y);     // rows: s0, s1, s2, s3 over all four groups
+}
 // The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
 // redo the conversion where the value is used (twice the registers).
 __device__ __forceinline__ f16x4 pinned(f16x4 x) {
@@ -182,11 +194,7 @@ __device__ __forceinline__ void rowred(const Tile& t, const f32x4* Y, f32x4 (*pa
       s[2] = fmaf(m, yc[i][2], s[2]);
       s[3] = fmaf(m, yc[i][3], s[3]);
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      s[r] = xor32_sum(xor16_sum(s[r]));
-    }
-    if (q == 0) part[w][16 * nt + (l & 15)] = s;
+    ((float*)&part[w][16 * nt + (l & 15)])[q] = sum4_scatter(s);
   }
 }
 
