@@ -1090,7 +1090,7 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
   float d = dcar, dn = dcar;                          // lane 0: dcar times lane 1's 16 decays, last first
 #pragma unroll
   for (int x = 7; x >= 0; --x) {
-    const uint32_t en = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)eu[x], 0xf5, 0xf, 0xf, false);  // quad_perm [1,1,3,3]
+    const uint32_t en = (uint32_t)__builtin_amdgcn_mov_dpp((int)eu[x], 0xf5, 0xf, 0xf, true);  // quad_perm [1,1,3,3]
     dn = dn * h2f((f16_t)(en >> 16));
     dn = dn * h2f((f16_t)(en & 0xffffu));
   }
