@@ -966,6 +966,7 @@ struct FlushShared4T {
       f16_t qoT[4][VD + FP];   // old Q^T, fp16
       f16x4 qo16[VD];          // old Q rows [v][a], fp16 (residual B operand)
       f16x4 qn16[VD];          // Q16 rows [v][r] (residual B operand)
+      f32x4 mb[NW4][4];        // per-wave broadcast of a 4 x 4 product (gram_qold_q)
     } r;
   };
   float skl[KD];               // column factor of the dequant (Sk)
@@ -1284,10 +1285,18 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4T<CF>& sh, float M
     const f16x8 bq = *(const f16x8*)&sh.qT[l16 & 3][32 * ks + 8 * q];
     macc = mma32(ao, bq, macc);
   }
+  // lanes 0-3 hold column r = l of the product; every lane reads the four columns back (same-address LDS reads are
+  // broadcasts): LDS instructions where sixteen readlanes were VALU ones
+  f32x4* mb = const_cast<f32x4*>(sh.r.mb[wave_id()]);
+  if (l < 4) mb[l] = macc;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+  for (int r = 0; r < 4; ++r) {
+    const f32x4 x = mb[r];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) M[a][r] = rl(macc[a], r);
+    for (int a = 0; a < 4; ++a) M[a][r] = x[a];
+  }
 }
 // P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lane
 // (q, l16) returns P[32 w + 16 g + l16][0..3] for g = q >> 1 (zero for r >= R).  The contraction runs over v, so each
