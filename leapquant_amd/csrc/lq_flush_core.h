@@ -1274,6 +1274,23 @@ __device__ __forceinline__ void tile_add_words4(Tile4& t, const uint32_t wds[2][
     }
   }
 }
+// M[a][r] = acc[a] of lane r (the 4 x 4 corner of a 16 x 16 MFMA result) in every lane: lanes 0-3 write their
+// columns to the wave's LDS words and every lane reads the four columns back (same-address reads are broadcasts), LDS
+// instructions where sixteen readlanes were VALU ones
+template <bool CF>
+__device__ __forceinline__ void bcast4x4(const FlushShared4T<CF>& sh, const f32x4& acc, float M[4][4]) {
+  const int l = lane_id();
+  f32x4* mb = const_cast<f32x4*>(sh.r.mb[wave_id()]);
+  if (l < 4) mb[l] = acc;
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const f32x4 x = mb[r];
+#pragma unroll
+    for (int a = 0; a < 4; ++a) M[a][r] = x[a];
+  }
+}
 // M[a][r] = sum_v Q_old[v][a] Q[v][r] (Q from sh.qT): every lane gets all 16 entries
 template <bool CF>
 __device__ __forceinline__ void gram_qold_q(const FlushShared4T<CF>& sh, float M[4][4]) {
@@ -1285,18 +1302,7 @@ __device__ __forceinline__ void gram_qold_q(const FlushShared4T<CF>& sh, float M
     const f16x8 bq = *(const f16x8*)&sh.qT[l16 & 3][32 * ks + 8 * q];
     macc = mma32(ao, bq, macc);
   }
-  // lanes 0-3 hold column r = l of the product; every lane reads the four columns back (same-address LDS reads are
-  // broadcasts): LDS instructions where sixteen readlanes were VALU ones
-  f32x4* mb = const_cast<f32x4*>(sh.r.mb[wave_id()]);
-  if (l < 4) mb[l] = macc;
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const f32x4 x = mb[r];
-#pragma unroll
-    for (int a = 0; a < 4; ++a) M[a][r] = x[a];
-  }
+  bcast4x4(sh, macc, M);
 }
 // P = B^T Q + pn U_old (Q_old^T Q) for the wave's two channel groups, fp16-rounded (kernels.py:1580-1700): lane
 // (q, l16) returns P[32 w + 16 g + l16][0..3] for g = q >> 1 (zero for r >= R).  The contraction runs over v, so each
@@ -1478,10 +1484,7 @@ __device__ void flush_head4(FlushShared4T<CF>& sh, const lq_state& st, const flo
       macc = mma32(ao, bp, macc);
     }
     float M2[4][4];
-#pragma unroll
-    for (int a = 0; a < 4; ++a)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) M2[a][r] = rl(macc[a], r);
+    bcast4x4(sh, macc, M2);
     const int v = tid;
     f32x4 s = sh.r.qpart[0][v];
 #pragma unroll
