@@ -942,10 +942,10 @@ constexpr int OPS4 = HALF + 8;       // operand row stride (bf16): 80 B rows, 16
 // CF (conflict-free layout): the factor tables [4][128] fp16 are read by the four lane rows of a 16-lane group at once
 // (row l & 3, same column), and rows of 128 halfs all start in the same bank, so each row is padded by 16 halfs (rows
 // then start 8 banks apart); the row-maximum table [16][128] fp32 is written by the four lane groups at once (row
-// 4 w + q, same column), padded by 16 floats (16 banks apart); store_half rotates the odd lane groups' columns.  The
-// standalone flush and the prefill dequant use it (the flush's LDS bank conflicts fall by three quarters, LDS-active
-// cycles by a third); the one-launch decode's flush does not: there the padded addressing costs the fused-conv kernel
-// registers (20 bytes per lane spilled), and the conflicts are not on its critical path.
+// 4 w + q, same column), padded by 16 floats (16 banks apart); store_half rotates the odd lane groups' columns (a
+// rotated group's words permuted once, no select per write).  The standalone flush, the prefill dequant and the
+// one-launch decode's flush use it (the flush's LDS bank conflicts fall by three quarters, LDS-active cycles by a
+// third).
 constexpr int FTP = 16, RMP = 16;
 
 struct Tile4 {

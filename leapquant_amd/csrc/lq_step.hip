@@ -98,7 +98,7 @@ template <int K_, int V_, int G, int RM>
 struct StepLds<K_, V_, G, true, RM> {
   union {
     StepShared<K_, V_, G, RM> st;
-    lqf::FlushShared4T<false> fl;
+    lqf::FlushShared4T<true> fl;
   };
 };
 
@@ -145,7 +145,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
         const float qm = code_range(st);
 #pragma unroll
         for (int g2 = 0; g2 < G; ++g2)
-          if ((pend >> g2) & 1u) lqf::flush_head4<128, 128, false>(lds.fl, st, Q0, slot0, hk * G + g2, qm);
+          if ((pend >> g2) & 1u) lqf::flush_head4<128, 128, true>(lds.fl, st, Q0, slot0, hk * G + g2, qm);
       }
     }
   }
@@ -535,7 +535,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 #pragma unroll
       for (int g2 = 0; g2 < G; ++g2)
         if (due[g2]) {
-          if (!DF || first) lqf::flush_head4<128, 128, false>(lds.fl, st, Q0, slot, hk * G + g2, qm);
+          if (!DF || first) lqf::flush_head4<128, 128, true>(lds.fl, st, Q0, slot, hk * G + g2, qm);
           else if (tid == 0) note_due(st.ctl, dlist, n * HV + hk * G + g2);   // a standalone flush finds it
           first = false;
         }
