@@ -707,11 +707,37 @@ struct QuantShared {
   float rsv[VD];                     // qmax / Sv per row
 };
 
-// column sums sum_v M[v][c] X[v][r] for this lane's channels: fn(cg, i, s) once per (group, channel) with the full sum
-// over the 128 rows (the rows of one lane first, in order, then across its 16 lanes)
+// 16 values, each summed over the 16 lanes of a DPP row exactly as sum16 sums one (xor 1, xor 2, half mirror, mirror:
+// the same two partial sums meet at every level, so the same bits), as a reduce-scatter: at each level a lane keeps
+// one of each pair of values and adds its partner's partial of it, so lane l ends with the total of value
+//   8 b3 + 4 (b2 ^ b3) + 2 (b1 ^ b2) + (b0 ^ b2)   (b = the bits of l mod 16),
+// an assignment under which both lanes of every pair, at every level, hold partials of the same value.  45 VALU
+// instructions where sixteen all-reductions take 64.
+__device__ __forceinline__ float sum16_scatter(const float (&v)[16], int l) {
+  const int b0 = l & 1, b1 = (l >> 1) & 1, b2 = (l >> 2) & 1, b3 = (l >> 3) & 1;
+  const bool s1 = b0 ^ b2, s2 = b1 ^ b2, s3 = b2 ^ b3, s4 = b3;
+  float r1[8], r2[4], r3[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r1[j] = (s1 ? v[2 * j + 1] : v[2 * j]) + dpp<DPP_XOR1>(s1 ? v[2 * j] : v[2 * j + 1]);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r2[j] = (s2 ? r1[2 * j + 1] : r1[2 * j]) + dpp<DPP_XOR2>(s2 ? r1[2 * j] : r1[2 * j + 1]);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+    r3[j] = (s3 ? r2[2 * j + 1] : r2[2 * j]) + dpp<DPP_HALF_MIRROR>(s3 ? r2[2 * j] : r2[2 * j + 1]);
+  return (s4 ? r3[1] : r3[0]) + dpp<DPP_MIRROR>(s4 ? r3[0] : r3[1]);
+}
+__device__ __forceinline__ int sum16_scatter_index(int l) {
+  const int b0 = l & 1, b1 = (l >> 1) & 1, b2 = (l >> 2) & 1, b3 = (l >> 3) & 1;
+  return 8 * b3 + 4 * (b2 ^ b3) + 2 * (b1 ^ b2) + (b0 ^ b2);
+}
+
+// column sums sum_v M[v][c] X[v][r] for this lane's channels (the rows of one lane first, in order, then across its 16
+// lanes): fn(cg, i, r, s) once per lane and group with the full sum of one (channel, column) pair, i = k >> 2 and
+// r = k & 3 for k = sum16_scatter_index(l)
 template <typename F>
 __device__ __forceinline__ void colred_q(const QTile& t, const f32x4* X, F fn) {
   const int l = lane_id();
+  const int k = sum16_scatter_index(l);
 #pragma unroll
   for (int cg = 0; cg < 2; ++cg) {
     f32x4 acc[4] = {};
@@ -725,13 +751,12 @@ __device__ __forceinline__ void colred_q(const QTile& t, const f32x4* X, F fn) {
         for (int r = 0; r < 4; ++r) acc[i][r] = fmaf(m, xv[r], acc[i][r]);
       }
     }
+    float v[16];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f32x4 s;
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) s[r] = sum16(acc[i][r]);
-      fn(cg, i, s);
-    }
+      for (int r = 0; r < 4; ++r) v[4 * i + r] = acc[i][r];
+    fn(cg, k >> 2, k & 3, sum16_scatter(v, l));
   }
 }
 
@@ -824,7 +849,7 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   for (int it = 0; it < iters; ++it) {
 #pragma unroll
     for (int b = 0; b < NB; ++b)
-      colred_q(t, sh.qv[b], [&](int cg, int i, f32x4 s) { if ((l & 15) == 0) sh.pp[b][32 * w + 16 * cg + 4 * q + i] = s; });
+      colred_q(t, sh.qv[b], [&](int cg, int i, int r, float s) { ((float*)&sh.pp[b][32 * w + 16 * cg + 4 * q + i])[r] = s; });
     __syncthreads();
     if (w == 0) {
       __builtin_amdgcn_s_setprio(3);
@@ -858,13 +883,8 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
   // U = fp16(S^T Q) straight to LDS (sh.pp is not read again before the next barrier), Q16 = fp16(Q)
 #pragma unroll
   for (int b = 0; b < NB; ++b)
-    colred_q(t, sh.qv[b], [&](int cg, int i, f32x4 s) {
-      if ((l & 15) == 0) {
-        f32x4 u;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) u[r] = 4 * b + r < R ? hround(s[r]) : 0.f;
-        sh.pp[b][32 * w + 16 * cg + 4 * q + i] = u;
-      }
+    colred_q(t, sh.qv[b], [&](int cg, int i, int r, float s) {
+      ((float*)&sh.pp[b][32 * w + 16 * cg + 4 * q + i])[r] = 4 * b + r < R ? hround(s) : 0.f;
     });
   __syncthreads();                                    // every wave has read Q (sh.qv)
   if (tid < VD) {
