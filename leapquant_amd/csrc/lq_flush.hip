@@ -945,18 +945,23 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
 #pragma unroll
     for (int i = 0; i < 4; ++i) rsk[cg][i] = r4[i];
   }
+  {
+    float mrow[8], mx[2];
 #pragma unroll
-  for (int nt = 0; nt < 8; ++nt) {
-    float m = 0.f;
+    for (int nt = 0; nt < 8; ++nt) {
+      float m = 0.f;
 #pragma unroll
-    for (int cg = 0; cg < 2; ++cg)
+      for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        t.a[cg][nt][i] = t.a[cg][nt][i] * rsk[cg][i];                           // kernels.py:2224-2227
-        m = fmaxf(m, fabsf(t.a[cg][nt][i]));
-      }
-    m = xor32_max(xor16_max(m));
-    if (q == 0) sh.rowmax[w][16 * nt + (l & 15)] = m;
+        for (int i = 0; i < 4; ++i) {
+          t.a[cg][nt][i] = t.a[cg][nt][i] * rsk[cg][i];                         // kernels.py:2224-2227
+          m = fmaxf(m, fabsf(t.a[cg][nt][i]));
+        }
+      mrow[nt] = m;
+    }
+    rowmax_scatter(mrow, mx);                         // lane group q: the wave's maxima of rows 16 (2 q + k) + l16
+#pragma unroll
+    for (int k = 0; k < 2; ++k) sh.rowmax[w][16 * (2 * q + k) + (l & 15)] = mx[k];
   }
   __syncthreads();
   // every read of the fp32 state is done: the checkpoint may now overwrite the block

@@ -97,6 +97,25 @@ __device__ __forceinline__ float sum4_scatter(const f32x4& s) {
   swap32(x, y);
   return __uint_as_float(x) + __uint_as_float(y);     // rows: s0, s1, s2, s3 over all four groups
 }
+// Row maxima over a wave's four lane groups (lane (q, l16) holds m[nt] for row 16 nt + l16 over its own channels): a
+// reduce-scatter, two swap32 rounds pairing groups q, q + 2, then a swap16 round pairing q, q + 1, after which group q
+// holds the wave's maxima of rows 16 (2 q) + l16 in x[0] and 16 (2 q + 1) + l16 in x[1] (12 instructions where eight
+// all-reductions take 48; maxima are exact, so the same values)
+__device__ __forceinline__ void rowmax_scatter(const float m[8], float x[2]) {
+  float n[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {                       // rows 0-1 of n[k]: row k; rows 2-3: row k + 4
+    uint32_t a = __float_as_uint(m[k]), b = __float_as_uint(m[k + 4]);
+    swap32(a, b);
+    n[k] = fmaxf(__uint_as_float(a), __uint_as_float(b));
+  }
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {                       // group q of x[k]: row 2 q + k
+    uint32_t a = __float_as_uint(n[k]), b = __float_as_uint(n[k + 2]);
+    swap16(a, b);
+    x[k] = fmaxf(__uint_as_float(a), __uint_as_float(b));
+  }
+}
 // The packed fp16 value as the compiler must keep it: without this it may keep the fp32 source alive instead and
 // redo the conversion where the value is used (twice the registers).
 __device__ __forceinline__ f16x4 pinned(f16x4 x) {
