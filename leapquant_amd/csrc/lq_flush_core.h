@@ -1115,41 +1115,29 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
     dn = dn * h2f((f16_t)(en & 0xffffu));
   }
   if (s == 0) d = dn;
-  float wj[16];                                       // the entries' weights, read before the walk
+  // no branch per entry: rows >= h hold decay 1 (d passes unchanged) and take zero operands.  A word (two entries) at
+  // a time, newest first: its weights read from LDS, its terms formed by one packed conversion each (each half read
+  // back with a shift or a mask: the same roundings as entry by entry) and written back over its raw key and decay
+  // words at once (both are in registers already)
 #pragma unroll
-  for (int x = 0; x < 4; ++x) {
-    const float4 w4 = *(const float4*)&sh.w[j0 + 4 * x];
-    wj[4 * x] = w4.x; wj[4 * x + 1] = w4.y; wj[4 * x + 2] = w4.z; wj[4 * x + 3] = w4.w;
-  }
-  uint32_t hw[8], lw[8], tw[8];                       // hi, second and (NT = 3) third terms
-  // no branch per entry: rows >= h hold decay 1 (d passes unchanged) and take zero operands
-#pragma unroll
-  for (int e = 15; e >= 0; --e) {
-    const float kd = bf2f((bf16_t)(ku[e >> 1] >> (16 * (e & 1)))) * (wj[e] * d);
-    const float r = j0 + e < h ? kd : 0.f;
-    const bf16_t bh_ = f2bf(r);
-    const float r1 = r - bf2f(bh_);
-    const bf16_t bl_ = f2bf(r1);
-    const bf16_t bt_ = NT == 3 ? f2bf(r1 - bf2f(bl_)) : (bf16_t)0;
-    if (e & 1) {
-      hw[e >> 1] = (uint32_t)bh_ << 16;
-      lw[e >> 1] = (uint32_t)bl_ << 16;
-      tw[e >> 1] = (uint32_t)bt_ << 16;
+  for (int x = 7; x >= 0; --x) {
+    const float2 w2 = *(const float2*)&sh.w[j0 + 2 * x];
+    const float kdo = bf_hi(ku[x]) * (w2.y * d);
+    const float ro = j0 + 2 * x + 1 < h ? kdo : 0.f;
+    d = d * h2f((f16_t)(eu[x] >> 16));
+    const float kde = bf_lo(ku[x]) * (w2.x * d);
+    const float re = j0 + 2 * x < h ? kde : 0.f;
+    d = d * h2f((f16_t)(eu[x] & 0xffffu));
+    const uint32_t hi = pk_bf16_kept(re, ro);
+    const float r1e = re - bf_lo(hi), r1o = ro - bf_hi(hi);
+    *(uint32_t*)&sh.op[0][c][jb + 2 * x] = hi;
+    if constexpr (NT == 3) {
+      const uint32_t mid = pk_bf16_kept(r1e, r1o);
+      *(uint32_t*)&sh.op[1][c][jb + 2 * x] = mid;
+      lo3[x] = pk_bf16(r1e - bf_lo(mid), r1o - bf_hi(mid));
     } else {
-      hw[e >> 1] |= (uint32_t)bh_;
-      lw[e >> 1] |= (uint32_t)bl_;
-      tw[e >> 1] |= (uint32_t)bt_;
+      *(uint32_t*)&sh.op[1][c][jb + 2 * x] = pk_bf16(r1e, r1o);
     }
-    d = d * h2f((f16_t)(eu[e >> 1] >> (16 * (e & 1))));
-  }
-  if constexpr (NT == 3) {
-#pragma unroll
-    for (int x = 0; x < 8; ++x) lo3[x] = tw[x];
-  }
-#pragma unroll
-  for (int x = 0; x < 2; ++x) {
-    *(uint4*)&sh.op[0][c][jb + 8 * x] = make_uint4(hw[4 * x], hw[4 * x + 1], hw[4 * x + 2], hw[4 * x + 3]);
-    *(uint4*)&sh.op[1][c][jb + 8 * x] = make_uint4(lw[4 * x], lw[4 * x + 1], lw[4 * x + 2], lw[4 * x + 3]);
   }
   return dpp<0xa0>(d);                                // quad_perm [0,0,2,2]: lane 0's D below its entries, to both
 }
