@@ -18,6 +18,10 @@ DEV = "cuda:0"
 
 CASES = [  # (kda, K, V, R, HV, H, NS): the four-wave flush, R = 8, KDA, the 64-dim layouts (pairs at even GQA)
     (False, 128, 128, 4, 32, 16, 65),
+    # GQA 2 and 4 with a candidate count that is not a multiple of 8 G (1218 = 76 x 16 + 2, 1572 = 49 x 32 + 4): the
+    # schedule's key-head grouping of candidates and its partial last block
+    (False, 128, 128, 4, 6, 3, 201),
+    (False, 128, 128, 4, 12, 3, 129),
     (False, 128, 128, 8, 16, 8, 65),
     (True, 128, 128, 4, 16, 16, 65),
     (False, 64, 128, 4, 32, 16, 65),
