@@ -73,9 +73,9 @@ struct StepShared {
 // ------------------------------------------------------------------------------------------------------------------
 // GDN step  (kernels.py:129-144 gate / beta, 236-279 norms and weights, 380-585 stream, dots and appends)
 //
-// One workgroup per (row n, key head hk) with V / 64 waves per value head g; wave (g, wi) owns tile rows 64 wi ..
-// 64 wi + 63.  Head dims (K, V) = (128, 128), (64, 128), (64, 64) (kernels.py:62): K sets the lanes' channel count in
-// the scalar work and the k-steps of every MFMA, V the waves per value head.
+// One workgroup per (row n, key head hk) with two waves per value head g (step_wph); wave (g, wi) owns tile rows
+// RW wi .. RW wi + RW - 1, RW = V / 2.  Head dims (K, V) = (128, 128), (64, 128), (64, 64) (kernels.py:62): K sets the
+// lanes' channel count in the scalar work and the k-steps of every MFMA, V the rows per wave.
 // Every dot product runs on the matrix cores:
 //   * m = deq(Sq) kn, y = deq(Sq) qn: the int8 tile goes from HBM straight into the A operand of
 //     v_mfma_i32_16x16x64_i8; B holds kf = kn Sk / 127 and qf = qn Sk / 127 as three int8 digits each (24-bit fixed
@@ -90,6 +90,11 @@ struct StepShared {
 // call instead of two.  The step's LDS and the flush's share the same bytes (both fit the 40 KiB that four workgroups
 // per CU allow).
 // ------------------------------------------------------------------------------------------------------------------
+// waves per value head of the step: V / 64, and two at V = 64 (each wave then owns 32 rows of the tile), so that a
+// 64-row head's bytes are requested by as many waves as a 128-row head's
+template <int V_>
+constexpr int step_wph() { return V_ == 64 ? 2 : V_ / 64; }
+
 template <int K_, int V_, int G, bool FL, int RM>
 struct StepLds {
   StepShared<K_, V_, G, RM> st;
@@ -106,13 +111,14 @@ struct StepLds<K_, V_, G, true, RM> {
 // by the last wave.  16 (the rank ablation R <= 16, K = V = 128; kernels.py:63, 457-469): up to G tiles, tile g taken
 // by the second wave of head g.
 template <int K_, int V_, int G, bool CONV, bool FL, int RM = 4, bool DF = false>
-__global__ __launch_bounds__(V_ * G) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(64 * step_wph<V_>() * G) __attribute__((amdgpu_waves_per_eu(4)))
 void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const float* Q0) {
   static_assert(!DF || FL, "deferred flush (lq_gdn_decode_deferred): the fused decode kernel");
   static_assert(!FL || (K_ == 128 && V_ == 128 && G == 2), "fused flush: the four-wave layout, 128 x 128 heads");
   static_assert(RM == 4 || (RM == 16 && K_ == 128 && V_ == 128 && !FL), "ranks above 4: 128 x 128 heads, no fused flush");
   constexpr int KD = K_, VD = V_;
-  constexpr int WPH = VD / 64;  // waves per value head
+  constexpr int WPH = step_wph<V_>();   // waves per value head
+  constexpr int RW = VD / WPH;          // tile rows per wave
   constexpr int NE = KD / 64;   // channels per lane in the scalar work
   constexpr int KS32 = KD / 32, KS64 = KD / 64;   // k-steps of the 16x16x32 (bf16 / fp16) and 16x16x64 (int8) MFMAs
   constexpr bool NT = KD == 128;                  // non-temporal bulk loads (see ld_once)
@@ -124,9 +130,11 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const int tid = threadIdx.x;
   const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave in the workgroup
   const int g = wv / WPH;       // value head of this wave within the key head
-  const int wi = wv % WPH;      // its tile part: rows 64 wi ..
-  const int lt = tid & (VD - 1);   // thread within the value head (the row it owns in the output phase)
+  const int wi = wv % WPH;      // its tile part: rows RW wi ..
   const int lane = tid & 63;
+  // the row this thread owns in the output phase; at V = 64 lanes RW .. 63 repeat the wave's rows and store nothing
+  const int lt = RW == 64 ? tid & (VD - 1) : RW * wi + (lane & (RW - 1));
+  const bool rowl = RW == 64 || lane < RW;
   const int n16 = lane & 15, q4 = lane >> 4;                 // MFMA lane coordinates
   const int hv = hk * G + g;
   const long long MIX = 2ll * H * KD + (long long)HV * VD;
@@ -170,7 +178,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   const int slot = io.idx[n];
   // padding row (kernels.py:374-378); a slot outside the cache (or, fused conv, outside the conv state) counts as one
   if (slot <= 0 || slot >= st.NS || (CONV && slot >= cv.NS)) {
-    out[lt] = 0;
+    if (rowl) out[lt] = 0;
     return;
   }
   // Every load below is unconditional (clamped addresses) and none sits in a divergent block: a load whose result is
@@ -301,7 +309,7 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
 
   if (CONV) {                   // the value channel lt of this head: conv output and state shift
     vin = conv_out(vtap, cv.silu);
-    conv_shift(cv, cvb, 2 * H * KD + hv * VD + lt, vtap);
+    if (rowl) conv_shift(cv, cvb, 2 * H * KD + hv * VD + lt, vtap);
   }
   // Every wave holds its bulk loads until its own small loads are back.  Under load the memory system serves requests
   // roughly in arrival order, chip-wide: a small load issued after the first bulk loads waits behind them (several
@@ -355,17 +363,17 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
       for (int ks = 0; ks < KS32; ++ks) kfr[t][ks] = ld_nt<NT>((const bf16x8*)(Kb + (long long)jr * KD + 32 * ks + 8 * q4));
     }
   }
-  i32x4 afr[4][KS64];           // the int8 tile: A fragments, row 64 wi + 16 rt + n16
+  i32x4 afr[RW / 16][KS64];     // the int8 tile: A fragments, row RW wi + 16 rt + n16
   {
-    const char* rp = base + (64 * wi + n16) * KD + 16 * q4;
+    const char* rp = base + (RW * wi + n16) * KD + 16 * q4;
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt)
+    for (int rt = 0; rt < RW / 16; ++rt)
 #pragma unroll
       for (int ks = 0; ks < KS64; ++ks) afr[rt][ks] = ld_nt<NT>((const i32x4*)(rp + 16 * rt * KD + 64 * ks));
   }
   // vector memory operations issued after the window's LDS loads: the keys and the tile (nothing else until the
   // stores at the end, so this count is exact)
-  constexpr int AFTER_WINDOW = KS32 * KT + 4 * KS64;
+  constexpr int AFTER_WINDOW = KS32 * KT + (RW / 16) * KS64;
   __builtin_amdgcn_sched_barrier(0);
 
   __syncthreads();              // digits, dot operands, scalars and w_j are in LDS (the barrier waits for no global load)
@@ -435,8 +443,8 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
   asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");
   __syncthreads();              // ... and the other wave's, with the key and factor dots of every wave
   if (!live) {                  // a full window (a flush that did not cover this row): zero output, nothing written;
-    if (!FL && lt == 0) note_due(st.ctl, dlist, n * HV + hv);   // flag it again so that the flush takes it
-    out[lt] = 0;
+    if (!FL && lt == 0 && rowl) note_due(st.ctl, dlist, n * HV + hv);   // flag it again so that the flush takes it
+    if (rowl) out[lt] = 0;
   } else {
   // ---- row v = lt: buffered entries, rank-R part, delta rule, output and appends (kernels.py:536-585) ----
   const float alpha = sh.sc[g][0], beta = sh.sc[g][1], kappa = sh.sc[g][2];
@@ -482,29 +490,31 @@ void gdn_step_kernel(lq_state st, lq_step_io io, lq_conv cv, int* dlist, const f
       bfr[ks] = bcol ? b : i32x4{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int rt = 0; rt < 4; ++rt) {
+    for (int rt = 0; rt < RW / 16; ++rt) {
       i32x4 acc = {0, 0, 0, 0};
 #pragma unroll
       for (int ks = 0; ks < KS64; ++ks) acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(afr[rt][ks], bfr[ks], acc, 0, 0, 0);
-      // lane (n16, q4) holds rows 64 wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
+      // lane (n16, q4) holds rows RW wi + 16 rt + 4 q4 + i of column n16; lanes 8 / 9 gather digits 0, 1 from 4, 8 lanes back
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float c0 = (float)acc[i];
         const float tot = fmaf(row_shr<8>(c0), 65536.0f, fmaf(row_shr<4>(c0), 256.0f, c0));
-        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[g][64 * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
+        if (n16 == 8 || n16 == 9) ((float*)&sh.mq[g][RW * wi + 16 * rt + 4 * q4 + i])[n16 - 8] = tot;
       }
     }
   }
-  // rows 64 wi .. 64 wi + 63 of the GEMV are this wave's own rows: LDS round trip within the wave, no barrier
+  // rows RW wi .. RW wi + RW - 1 of the GEMV are this wave's own rows: LDS round trip within the wave, no barrier
   const float2 mqr = sh.mq[g][lt];
   const float mq = (mqr.x * (sh.sc[g][3] * (1.0f / DIGIT_SCALE))) * sv;
   const float yq = (mqr.y * (sh.sc[g][4] * (1.0f / DIGIT_SCALE))) * sv;
   const float pn = P * alpha;
   const float u = beta * (vin - (pn * (mq + a6) + a4));
   const float y = pn * (yq + a7) + a5 + kappa * u;
-  out[lt] = f2bf(y);
-  ((bf16_t*)st.Ubuf)[(sh_ * L + h) * VD + lt] = f2bf(u);
-  if (lt == 0) {
+  if (rowl) {
+    out[lt] = f2bf(y);
+    ((bf16_t*)st.Ubuf)[(sh_ * L + h) * VD + lt] = f2bf(u);
+  }
+  if (lt == 0 && rowl) {
     Wp[h] = 1.0f;
     st.Pbuf[sh_] = pn;
     st.hcnt[sh_] = h + 1;
@@ -966,9 +976,9 @@ template <int K_, int V_, bool CONV, int RM = 4>
 static int launch_gdn(const lq_state* st, const lq_step_io* io, const lq_conv& cv, int* dlist, hipStream_t s) {
   dim3 grid((unsigned)(io->N * st->H));
   switch (st->HV / st->H) {
-    case 1: gdn_step_kernel<K_, V_, 1, CONV, false, RM><<<grid, V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
-    case 2: gdn_step_kernel<K_, V_, 2, CONV, false, RM><<<grid, 2 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
-    case 4: gdn_step_kernel<K_, V_, 4, CONV, false, RM><<<grid, 4 * V_, 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 1: gdn_step_kernel<K_, V_, 1, CONV, false, RM><<<grid, 64 * step_wph<V_>(), 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 2: gdn_step_kernel<K_, V_, 2, CONV, false, RM><<<grid, 128 * step_wph<V_>(), 0, s>>>(*st, *io, cv, dlist, nullptr); break;
+    case 4: gdn_step_kernel<K_, V_, 4, CONV, false, RM><<<grid, 256 * step_wph<V_>(), 0, s>>>(*st, *io, cv, dlist, nullptr); break;
     default: return LQ_ERR_ARG;
   }
   return hipGetLastError() == hipSuccess ? LQ_OK : LQ_ERR_HIP;

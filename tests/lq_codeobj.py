@@ -78,7 +78,7 @@ def _targs(name):
 
 # kernel family -> workgroup size of its launch sites, from the template arguments
 LAUNCH_BLOCK = {
-    "gdn_step_kernel": lambda t: int(t[1]) * int(t[2]),          # <K, V, G, ...>: V * G threads
+    "gdn_step_kernel": lambda t: 128 * int(t[2]),                # <K, V, G, ...>: two waves per value head
     "kda_step_kernel": lambda t: 128,
     "dense_step_kernel": lambda t: 128 * int(t[0]),              # <G, F>
     "conv_update_kernel": lambda t: 256,
