@@ -913,33 +913,39 @@ void quantize_kernel(lq_state st, const float* __restrict__ Q0, const int* __res
     }
   }
   __syncthreads();
-  // E = S - Q U^T (fp32), column scales
+  // E = S - Q16 U16^T on the matrix cores (kernels.py:2212-2217): the tile's lane layout is the D layout of
+  // v_mfma_f32_16x16x4_f32 (register i of lane l: channel 32 w + 16 cg + 4 (l >> 4) + i, row 16 nt + (l & 15)), so the
+  // tile is the accumulator, A = -U16 (lane l: channel 32 w + 16 cg + (l & 15), factor 4 b + (l >> 4)) and B = Q16
+  // (lane l: row 16 nt + (l & 15), factor 4 b + (l >> 4)): one MFMA per (group, row tile) and block of four factors.
+  // The fp16 factors' products are exact; only the sums round.
+  {
+    float nu[2][NB];
+#pragma unroll
+    for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+      for (int b = 0; b < NB; ++b) nu[cg][b] = -((const float*)&sh.pp[b][32 * w + 16 * cg + (l & 15)])[q];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      float qb[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) qb[b] = ((const float*)&sh.qv[b][16 * nt + (l & 15)])[q];
+#pragma unroll
+      for (int cg = 0; cg < 2; ++cg)
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          t.a[cg][nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(nu[cg][b], qb[b], t.a[cg][nt], 0, 0, 0);
+    }
+  }
+  // column sums of |E|; the scales below, once per column
 #pragma unroll
   for (int cg = 0; cg < 2; ++cg)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int c = 32 * w + 16 * cg + 4 * q + i;
-      f32x4 nunc[NB];                                 // -U of the column, negated once (fma(q, -u, e) = fma(-q, u, e))
-#pragma unroll
-      for (int b = 0; b < NB; ++b) nunc[b] = -sh.pp[b][c];
       float s = 0.f;
 #pragma unroll
-      for (int nt = 0; nt < 8; ++nt) {
-        float e = t.a[cg][nt][i];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          const f32x4 qnv = sh.qv[b][16 * nt + (l & 15)];
-#pragma unroll
-          for (int r = 0; r < 4; ++r) e = fmaf(qnv[r], nunc[b][r], e);
-        }
-        t.a[cg][nt][i] = e;
-        s += fabsf(e);
-      }
+      for (int nt = 0; nt < 8; ++nt) s += fabsf(t.a[cg][nt][i]);
       s = sum16(s);
-      if ((l & 15) == 0) sh.sk[c] = s;                // the column's sum of |E|; its scale below, once per column
-      // one column at a time: without this the compiler requests the next columns' U rows early and the kernel
-      // spills (118 -> 128 VGPRs and 28 bytes of scratch per lane; the quantize then ran 18% slower)
-      __builtin_amdgcn_sched_barrier(0);
+      if ((l & 15) == 0) sh.sk[32 * w + 16 * cg + 4 * q + i] = s;
     }
   __syncthreads();
   // E / Sk and E / (Sk Sv) (kernels.py:2224-2229) as products with reciprocals taken once per column and once per row
