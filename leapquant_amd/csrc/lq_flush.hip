@@ -1207,23 +1207,25 @@ void quantize64_kernel(lq_state st, const float* __restrict__ Q0, const int* __r
     sh.qv[tid] = x;
   }
   __syncthreads();
-  // E = S - Q U^T (fp32), column scales per head (kernels.py:2212-2222)
+  // E = S - Q16 U16^T on the matrix cores (kernels.py:2212-2217), as in quantize_kernel: the tile is the accumulator
+  // of v_mfma_f32_16x16x4_f32 (register i of lane l: channel 16 w + 4 q + i, row 16 nt + l16), A = -U16 of the row
+  // tile's head (lane l: channel 16 w + l16, factor q), B = Q16 (lane l: row 16 nt + l16, factor q)
+#pragma unroll
+  for (int nt = 0; nt < NTV; ++nt) {
+    const int h = (16 * nt) / V_;
+    const float nu = -((const float*)&sh.pp[h][16 * w + l16])[q];
+    const float qb = ((const float*)&sh.qv[16 * nt + l16])[q];
+    t.a[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(nu, qb, t.a[nt], 0, 0, 0);
+  }
+  // column scales per head (kernels.py:2222)
 #pragma unroll
   for (int h = 0; h < HP; ++h)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = 16 * w + 4 * q + i;
-      const f32x4 nunc = -sh.pp[h][c];                // -U, negated once (fma(q, -u, e) = fma(-q, u, e))
       float sa = 0.f;
 #pragma unroll
-      for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) {
-        const f32x4 qnv = sh.qv[16 * nt + l16];
-        float e = t.a[nt][i];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) e = fmaf(qnv[r], nunc[r], e);
-        t.a[nt][i] = e;
-        sa += fabsf(e);
-      }
+      for (int nt = h * V_ / 16; nt < (h + 1) * V_ / 16; ++nt) sa += fabsf(t.a[nt][i]);
       sa = sum16(sa);
       const float skc = fmaxf(sqrtf(sa / (float)V_), LQ_EPS);                     // kernels.py:2222
       if (l16 == 0) sh.sk[h][c] = skc;
