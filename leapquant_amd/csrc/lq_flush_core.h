@@ -1111,8 +1111,8 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
 #pragma unroll
   for (int x = 7; x >= 0; --x) {
     const uint32_t en = (uint32_t)__builtin_amdgcn_mov_dpp((int)eu[x], 0xf5, 0xf, 0xf, true);  // quad_perm [1,1,3,3]
-    dn = dn * h2f((f16_t)(en >> 16));
-    dn = dn * h2f((f16_t)(en & 0xffffu));
+    dn = hmul<1>(en, dn);
+    dn = hmul<0>(en, dn);
   }
   if (s == 0) d = dn;
   // no branch per entry: rows >= h hold decay 1 (d passes unchanged) and take zero operands.  A word (two entries) at
@@ -1124,10 +1124,10 @@ __device__ __forceinline__ float kda_key_scan4(FlushShared4T<CF>& sh, float dcar
     const float2 w2 = *(const float2*)&sh.w[j0 + 2 * x];
     const float kdo = bf_hi(ku[x]) * (w2.y * d);
     const float ro = j0 + 2 * x + 1 < h ? kdo : 0.f;
-    d = d * h2f((f16_t)(eu[x] >> 16));
+    d = hmul<1>(eu[x], d);
     const float kde = bf_lo(ku[x]) * (w2.x * d);
     const float re = j0 + 2 * x < h ? kde : 0.f;
-    d = d * h2f((f16_t)(eu[x] & 0xffffu));
+    d = hmul<0>(eu[x], d);
     const uint32_t hi = pk_bf16_kept(re, ro);
     const float r1e = re - bf_lo(hi), r1o = ro - bf_hi(hi);
     *(uint32_t*)&sh.op[0][c][jb + 2 * x] = hi;

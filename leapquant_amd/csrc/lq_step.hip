@@ -618,8 +618,8 @@ __device__ __forceinline__ void kda_scan_rows(KdaShared& sh, const uint32_t (&kr
         const int r = 8 * g8 + i;
         if (r < cnt) {
           *(uint32_t*)&sh.gk[gb + r][2 * lane] = pk_bf16(bf_lo(kr[r]) * d0, bf_hi(kr[r]) * d1);
-          d0 = d0 * h2f((f16_t)(ev[i] & 0xffffu));
-          d1 = d1 * h2f((f16_t)(ev[i] >> 16));
+          d0 = lqf::hmul<0>(ev[i], d0);             // the decays and products are positive: the same bits as cvt + mul
+          d1 = lqf::hmul<1>(ev[i], d1);
         }
       }
     }
