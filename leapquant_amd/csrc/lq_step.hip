@@ -596,10 +596,17 @@ struct KdaShared {
   f16_t uq[4][KD + VD];     // the checkpoint's factor rows (U_r | Q_r), fp16
 };
 
-// per-channel gate g (kernels.py:704-712, 802): glb sigmoid(e^A_log (a + dt_bias)) (glb != 0), else -e^A_log softplus
+// per-channel gate g (kernels.py:704-712, 802): glb sigmoid(e^A_log (a + dt_bias)) (glb != 0), else -e^A_log softplus.
+// The gate's exponentials (here, and the decays e^g and e^gn below) are the hardware's: v_exp_f32 of x log2(e) (HIP's
+// __expf), as the reference's __expf (kernels.py:704-707); the softplus keeps log1p, where the reference's
+// __logf(1 + e^x) cancels: for gates of 1e-4, e^x ~ 1e-4 and 1 + e^x keeps ~3 of its digits.
+__device__ __forceinline__ float softplus20_hx(float x) {
+  const float t = log1pf(__expf(fminf(x, (float)LQ_SOFTPLUS_THRESHOLD)));
+  return x <= (float)LQ_SOFTPLUS_THRESHOLD ? t : x;
+}
 __device__ __forceinline__ float kda_gate(float a, float dt, float ea, float glb) {
   const float xg = a + dt;
-  return glb != 0.f ? glb / (1.0f + expf(-ea * xg)) : -ea * softplus20f(xg);
+  return glb != 0.f ? glb / (1.0f + __expf(-ea * xg)) : -ea * softplus20_hx(xg);
 }
 
 // Decayed keys K~_j = bf16(K_j dcur), dcur *= e_j, backwards over a wave's cnt <= 16 entries of a chunk, LDS rows
@@ -741,8 +748,8 @@ void kda_step_kernel(lq_state st, lq_step_io io, float glb, int* dlist) {
     for (int e = 0; e < 2; ++e) {
       const float g = kda_gate(bf2f(axr[e]), dtx[e], ea, glb);
       gnv[e] = pbx[e] + g;
-      pcv[e] = expf(gnv[e]);
-      env[e] = expf(g);
+      pcv[e] = __expf(gnv[e]);
+      env[e] = __expf(g);
     }
     const float kx[2] = {bf2f(kxr[0]), bf2f(kxr[1])}, qx[2] = {bf2f(qxr[0]), bf2f(qxr[1])};
     float nq = qx[0] * qx[0], nk = kx[0] * kx[0], nkq = kx[0] * qx[0];
@@ -796,8 +803,8 @@ void kda_step_kernel(lq_state st, lq_step_io io, float glb, int* dlist) {
   } else {
     // the scan starts at exp(g) of the channel (the same gate as wave 0's, so the same bits) and runs over wave 1's
     // entries first; the product it reaches is where wave 0's entries continue
-    float d0 = expf(kda_gate(bf2f(axr[0]), dtx[0], ea, glb));
-    float d1 = expf(kda_gate(bf2f(axr[1]), dtx[1], ea, glb));
+    float d0 = __expf(kda_gate(bf2f(axr[0]), dtx[0], ea, glb));
+    float d1 = __expf(kda_gate(bf2f(axr[1]), dtx[1], ea, glb));
     asm volatile("s_waitcnt vmcnt(%0)" :: "n"(AFTER_WINDOW) : "memory");   // own decay rows in LDS, keys in registers
     kda_scan_rows(sh, kr, ck.jb - ck.cb, ck.cnt, lane, d0, d1);
     sh.dhand[lane] = make_float2(d0, d1);
