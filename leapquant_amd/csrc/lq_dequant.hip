@@ -19,7 +19,9 @@ __global__ __launch_bounds__(FT4) __attribute__((amdgpu_waves_per_eu(4)))
 void dequant4_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   __shared__ FlushShared4 sh;
   const int HV = st.HV, L = st.L, R = st.R;
-  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  // the value heads of a key head on one XCD at about the same time: their shared window keys are read into its L2 once
+  const int p = sched_unit((int)blockIdx.x, HV / st.H, (int)gridDim.x);
+  const int n = p / HV, hv = p - n * HV;
   const int slot = idx[n];
   if (slot <= 0 || slot >= st.NS) return;
   const long long sh_ = (long long)slot * HV + hv;
@@ -118,7 +120,9 @@ void kda_dequant4_kernel(lq_state st, const int* __restrict__ idx, float qmax) {
   __shared__ FlushShared4 sh;
   __shared__ float pcs[KD];                           // exp(P[c])
   const int HV = st.HV, L = st.L, R = st.R;
-  const int n = blockIdx.x / HV, hv = blockIdx.x - n * HV;
+  // the value heads of a key head on one XCD at about the same time: their shared window keys are read into its L2 once
+  const int p = sched_unit((int)blockIdx.x, HV / st.H, (int)gridDim.x);
+  const int n = p / HV, hv = p - n * HV;
   const int slot = idx[n];
   if (slot <= 0 || slot >= st.NS) return;
   const long long sh_ = (long long)slot * HV + hv;

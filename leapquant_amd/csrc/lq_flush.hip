@@ -32,20 +32,6 @@ using namespace lqf;
 // is skipped or, if it names a head due again, flushed once; the last workgroup to finish empties the list.
 // `head(slot, hv0, mask, sched)` flushes the due heads hv0 + h (bit h of mask) of one unit with the whole workgroup
 // and, with sched set, leaves the workgroup's next candidate in `due`, a word of the workgroup's shared memory.
-// The unit a dynamic-schedule candidate names.  Candidate c = 8 j + x is taken in schedule group x (x = blockIdx.x mod
-// 8 for the first round, which is the XCD the dispatcher places the workgroup on, and the group's counter after it),
-// as the group's j-th.  With G value heads per key head, the G candidates j = G m .. G m + G - 1 of group x name the G
-// value heads of one key head (unit G (8 m + x) + j mod G), so they are flushed on one XCD at about the same time and
-// the key window they share is read into that XCD's L2 once.  A bijection on each block of 8 G candidates; the last,
-// partial block keeps its order.
-__device__ __forceinline__ int sched_unit(int c, int G, int total) {
-  const int blk = SCHED_GROUPS * G;
-  if (G == 1 || c >= total - total % blk) return c;
-  const int j = c / SCHED_GROUPS, x = c - SCHED_GROUPS * j;
-  const int m = j / G;
-  return blk * m + G * x + (j - G * m);
-}
-
 template <int U>
 __device__ __forceinline__ unsigned unit_mask(const lq_state& st, int slot, int hv0) {
   unsigned m = 0;

@@ -615,6 +615,20 @@ __device__ __forceinline__ int sched_candidate(int take) {
   return (int)gridDim.x + SCHED_GROUPS * (take & ((1 << SCHED_BITS) - 1)) + (int)(blockIdx.x % SCHED_GROUPS);
 }
 __device__ __forceinline__ int sched_next(int* sched) { return sched_candidate(sched_take(sched)); }
+// The unit a dynamic-schedule candidate names.  Candidate c = 8 j + x is taken in schedule group x (x = blockIdx.x mod
+// 8 for the first round, which is the XCD the dispatcher places the workgroup on, and the group's counter after it),
+// as the group's j-th.  With G value heads per key head, the G candidates j = G m .. G m + G - 1 of group x name the G
+// value heads of one key head (unit G (8 m + x) + j mod G), so they are flushed on one XCD at about the same time and
+// the key window they share is read into that XCD's L2 once.  A bijection on each block of 8 G candidates; the last,
+// partial block keeps its order.  A launch of one workgroup per unit maps its workgroups the same way (workgroup
+// b = 8 j + x runs on XCD x, and b, b + 8, ... are dispatched one after the other).
+__device__ __forceinline__ int sched_unit(int c, int G, int total) {
+  const int blk = SCHED_GROUPS * G;
+  if (G == 1 || c >= total - total % blk) return c;
+  const int j = c / SCHED_GROUPS, x = c - SCHED_GROUPS * j;
+  const int m = j / G;
+  return blk * m + G * x + (j - G * m);
+}
 // the take's value where it is used: an opaque copy, so that nothing computed from it moves up to the take (and with it
 // the wait for the atomic's return)
 __device__ __forceinline__ int take_result(int take) {
